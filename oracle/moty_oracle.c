@@ -1,0 +1,465 @@
+/* moty_oracle.c -- CPU restatement of moty's quantized-matmul + MoE path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker for the HIP library in
+ * moty_amd/: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg may load it.  The product path never calls into it.
+ *
+ * Every function restates one reference function (cited as file:line relative
+ * to the reference's c/ directory).  Floating-point steps are written out in
+ * the exact order the reference's x86-64 AVX512-VNNI build evaluates them
+ * (gcc -O2, whose default -ffp-contract=fast turns `a += b*c` into an FMA);
+ * this file is compiled with -ffp-contract=off, so every FMA below is explicit.
+ *
+ * Pinning (what checks each function beyond retyping it):
+ *   o_qrow_i8, o_quantize_rows, o_pack_int4_grouped  -> compiled reference
+ *       (oracle/_ref), reconstruction bound |x - s*q| <= s/2, golden fixtures
+ *   o_dot_i8i8, o_matmul_q_s   -> brute-force int64 sums, _ref, fixtures,
+ *       batch invariance (S rows == S single calls)
+ *   o_dot_i4g8p, o_matmul_i4g_idot4, o_matmul_i4g_f32 -> _ref, and a double
+ *       dequant reference within the reference's own tolerance
+ *   o_dot_f32 (AVX512 lane order), o_matmul_f32  -> _ref bit-exact, double sum
+ *   o_expf     -> exhaustive over all 2^32 inputs against libm expf
+ *   o_softmax, o_silu_mul, o_topk -> _ref, naive greedy top-k
+ *   o_moe_batch / o_moe_olmoe -> _ref (moty_nn_moe_topk_batch and the
+ *       olmoe call sequence), plus the permutation property of the grouping
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define O_EXPORT __attribute__((visibility("default")))
+
+/* ------------------------------------------------------------------ */
+/* a1: per-row symmetric int8 activation quantization.                  */
+/* hw/hw_quant.h:9-16                                                   */
+O_EXPORT float o_qrow_i8(const float *x, int8_t *q, int n) {
+    float amax = 0.f;
+    for (int i = 0; i < n; i++) { float a = fabsf(x[i]); if (a > amax) amax = a; }
+    float s = amax / 127.f;
+    if (s < 1e-12f) s = 1e-12f;
+    float inv = 1.f / s;
+    for (int i = 0; i < n; i++) q[i] = (int8_t)lrintf(x[i] * inv);
+    return s;
+}
+
+/* a2: int8 x int8 -> int32 (hw/hw_scalar.h:8-12; the VNNI kernel of
+ * hw/hw_avx512.h:24-54 is exact integer arithmetic, so any order agrees). */
+O_EXPORT int32_t o_dot_i8i8(const int8_t *w, const int8_t *x, int n) {
+    int64_t s = 0;
+    for (int i = 0; i < n; i++) s += (int64_t)w[i] * x[i];
+    return (int32_t)s;
+}
+
+/* a4: weight quantization, per row, division by s (not *inv).
+ * nn/quant.c:12-33 */
+O_EXPORT void o_quantize_rows(const float *w, int8_t *q, float *scale, int O, int I, int bits) {
+    int qmax = (1 << (bits - 1)) - 1;
+    for (int o = 0; o < O; o++) {
+        const float *wr = w + (int64_t)o * I;
+        float amax = 0.f;
+        for (int i = 0; i < I; i++) { float a = fabsf(wr[i]); if (a > amax) amax = a; }
+        float s = amax / (float)qmax;
+        if (s < 1e-8f) s = 1e-8f;
+        scale[o] = s;
+        for (int i = 0; i < I; i++) {
+            int v = (int)lrintf(wr[i] / s);
+            if (v > qmax) v = qmax;
+            if (v < -qmax - 1) v = -qmax - 1;
+            q[(int64_t)o * I + i] = (int8_t)v;
+        }
+    }
+}
+
+/* a6: grouped int4 packing, f32 scale amax/7 per group, nibble = v+8,
+ * even element in the low nibble.  nn/quant.c:57-83 (gs % 16 == 0 is
+ * checked by the caller, quant.c:80). */
+O_EXPORT void o_pack_int4_grouped(const float *w, uint8_t *q4, float *scale, int O, int I, int gs) {
+    int rb = (I + 1) / 2, ng = (I + gs - 1) / gs;
+    for (int o = 0; o < O; o++) {
+        const float *wr = w + (int64_t)o * I;
+        uint8_t *qr = q4 + (int64_t)o * rb;
+        float *scl = scale + (int64_t)o * ng;
+        for (int g = 0; g * gs < I; g++) {
+            int base = g * gs, glen = gs;
+            if (base + glen > I) glen = I - base;
+            float amax = 0.f;
+            for (int i = base; i < base + glen; i++) { float a = fabsf(wr[i]); if (a > amax) amax = a; }
+            float s = amax / 7.f;
+            if (s < 1e-8f) s = 1e-8f;
+            scl[g] = s;
+            for (int i = base; i < base + glen; i += 2) {
+                int v0 = (int)lrintf(wr[i] / s);
+                if (v0 > 7) v0 = 7;
+                if (v0 < -8) v0 = -8;
+                int v1 = 0;
+                if (i + 1 < base + glen) {
+                    v1 = (int)lrintf(wr[i + 1] / s);
+                    if (v1 > 7) v1 = 7;
+                    if (v1 < -8) v1 = -8;
+                }
+                qr[i >> 1] = (uint8_t)((v0 + 8) | ((v1 + 8) << 4));
+            }
+        }
+    }
+}
+
+/* a3: Q8 GEMV/GEMM, IDOT path (default).  nn/matmul.c:51-66 + :29-36.
+ * y[s*O+o] = (scale[o] * sx[s]) * (float)dot, two plain multiplies. */
+O_EXPORT void o_matmul_q_s(float *y, const float *x, const int8_t *q, const float *scale,
+                           int S, int I, int O) {
+    int8_t *xi = malloc((size_t)S * I + 1);
+    float *sx = malloc(sizeof(float) * (size_t)(S + 1));
+    for (int s = 0; s < S; s++) sx[s] = o_qrow_i8(x + (int64_t)s * I, xi + (int64_t)s * I, I);
+    #pragma omp parallel for schedule(static)
+    for (int o = 0; o < O; o++)
+        for (int s = 0; s < S; s++) {
+            float a = scale[o] * sx[s];
+            y[(int64_t)s * O + o] = a * (float)o_dot_i8i8(q + (int64_t)o * I, xi + (int64_t)s * I, I);
+        }
+    free(xi); free(sx);
+}
+
+/* Q8 GEMM on activations already quantized (same arithmetic as above). */
+O_EXPORT void o_matmul_q8_preq(float *y, const int8_t *xi, const float *sx, const int8_t *q,
+                               const float *scale, int32_t *acc, int S, int I, int O) {
+    #pragma omp parallel for schedule(static)
+    for (int o = 0; o < O; o++)
+        for (int s = 0; s < S; s++) {
+            int32_t d = o_dot_i8i8(q + (int64_t)o * I, xi + (int64_t)s * I, I);
+            if (acc) acc[(int64_t)s * O + o] = d;
+            if (y) y[(int64_t)s * O + o] = (scale[o] * sx[s]) * (float)d;
+        }
+}
+
+/* a7: grouped int4 dot with int8 activations (IDOT4).  hw/hw_avx512.h:155-176.
+ * Per group: d = sum(n*x) over unsigned nibbles, then
+ * acc = fma(scl[g], (float)(d - 8*xgsum[g]), acc), groups in ascending order
+ * (two statements per 64-chunk; gcc contracts each into one FMA). */
+O_EXPORT float o_dot_i4g8p(const uint8_t *w4, const float *scl, const int8_t *x,
+                           const int32_t *xgsum, int I) {
+    float acc = 0.f;
+    for (int i = 0; i + 64 <= I; i += 64) {
+        for (int h = 0; h < 2; h++) {
+            int g = (i >> 5) + h;
+            int32_t d = 0;
+            for (int j = 0; j < 32; j++) {
+                int e = g * 32 + j;
+                uint8_t b = w4[e >> 1];
+                int n = (e & 1) ? (b >> 4) : (b & 0xF);
+                d += n * x[e];
+            }
+            acc = fmaf(scl[g], (float)(d - 8 * xgsum[g]), acc);
+        }
+    }
+    return acc;
+}
+
+/* a8, IDOT4=1 branch: nn/matmul.c:164-197 + i4g_vnni_rows :148-160.
+ * Requires gs == 32, I % 64 == 0, I <= 16384 (the caller checks). */
+O_EXPORT void o_matmul_i4g_idot4(float *y, const float *x, const uint8_t *q4, const float *scale,
+                                 int S, int I, int O) {
+    int ng = I / 32, rb = (I + 1) / 2;
+    int8_t *xi = malloc((size_t)S * I + 1);
+    int32_t *xg = malloc(sizeof(int32_t) * ((size_t)S * ng + 1));
+    float *sx = malloc(sizeof(float) * (size_t)(S + 1));
+    for (int s = 0; s < S; s++) {
+        sx[s] = o_qrow_i8(x + (int64_t)s * I, xi + (int64_t)s * I, I);
+        for (int g = 0; g < ng; g++) {
+            int32_t a = 0;
+            for (int j = 0; j < 32; j++) a += xi[(int64_t)s * I + g * 32 + j];
+            xg[(int64_t)s * ng + g] = a;
+        }
+    }
+    #pragma omp parallel for schedule(static)
+    for (int o = 0; o < O; o++)
+        for (int s = 0; s < S; s++)
+            y[(int64_t)s * O + o] = sx[s] * o_dot_i4g8p(q4 + (int64_t)o * rb, scale + (int64_t)o * ng,
+                                                        xi + (int64_t)s * I, xg + (int64_t)s * ng, I);
+    free(xi); free(xg); free(sx);
+}
+
+/* The 16-lane horizontal sum of gcc's _mm512_reduce_add_ps: halves 256/128,
+ * then lanes {2,3} onto {0,1}, then lane 1 onto lane 0. */
+static float hsum16(const float *v) {
+    float a[8], b[4];
+    for (int j = 0; j < 8; j++) a[j] = v[j + 8] + v[j];
+    for (int j = 0; j < 4; j++) b[j] = a[j + 4] + a[j];
+    float c0 = b[0] + b[2], c1 = b[1] + b[3];
+    return c0 + c1;
+}
+
+/* a8, default branch (IDOT4 unset): exact f32 activations times dequantized
+ * s*(n-8).  nn/matmul.c:199-253, AVX512 gs == 32 block (:219-235): per group
+ * s1 = x[16:32]*w[16:32] (plain product), s0 + s1 contracted by gcc into
+ * fma(x[0:16], w[0:16], s1), then a = fma(reduce(.), sc, a).  Restated for gs == 32, I % 32 == 0 only. */
+O_EXPORT void o_matmul_i4g_f32(float *y, const float *x, const uint8_t *q4, const float *scale,
+                               int S, int I, int O) {
+    int ng = I / 32, rb = (I + 1) / 2;
+    #pragma omp parallel for schedule(static)
+    for (int o = 0; o < O; o++) {
+        const uint8_t *w = q4 + (int64_t)o * rb;
+        const float *scl = scale + (int64_t)o * ng;
+        for (int s = 0; s < S; s++) {
+            const float *xs = x + (int64_t)s * I;
+            float a = 0.f;
+            for (int g = 0; g < ng; g++) {
+                float t[16];
+                for (int j = 0; j < 16; j++) {
+                    int e0 = g * 32 + j, e1 = g * 32 + 16 + j;
+                    int n0 = (e0 & 1) ? (w[e0 >> 1] >> 4) : (w[e0 >> 1] & 0xF);
+                    int n1 = (e1 & 1) ? (w[e1 >> 1] >> 4) : (w[e1 >> 1] & 0xF);
+                    float p1 = xs[e1] * (float)(n1 - 8);
+                    t[j] = fmaf(xs[e0], (float)(n0 - 8), p1);
+                }
+                a = fmaf(hsum16(t), scl[g], a);
+            }
+            y[(int64_t)s * O + o] = a;
+        }
+    }
+}
+
+/* a10: f32 dot, AVX512 order.  hw/hw_avx512.h:231-243: two 16-lane FMA
+ * chains over 32-element steps, a 16-element step on chain 0, then
+ * reduce(s0 + s1), then a scalar FMA tail. */
+O_EXPORT float o_dot_f32(const float *a, const float *b, int n) {
+    float s0[16], s1[16];
+    for (int l = 0; l < 16; l++) { s0[l] = 0.f; s1[l] = 0.f; }
+    int i = 0;
+    for (; i + 32 <= n; i += 32)
+        for (int l = 0; l < 16; l++) {
+            s0[l] = fmaf(a[i + l], b[i + l], s0[l]);
+            s1[l] = fmaf(a[i + 16 + l], b[i + 16 + l], s1[l]);
+        }
+    for (; i + 16 <= n; i += 16)
+        for (int l = 0; l < 16; l++) s0[l] = fmaf(a[i + l], b[i + l], s0[l]);
+    float t[16];
+    for (int l = 0; l < 16; l++) t[l] = s0[l] + s1[l];
+    float s = hsum16(t);
+    for (; i < n; i++) s = fmaf(a[i], b[i], s);
+    return s;
+}
+
+/* moty_matmul (nn/matmul.c:15-27): y[s*O+o] = dot_f32(x[s], W[o], I). */
+O_EXPORT void o_matmul_f32(float *y, const float *x, const float *W, int S, int I, int O) {
+    #pragma omp parallel for schedule(static)
+    for (int o = 0; o < O; o++)
+        for (int s = 0; s < S; s++)
+            y[(int64_t)s * O + o] = o_dot_f32(x + (int64_t)s * I, W + (int64_t)o * I, I);
+}
+
+/* ------------------------------------------------------------------ */
+/* expf.  The reference calls glibc 2.35 expf (hw/hw_ops.h:20,24).  glibc's
+ * expf is the table-driven method of ARM's optimized-routines (Szabolcs
+ * Nagy): k = round(x*N/ln2), N = 32, r = x*N/ln2 - k,
+ * exp(x) = 2^(k/N) * (1 + C2 r + C1 r^2 + C0 r^3) evaluated in double, with
+ * the x86-64 FMA build contracting every multiply-add.  o_expf restates it;
+ * the HIP library uses the same steps.  The 2^(i/32) table is built from
+ * exp2l; the whole function is checked against libm expf on every float. */
+static uint64_t g_t2[32];
+static int g_t2_ready;
+static const double EXP_N = 32.0;
+static const double EXP_C0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+static const double EXP_C1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+static const double EXP_C2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+static const double EXP_INVLN2N = 0x1.71547652b82fep+0 * 32.0;
+static const double EXP_SHIFT = 0x1.8p+52;
+
+static void t2_init(void) {
+    if (g_t2_ready) return;
+    for (int i = 0; i < 32; i++) {
+        double v = (double)exp2l((long double)i / 32.0L);
+        uint64_t u; memcpy(&u, &v, 8);
+        g_t2[i] = u - ((uint64_t)i << 47);
+    }
+    g_t2_ready = 1;
+}
+
+O_EXPORT void o_expf_table(uint64_t *out32) { t2_init(); memcpy(out32, g_t2, sizeof g_t2); }
+
+O_EXPORT float o_expf(float x) {
+    t2_init();
+    uint32_t ux; memcpy(&ux, &x, 4);
+    uint32_t abstop = (ux >> 20) & 0x7ff;
+    if (abstop >= 0x42b) {                       /* |x| >= 88 or nan/inf */
+        if (ux == 0xff800000u) return 0.f;       /* -inf */
+        if (abstop >= 0x7f8) return x + x;       /* inf or nan */
+        if (x > 0x1.62e42ep6f) return INFINITY;  /* overflow */
+        if (x < -0x1.9fe368p6f) return 0.f;      /* underflow */
+    }
+    (void)EXP_N;
+    double xd = (double)x;
+    double kd = fma(EXP_INVLN2N, xd, EXP_SHIFT);
+    uint64_t ki; memcpy(&ki, &kd, 8);
+    kd -= EXP_SHIFT;
+    double r = fma(EXP_INVLN2N, xd, -kd);
+    uint64_t t = g_t2[ki % 32] + (ki << 47);
+    double s; memcpy(&s, &t, 8);
+    double z = fma(EXP_C0, r, EXP_C1);
+    double r2 = r * r;
+    double y = fma(EXP_C2, r, 1.0);
+    y = fma(z, r2, y);
+    y = y * s;
+    return (float)y;
+}
+
+/* Exhaustive comparison of o_expf with libm expf over [lo, hi) of the 32-bit
+ * patterns; returns the number of mismatching non-NaN inputs. */
+O_EXPORT int64_t o_expf_check_range(uint64_t lo, uint64_t hi) {
+    int64_t bad = 0;
+    t2_init();
+    #pragma omp parallel for reduction(+:bad) schedule(dynamic, 65536)
+    for (int64_t u = (int64_t)lo; u < (int64_t)hi; u++) {
+        uint32_t b = (uint32_t)u; float x; memcpy(&x, &b, 4);
+        if (x != x) continue;
+        float p = expf(x), q = o_expf(x);
+        uint32_t bp, bq; memcpy(&bp, &p, 4); memcpy(&bq, &q, 4);
+        if (bp != bq) bad++;
+    }
+    return bad;
+}
+
+/* a9: g = (g / (1 + expf(-g))) * u.  hw/hw_ops.h:19-21 */
+O_EXPORT void o_silu_mul(float *g, const float *u, int64_t n) {
+    for (int64_t i = 0; i < n; i++) { float v = g[i]; g[i] = (v / (1.f + expf(-v))) * u[i]; }
+}
+
+/* a11: max-subtracted softmax with a sequential sum.  hw/hw_ops.h:22-26 */
+O_EXPORT void o_softmax(float *x, int n) {
+    float m = -1e30f;
+    for (int i = 0; i < n; i++) if (x[i] > m) m = x[i];
+    float s = 0.f;
+    for (int i = 0; i < n; i++) { x[i] = expf(x[i] - m); s += x[i]; }
+    for (int i = 0; i < n; i++) x[i] /= s;
+}
+
+/* a12: greedy top-K, strict '>', lowest index wins ties, optional
+ * normalisation by the sequential sum.  runtime/moecache.c:97-111 */
+O_EXPORT void o_topk(const float *p, int E, int K, int *idx, float *w, int norm) {
+    for (int kk = 0; kk < K; kk++) {
+        int best = -1; float bv = -1e30f;
+        for (int e = 0; e < E; e++) {
+            int taken = 0;
+            for (int j = 0; j < kk; j++) if (idx[j] == e) { taken = 1; break; }
+            if (!taken && p[e] > bv) { bv = p[e]; best = e; }
+        }
+        idx[kk] = best; w[kk] = bv;
+    }
+    if (norm) {
+        float sm = 0.f;
+        for (int kk = 0; kk < K; kk++) sm += w[kk];
+        if (sm > 0) for (int kk = 0; kk < K; kk++) w[kk] /= sm;
+    }
+}
+
+/* Router: logits = x . Wr^T (f32, a10), optional per-expert logit bias
+ * (moty_moe_route_bias, runtime/moecache.c:91-95 adds to the chosen
+ * logits), softmax (a11), top-K (a12). */
+O_EXPORT void o_route(const float *x, const float *Wr, const float *bias, int S, int D, int E,
+                      int K, int norm, int *idx, float *w, float *probs_out) {
+    float *lg = malloc(sizeof(float) * (size_t)S * E);
+    o_matmul_f32(lg, x, Wr, S, D, E);
+    for (int s = 0; s < S; s++) {
+        float *p = lg + (int64_t)s * E;
+        if (bias) for (int e = 0; e < E; e++) p[e] += bias[e];
+        o_softmax(p, E);
+        o_topk(p, E, K, idx + (int64_t)s * K, w + (int64_t)s * K, norm);
+    }
+    if (probs_out) memcpy(probs_out, lg, sizeof(float) * (size_t)S * E);
+    free(lg);
+}
+
+/* One expert over one token row: the per-token body of engines/olmoe.c:
+ * 230-240 and of nn/moe.c:192-198 (the two agree per row, matmul_q_s is
+ * batch-invariant).  Expert weights are stacked [E][I][D] / [E][D][I]. */
+static void expert_row(float *hh, const float *xs, const int8_t *G, const float *GS,
+                       const int8_t *U, const float *US, const int8_t *Dn, const float *DS,
+                       int eid, int I, int D, float *g, float *u) {
+    const int8_t *ge = G + (int64_t)eid * I * D, *ue = U + (int64_t)eid * I * D;
+    const int8_t *de = Dn + (int64_t)eid * D * I;
+    o_matmul_q_s(g, xs, ge, GS + (int64_t)eid * I, 1, D, I);
+    o_matmul_q_s(u, xs, ue, US + (int64_t)eid * I, 1, D, I);
+    o_silu_mul(g, u, I);
+    o_matmul_q_s(hh, g, de, DS + (int64_t)eid * D, 1, I, D);
+}
+
+/* a13, olmoe engine order: engines/olmoe.c:219-244.  Per token, experts in
+ * top-k order, out[d] = fma(w[kk], hh[d], out[d]). */
+O_EXPORT void o_moe_olmoe(float *out, const float *x, int S, const float *Wr, const float *bias,
+                          const int8_t *G, const float *GS, const int8_t *U, const float *US,
+                          const int8_t *Dn, const float *DS, int E, int K, int I, int D, int norm,
+                          int *idx_out, float *w_out) {
+    int *idx = malloc(sizeof(int) * (size_t)S * K);
+    float *w = malloc(sizeof(float) * (size_t)S * K);
+    o_route(x, Wr, bias, S, D, E, K, norm, idx, w, NULL);
+    memset(out, 0, sizeof(float) * (size_t)S * D);
+    #pragma omp parallel
+    {
+        float *g = malloc(sizeof(float) * I), *u = malloc(sizeof(float) * I);
+        float *hh = malloc(sizeof(float) * D);
+        #pragma omp for schedule(dynamic, 1)
+        for (int s = 0; s < S; s++) {
+            for (int kk = 0; kk < K; kk++) {
+                expert_row(hh, x + (int64_t)s * D, G, GS, U, US, Dn, DS, idx[s * K + kk], I, D, g, u);
+                float *os = out + (int64_t)s * D;
+                for (int d = 0; d < D; d++) os[d] = fmaf(w[s * K + kk], hh[d], os[d]);
+            }
+        }
+        free(g); free(u); free(hh);
+    }
+    if (idx_out) memcpy(idx_out, idx, sizeof(int) * (size_t)S * K);
+    if (w_out) memcpy(w_out, w, sizeof(float) * (size_t)S * K);
+    free(idx); free(w);
+}
+
+/* a13, shared batch order: nn/moe.c:159-205 (moe_batch_core, no shared
+ * expert), routing always normalised (nn/moe.c:27-30).  Experts ascending;
+ * each token's contribution from expert eid is added when eid is visited,
+ * so per token the combine runs in ascending expert id. */
+O_EXPORT void o_moe_batch(float *out, const float *x, int S, const float *Wr, const float *bias,
+                          const int8_t *G, const float *GS, const int8_t *U, const float *US,
+                          const int8_t *Dn, const float *DS, int E, int K, int I, int D,
+                          int *idx_out, float *w_out) {
+    int *idx = malloc(sizeof(int) * (size_t)S * K);
+    float *w = malloc(sizeof(float) * (size_t)S * K);
+    o_route(x, Wr, bias, S, D, E, K, 1, idx, w, NULL);
+    memset(out, 0, sizeof(float) * (size_t)S * D);
+    #pragma omp parallel
+    {
+        float *g = malloc(sizeof(float) * I), *u = malloc(sizeof(float) * I);
+        float *hh = malloc(sizeof(float) * D);
+        int *ord = malloc(sizeof(int) * K);
+        #pragma omp for schedule(dynamic, 1)
+        for (int s = 0; s < S; s++) {
+            /* visit this token's experts in ascending id */
+            for (int kk = 0; kk < K; kk++) ord[kk] = kk;
+            for (int a = 1; a < K; a++)
+                for (int b = a; b > 0 && idx[s * K + ord[b]] < idx[s * K + ord[b - 1]]; b--) {
+                    int t = ord[b]; ord[b] = ord[b - 1]; ord[b - 1] = t;
+                }
+            for (int j = 0; j < K; j++) {
+                int kk = ord[j];
+                expert_row(hh, x + (int64_t)s * D, G, GS, U, US, Dn, DS, idx[s * K + kk], I, D, g, u);
+                float *os = out + (int64_t)s * D;
+                for (int d = 0; d < D; d++) os[d] = fmaf(w[s * K + kk], hh[d], os[d]);
+            }
+        }
+        free(g); free(u); free(hh); free(ord);
+    }
+    if (idx_out) memcpy(idx_out, idx, sizeof(int) * (size_t)S * K);
+    if (w_out) memcpy(w_out, w, sizeof(float) * (size_t)S * K);
+    free(idx); free(w);
+}
+
+/* Dense SwiGLU FFN over Q8 weights: nn/ffn.c:26-55 / engines/qwen.c:659-679
+ * (gate, up, silu*up, down through matmul_q_s). */
+O_EXPORT void o_dense_ffn_q8(float *out, const float *x, int S, const int8_t *G, const float *GS,
+                             const int8_t *U, const float *US, const int8_t *Dn, const float *DS,
+                             int D, int I) {
+    float *g = malloc(sizeof(float) * (size_t)S * I), *u = malloc(sizeof(float) * (size_t)S * I);
+    o_matmul_q_s(g, x, G, GS, S, D, I);
+    o_matmul_q_s(u, x, U, US, S, D, I);
+    o_silu_mul(g, u, (int64_t)S * I);
+    o_matmul_q_s(out, g, Dn, DS, S, I, D);
+    free(g); free(u);
+}

@@ -1,0 +1,225 @@
+"""ctypes loaders for the CPU checkers: the oracle restatement
+(oracle/liboracle.so) and the compiled reference (oracle/_ref/*.so).
+
+Test infrastructure only; the product library is loaded by moty_amd."""
+import ctypes as C
+import os
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_SO = os.path.join(ROOT, "oracle", "liboracle.so")
+REF_SO = os.path.join(ROOT, "oracle", "_ref", "libmotyref.so")
+REF_F32_SO = os.path.join(ROOT, "oracle", "_ref", "libmotyref_f32.so")
+
+P = C.c_void_p
+I32 = C.c_int
+I64 = C.c_int64
+F32 = C.c_float
+
+
+def ptr(a):
+    return None if a is None else C.c_void_p(a.ctypes.data)
+
+
+_SIGS = {
+    "o_qrow_i8": (F32, [P, P, I32]),
+    "o_dot_i8i8": (C.c_int32, [P, P, I32]),
+    "o_quantize_rows": (None, [P, P, P, I32, I32, I32]),
+    "o_pack_int4_grouped": (None, [P, P, P, I32, I32, I32]),
+    "o_matmul_q_s": (None, [P, P, P, P, I32, I32, I32]),
+    "o_matmul_q8_preq": (None, [P, P, P, P, P, P, I32, I32, I32]),
+    "o_dot_i4g8p": (F32, [P, P, P, P, I32]),
+    "o_matmul_i4g_idot4": (None, [P, P, P, P, I32, I32, I32]),
+    "o_matmul_i4g_f32": (None, [P, P, P, P, I32, I32, I32]),
+    "o_dot_f32": (F32, [P, P, I32]),
+    "o_matmul_f32": (None, [P, P, P, I32, I32, I32]),
+    "o_expf": (F32, [F32]),
+    "o_expf_table": (None, [P]),
+    "o_expf_check_range": (I64, [C.c_uint64, C.c_uint64]),
+    "o_silu_mul": (None, [P, P, I64]),
+    "o_softmax": (None, [P, I32]),
+    "o_topk": (None, [P, I32, I32, P, P, I32]),
+    "o_route": (None, [P, P, P, I32, I32, I32, I32, I32, P, P, P]),
+    "o_moe_olmoe": (None, [P, P, I32, P, P, P, P, P, P, P, P, I32, I32, I32, I32, I32, P, P]),
+    "o_moe_batch": (None, [P, P, I32, P, P, P, P, P, P, P, P, I32, I32, I32, I32, P, P]),
+    "o_dense_ffn_q8": (None, [P, P, I32, P, P, P, P, P, P, I32, I32]),
+    "ref_init": (None, [I32]),
+    "ref_tier": (C.c_char_p, []),
+    "ref_qrow_i8": (F32, [P, P, I32]),
+    "ref_dot_i8i8": (C.c_int32, [P, P, I32]),
+    "ref_dot_f32": (F32, [P, P, I32]),
+    "ref_dot_i4g8p": (F32, [P, P, P, P, I32]),
+    "ref_quantize_rows": (None, [P, P, P, I32, I32, I32]),
+    "ref_pack_int4_grouped": (None, [P, P, P, I32, I32, I32]),
+    "ref_matmul_q_s": (None, [P, P, P, P, I32, I32, I32]),
+    "ref_matmul_i4_grouped_s": (None, [P, P, P, P, I32, I32, I32, I32]),
+    "ref_matmul": (None, [P, P, P, I32, I32, I32]),
+    "ref_silu_mul": (None, [P, P, I64]),
+    "ref_softmax": (None, [P, I32]),
+    "ref_expf": (F32, [F32]),
+    "ref_topk": (None, [P, I32, I32, P, P, I32]),
+    "ref_moe_batch": (None, [P, P, I32, P, P, P, P, P, P, P, I32, I32, I32, I32]),
+    "ref_moe_olmoe": (None, [P, P, I32, P, P, P, P, P, P, P, I32, I32, I32, I32, I32, P]),
+}
+
+
+def _bind(lib):
+    for name, (res, args) in _SIGS.items():
+        if hasattr(lib, name):
+            f = getattr(lib, name)
+            f.restype = res
+            f.argtypes = args
+    return lib
+
+
+_cache = {}
+
+
+def oracle():
+    if "o" not in _cache:
+        if not os.path.exists(ORACLE_SO):
+            raise RuntimeError("oracle/liboracle.so is not built (run __graft_entry__.build())")
+        _cache["o"] = _bind(C.CDLL(ORACLE_SO))
+    return _cache["o"]
+
+
+def cpu_has_vnni():
+    try:
+        with open("/proc/cpuinfo") as f:
+            flags = f.read()
+        return "avx512_vnni" in flags and "avx512bw" in flags
+    except OSError:
+        return False
+
+
+def ref(idot4=True):
+    """The compiled reference; None when it is not built or the host lacks
+    the AVX512-VNNI tier it was compiled for."""
+    key = "r4" if idot4 else "r32"
+    if key not in _cache:
+        path = REF_SO if idot4 else REF_F32_SO
+        if not os.path.exists(path) or not cpu_has_vnni():
+            _cache[key] = None
+        else:
+            lib = _bind(C.CDLL(path))
+            lib.ref_init(1 if idot4 else 0)
+            _cache[key] = lib
+    return _cache[key]
+
+
+# ---- numpy-level helpers over the oracle ----
+def f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def o_quantize_rows(w, bits=8):
+    O, I = w.shape
+    q = np.empty((O, I), np.int8)
+    s = np.empty(O, np.float32)
+    oracle().o_quantize_rows(ptr(f32(w)), ptr(q), ptr(s), O, I, bits)
+    return q, s
+
+
+def o_pack_int4_grouped(w, gs=32):
+    O, I = w.shape
+    ng = (I + gs - 1) // gs
+    q4 = np.empty((O, (I + 1) // 2), np.uint8)
+    s = np.empty((O, ng), np.float32)
+    oracle().o_pack_int4_grouped(ptr(f32(w)), ptr(q4), ptr(s), O, I, gs)
+    return q4, s
+
+
+def o_qrow(x):
+    x = f32(x)
+    S, I = x.shape
+    q = np.empty((S, I), np.int8)
+    sx = np.empty(S, np.float32)
+    for s in range(S):
+        sx[s] = oracle().o_qrow_i8(C.c_void_p(x.ctypes.data + s * I * 4), C.c_void_p(q.ctypes.data + s * I), I)
+    return q, sx
+
+
+def o_matmul_q_s(x, q, scale):
+    x = f32(x)
+    S, I = x.shape
+    O = q.shape[0]
+    y = np.empty((S, O), np.float32)
+    oracle().o_matmul_q_s(ptr(y), ptr(x), ptr(q), ptr(scale), S, I, O)
+    return y
+
+
+def o_matmul_q8_acc(xq, q):
+    S, I = xq.shape
+    O = q.shape[0]
+    acc = np.empty((S, O), np.int32)
+    sx = np.ones(S, np.float32)
+    sc = np.ones(O, np.float32)
+    oracle().o_matmul_q8_preq(None, ptr(xq), ptr(sx), ptr(q), ptr(sc), ptr(acc), S, I, O)
+    return acc
+
+
+def o_matmul_i4g(x, q4, scale, idot4=True):
+    x = f32(x)
+    S, I = x.shape
+    O = q4.shape[0]
+    y = np.empty((S, O), np.float32)
+    fn = oracle().o_matmul_i4g_idot4 if idot4 else oracle().o_matmul_i4g_f32
+    fn(ptr(y), ptr(x), ptr(q4), ptr(scale), S, I, O)
+    return y
+
+
+def o_matmul_f32(x, W):
+    x = f32(x)
+    S, I = x.shape
+    O = W.shape[0]
+    y = np.empty((S, O), np.float32)
+    oracle().o_matmul_f32(ptr(y), ptr(x), ptr(f32(W)), S, I, O)
+    return y
+
+
+def o_route(x, Wr, K, norm, bias=None):
+    x = f32(x)
+    S, D = x.shape
+    E = Wr.shape[0]
+    idx = np.empty((S, K), np.int32)
+    w = np.empty((S, K), np.float32)
+    probs = np.empty((S, E), np.float32)
+    oracle().o_route(ptr(x), ptr(f32(Wr)), ptr(None if bias is None else f32(bias)), S, D, E, K, norm,
+                     ptr(idx), ptr(w), ptr(probs))
+    return idx, w, probs
+
+
+def o_moe(x, Wr, ex, K, order="batch", norm=1, bias=None):
+    """ex = dict(G,GS,U,US,Dn,DS) stacked expert weights."""
+    x = f32(x)
+    S, D = x.shape
+    E = Wr.shape[0]
+    I = ex["G"].shape[1]
+    out = np.empty((S, D), np.float32)
+    idx = np.empty((S, K), np.int32)
+    w = np.empty((S, K), np.float32)
+    args = [ptr(ex[k]) for k in ("G", "GS", "U", "US", "Dn", "DS")]
+    b = ptr(None if bias is None else f32(bias))
+    if order == "batch":
+        oracle().o_moe_batch(ptr(out), ptr(x), S, ptr(f32(Wr)), b, *args, E, K, I, D, ptr(idx), ptr(w))
+    else:
+        oracle().o_moe_olmoe(ptr(out), ptr(x), S, ptr(f32(Wr)), b, *args, E, K, I, D, norm, ptr(idx), ptr(w))
+    return out, idx, w
+
+
+def o_dense_ffn_q8(x, G, GS, U, US, Dn, DS):
+    x = f32(x)
+    S, D = x.shape
+    I = G.shape[0]
+    out = np.empty((S, D), np.float32)
+    oracle().o_dense_ffn_q8(ptr(out), ptr(x), S, ptr(G), ptr(GS), ptr(U), ptr(US), ptr(Dn), ptr(DS), D, I)
+    return out
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+def randn(seed, shape, std=1.0):
+    return (rng(seed).standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
