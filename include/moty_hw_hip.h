@@ -1,0 +1,144 @@
+/* moty_hw_hip.h -- libmoty-hw-hip: the MI355X (gfx950) backend for moty's
+ * quantized-matmul and MoE hot path, as a plain C ABI.
+ *
+ * Two surfaces:
+ *  1. Host-pointer drop-ins with the reference's own signatures and argument
+ *     meaning.  Weights are uploaded once, on first use, into a device cache
+ *     keyed by the host pointer (weights are persistent for a model's life in
+ *     the reference, nn/nn_mat.h:18-25); x is uploaded and y downloaded per
+ *     call; the call is synchronous, like the CPU kernels.
+ *  2. Device-pointer entry points (suffix _dev): every pointer is device
+ *     memory, work is queued on `stream` (a hipStream_t, NULL = the default
+ *     stream) and returns without synchronising.
+ *
+ * Every function returns MOTY_HIP_OK (0) or an error code, and never aborts;
+ * moty_hip_last_error() describes the last failure.  A caller that keeps a
+ * CPU path (as engines/glm.c:798-810 does for its CUDA matmul) falls back
+ * on a nonzero return.  Calls share library-owned scratch per device and are
+ * not re-entrant, like the reference's process-static activation buffers
+ * (nn/matmul.c:55-58).
+ *
+ * Numerics match the reference's x86-64 AVX512-VNNI build: int8 activations
+ * and int32 accumulators bit-exact, float steps in the reference's order
+ * (including the FMAs gcc contracts), expf identical to glibc's.
+ */
+#ifndef MOTY_HW_HIP_H
+#define MOTY_HW_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOTY_HIP_OK 0
+#define MOTY_HIP_EINVAL 1  /* bad argument or shape */
+#define MOTY_HIP_EHIP 2    /* HIP runtime error (no device, fault, ...) */
+#define MOTY_HIP_ENOMEM 3  /* device allocation failed */
+#define MOTY_HIP_EUNSUP 4  /* shape/format this backend does not serve */
+
+/* combine order of the MoE layer */
+#define MOTY_MOE_ORDER_TOPK 0   /* per token, experts in top-k order: engines/olmoe.c:230-243 */
+#define MOTY_MOE_ORDER_EXPERT 1 /* per token, ascending expert id: nn/moe.c:186-203 */
+
+/* ---------------- library ---------------- */
+/* Select the device for this thread's calls and create its stream/scratch.
+ * Optional: every entry point initialises device 0 on first use. */
+int moty_hip_init(int device);
+/* Free the weight cache, scratch and stream of every initialised device. */
+int moty_hip_shutdown(void);
+const char *moty_hip_last_error(void);
+/* Kernel tier string, the analogue of HW_IDOT_KERNEL/HW_F32_KERNEL
+ * (hw/hw.h:160-208): "gfx950-mfma-i8/gfx950-f32". */
+const char *moty_hip_kernel_tier(void);
+
+/* ---------------- host-pointer drop-ins ---------------- */
+/* moty_matmul_q_s (nn/nn_matmul.h:64, nn/matmul.c:51-66): Q8_0 per-row int8
+ * weights q [O][I] + scale [O]; x [S][I] f32 token-major; y [S][O].  IDOT=0
+ * in the environment is reported as MOTY_HIP_EUNSUP (the f32xint8 variant
+ * stays on the CPU). */
+int moty_hip_matmul_q_s(float *y, const float *x, const int8_t *q, const float *scale, int S, int I, int O);
+/* moty_matmul_i4_grouped_s (nn/nn_matmul.h:67-68, nn/matmul.c:164-197):
+ * nibbles q4 [O][(I+1)/2], f32 group scales [O][ceil(I/gs)].  IDOT4 is read
+ * from the environment once per process (nn/matmul.c:171): IDOT4=1 with
+ * gs == 32, I % 64 == 0, I <= 16384 selects the int8-activation path,
+ * anything else the exact f32 path (served for gs == 32, I % 32 == 0). */
+int moty_hip_matmul_i4_grouped_s(float *y, const float *x, const uint8_t *q4, const float *scale, int S, int I,
+                                 int O, int gs);
+/* moty_matmul (nn/nn_matmul.h:63, nn/matmul.c:15-27): f32 W [O][I], dot_f32
+ * in the AVX512 order (hw/hw_avx512.h:231-243).  The f32 MoE router. */
+int moty_hip_matmul(float *y, const float *x, const float *W, int S, int I, int O);
+
+/* The MoE layer's inputs (the device analogue of MotyMoeView, nn/moe.h:19-33,
+ * with the experts resident instead of behind an ExpertCache):
+ * router [E][D] f32; experts stacked g,u [E][I][D], d [E][D][I] int8 with
+ * per-row scales gs,us [E][I], ds [E][D] (ExpertSlot, runtime/moe.h:35-39,
+ * quantized by moty_quantize_rows with EBITS=8). */
+typedef struct MotyHipMoe {
+    const float *router;
+    const float *logit_bias; /* [E] added to the logits before softmax, or NULL */
+    const int8_t *g, *u, *d;
+    const float *gs, *us, *ds;
+    int E, K, I, D;
+    int norm_topk;           /* moty_moe_topk's norm_topk (runtime/moecache.c:97) */
+    int combine_order;       /* MOTY_MOE_ORDER_* */
+    int32_t *idx_out;        /* optional [S][K] expert ids (same memory kind as x) */
+    float *w_out;            /* optional [S][K] routing weights */
+    int32_t *counts_out;     /* optional [E] tokens per expert */
+} MotyHipMoe;
+
+/* moty_nn_moe_topk_batch (nn/moe.h:38, nn/moe.c:159-208; no shared expert)
+ * with combine_order = EXPERT and norm_topk = 1, or the olmoe engine's
+ * per-token MoE (engines/olmoe.c:219-244) with combine_order = TOPK.
+ * Host pointers; out [S][D]. */
+int moty_hip_moe_topk(const MotyHipMoe *m, const float *x, int S, float *out);
+
+/* Drop the cached device copy of a host weight buffer (after the caller
+ * frees or rewrites it). */
+int moty_hip_weight_forget(const void *host_ptr);
+
+/* HwBackend.matmul_i8 slot (hw/hw_backend.h:57-58), which returns void:
+ * on failure y is left untouched and moty_hip_last_error() says why. */
+void moty_hip_hw_matmul_i8(float *y, const float *x, const int8_t *q, const float *scale, int S, int I, int O);
+
+/* ---------------- device-pointer entry points ---------------- */
+/* qrow_i8 over S rows (hw/hw_quant.h:9-16): q [S][I], sx [S]; xg [S][I/32]
+ * group sums when non-NULL (I % 32 == 0). */
+int moty_hip_qrow_i8_dev(const float *x, int8_t *q, float *sx, int32_t *xg, int S, int I, void *stream);
+/* moty_quantize_rows (nn/quant.c:12-33) */
+int moty_hip_quantize_rows_dev(const float *w, int8_t *q, float *scale, int O, int I, int bits, void *stream);
+/* moty_pack_int4_grouped (nn/quant.c:57-83); gs % 16 == 0 as the reference requires */
+int moty_hip_pack_int4_grouped_dev(const float *w, uint8_t *q4, float *scale, int O, int I, int gs,
+                                   void *stream);
+/* moty_matmul_q_s: S <= 4 runs the decode GEMV with fused activation
+ * quantization, larger S quantizes then runs the int8 MFMA GEMM. */
+int moty_hip_matmul_q_s_dev(float *y, const float *x, const int8_t *q, const float *scale, int S, int I, int O,
+                            void *stream);
+/* the Q8 GEMM on activations already quantized by moty_hip_qrow_i8_dev
+ * (several projections of one input share one quantization) */
+int moty_hip_matmul_q8_preq_dev(float *y, const int8_t *xq, const float *sx, const int8_t *q, const float *scale,
+                                int S, int I, int O, void *stream);
+/* moty_matmul_i4_grouped_s; idot4 selects the path explicitly */
+int moty_hip_matmul_i4_grouped_s_dev(float *y, const float *x, const uint8_t *q4, const float *scale, int S,
+                                     int I, int O, int gs, int idot4, void *stream);
+/* moty_matmul (f32, dot_f32 order) */
+int moty_hip_matmul_dev(float *y, const float *x, const float *W, int S, int I, int O, void *stream);
+/* moty_hw_silu_mul (hw/hw_ops.h:19-21): g = silu(g) * u */
+int moty_hip_silu_mul_dev(float *g, const float *u, int64_t n, void *stream);
+/* moty_softmax_row (nn/norm.c:10, hw/hw_ops.h:22-26) over S rows of n, in place */
+int moty_hip_softmax_rows_dev(float *x, int S, int n, void *stream);
+/* expf over an array, bit-identical to the glibc expf the reference calls
+ * (hw/hw_ops.h:20); the device routine every SiLU/softmax here uses. */
+int moty_hip_expf_dev(const float *x, float *y, int64_t n, void *stream);
+/* Dense SwiGLU FFN over Q8 weights, moty_nn_dense_ffn (nn/ffn.c:26-55):
+ * gate,up [I][D] + scales [I], down [D][I] + scale [D]; x [S][D]; out [S][D]. */
+int moty_hip_dense_ffn_q8_dev(float *out, const float *x, int S, const int8_t *gate, const float *gs,
+                              const int8_t *up, const float *us, const int8_t *down, const float *ds, int D, int I,
+                              void *stream);
+/* the MoE layer, all pointers in m and x/out on the device */
+int moty_hip_moe_topk_dev(const MotyHipMoe *m, const float *x, int S, float *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MOTY_HW_HIP_H */

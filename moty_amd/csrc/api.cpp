@@ -1,0 +1,495 @@
+// api.cpp -- the C ABI of libmoty-hw-hip (include/moty_hw_hip.h).
+//
+// Owns, per device: one HIP stream for the synchronous host-pointer calls,
+// a growable scratch arena (activation quantization, MoE intermediates),
+// a transfer arena for host x/y, and the weight cache keyed by host pointer.
+// Device entry points only validate, carve scratch and queue kernels.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <mutex>
+#include <unordered_map>
+
+#include "../../include/moty_hw_hip.h"
+#include "common.h"
+#include "kernels.h"
+
+namespace moty {
+
+static thread_local char g_err[512] = "";
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+}
+
+int check_hip(hipError_t e, const char* what) {
+  set_error("%s: %s", what, hipGetErrorString(e));
+  return e == hipErrorOutOfMemory ? MOTY_ENOMEM : MOTY_EHIP;
+}
+
+struct WEntry {
+  void* dev;
+  size_t bytes;
+};
+
+struct Arena {
+  void* p = nullptr;
+  size_t cap = 0;
+};
+
+struct Dev {
+  bool ready = false;
+  hipStream_t stream = nullptr;
+  Arena scratch, io;
+  std::unordered_map<const void*, WEntry> wcache;
+};
+
+constexpr int MAX_DEV = 16;
+static Dev g_dev[MAX_DEV];
+static std::mutex g_mu;  // guards g_dev[*] set-up and the weight caches
+static thread_local int t_dev = -1;
+
+static int dev_init(int d) {
+  int n = 0;
+  HIP_TRY(hipGetDeviceCount(&n));
+  if (d < 0 || d >= n || d >= MAX_DEV) {
+    set_error("moty_hip_init: device %d not present (%d visible)", d, n);
+    return MOTY_EINVAL;
+  }
+  HIP_TRY(hipSetDevice(d));
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!g_dev[d].ready) {
+    HIP_TRY(hipStreamCreateWithFlags(&g_dev[d].stream, hipStreamNonBlocking));
+    g_dev[d].ready = true;
+  }
+  t_dev = d;
+  return MOTY_OK;
+}
+
+static int cur(Dev** out) {
+  if (t_dev < 0) {
+    int rc = dev_init(0);
+    if (rc) return rc;
+  } else {
+    HIP_TRY(hipSetDevice(t_dev));
+  }
+  *out = &g_dev[t_dev];
+  return MOTY_OK;
+}
+
+// Grow an arena to at least `bytes`.  Waits for queued work that may still
+// read the old buffer before releasing it.
+static int arena_get(Arena& a, size_t bytes, void** p) {
+  if (bytes == 0) bytes = 256;
+  if (a.cap < bytes) {
+    if (a.p) {
+      HIP_TRY(hipDeviceSynchronize());
+      HIP_TRY(hipFree(a.p));
+      a.p = nullptr;
+      a.cap = 0;
+    }
+    size_t nb = bytes + bytes / 4;
+    nb = (nb + (1 << 20) - 1) & ~(size_t)((1 << 20) - 1);
+    hipError_t e = hipMalloc(&a.p, nb);
+    if (e != hipSuccess) {
+      a.p = nullptr;
+      return check_hip(e, "scratch hipMalloc");
+    }
+    a.cap = nb;
+  }
+  *p = a.p;
+  return MOTY_OK;
+}
+
+static inline size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// Device copy of a persistent host weight buffer.
+static int weight(Dev* d, const void* host, size_t bytes, const void** dev) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = d->wcache.find(host);
+  if (it != d->wcache.end() && it->second.bytes >= bytes) {
+    *dev = it->second.dev;
+    return MOTY_OK;
+  }
+  if (it != d->wcache.end()) {
+    HIP_TRY(hipStreamSynchronize(d->stream));
+    HIP_TRY(hipFree(it->second.dev));
+    d->wcache.erase(it);
+  }
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
+  if (e != hipSuccess) return check_hip(e, "weight hipMalloc");
+  e = hipMemcpy(p, host, bytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    hipFree(p);
+    return check_hip(e, "weight upload");
+  }
+  d->wcache[host] = WEntry{p, bytes};
+  *dev = p;
+  return MOTY_OK;
+}
+
+static int env_int(const char* name, int dflt) {
+  const char* e = getenv(name);
+  return e ? atoi(e) : dflt;
+}
+
+}  // namespace moty
+
+using namespace moty;
+
+#define CUR(d)          \
+  Dev* d = nullptr;     \
+  {                     \
+    int _rc = cur(&d);  \
+    if (_rc) return _rc; \
+  }
+#define STREAM(s) ((hipStream_t)(s))
+
+extern "C" {
+
+int moty_hip_init(int device) { return dev_init(device); }
+
+int moty_hip_shutdown(void) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  for (int i = 0; i < MAX_DEV; i++) {
+    Dev& d = g_dev[i];
+    if (!d.ready) continue;
+    HIP_TRY(hipSetDevice(i));
+    HIP_TRY(hipDeviceSynchronize());
+    for (auto& kv : d.wcache) hipFree(kv.second.dev);
+    d.wcache.clear();
+    if (d.scratch.p) hipFree(d.scratch.p);
+    if (d.io.p) hipFree(d.io.p);
+    d.scratch = Arena();
+    d.io = Arena();
+    hipStreamDestroy(d.stream);
+    d.stream = nullptr;
+    d.ready = false;
+  }
+  t_dev = -1;
+  return MOTY_OK;
+}
+
+const char* moty_hip_last_error(void) { return g_err; }
+const char* moty_hip_kernel_tier(void) { return "gfx950-mfma-i8/gfx950-f32"; }
+
+// ---------------- device-pointer entry points ----------------
+
+int moty_hip_qrow_i8_dev(const float* x, int8_t* q, float* sx, int32_t* xg, int S, int I, void* stream) {
+  CUR(d);
+  if (S < 0 || I <= 0 || !x || !q || !sx) return set_error("qrow_i8: bad arguments"), MOTY_EINVAL;
+  return launch_qrow_i8(x, q, sx, xg, S, I, I, I, STREAM(stream));
+}
+
+int moty_hip_quantize_rows_dev(const float* w, int8_t* q, float* scale, int O, int I, int bits, void* stream) {
+  CUR(d);
+  if (O < 0 || I <= 0 || bits < 2 || bits > 8 || !w || !q || !scale)
+    return set_error("quantize_rows: bad arguments"), MOTY_EINVAL;
+  return launch_quantize_rows(w, q, scale, O, I, bits, STREAM(stream));
+}
+
+int moty_hip_pack_int4_grouped_dev(const float* w, uint8_t* q4, float* scale, int O, int I, int gs,
+                                   void* stream) {
+  CUR(d);
+  if (gs <= 0 || gs % 16) return set_error("pack_int4_grouped: gs=%d not a multiple of 16", gs), MOTY_EINVAL;
+  if (O < 0 || I <= 0 || !w || !q4 || !scale) return set_error("pack_int4_grouped: bad arguments"), MOTY_EINVAL;
+  return launch_pack_i4g(w, q4, scale, O, I, gs, STREAM(stream));
+}
+
+int moty_hip_matmul_q8_preq_dev(float* y, const int8_t* xq, const float* sx, const int8_t* q, const float* scale,
+                                int S, int I, int O, void* stream) {
+  CUR(d);
+  if (S < 0 || I <= 0 || O < 0) return set_error("matmul_q8_preq: bad shape"), MOTY_EINVAL;
+  int rc = launch_gemm_q8(xq, sx, q, scale, y, S, I, O, STREAM(stream));
+  if (rc == MOTY_EUNSUP) set_error("matmul_q8_preq: I=%d must be a multiple of 16", I);
+  return rc;
+}
+
+int moty_hip_matmul_q_s_dev(float* y, const float* x, const int8_t* q, const float* scale, int S, int I, int O,
+                            void* stream) {
+  CUR(d);
+  if (S < 0 || I <= 0 || O < 0 || !y || !x || !q || !scale) return set_error("matmul_q_s: bad arguments"), MOTY_EINVAL;
+  if (S == 0 || O == 0) return MOTY_OK;
+  if (I > 16384 || (I % 16)) {
+    set_error("matmul_q_s: I=%d unsupported (needs I %% 16 == 0, I <= 16384)", I);
+    return MOTY_EUNSUP;
+  }
+  hipStream_t st = STREAM(stream);
+  if (S <= GEMV_MAX_S) return launch_gemv_q8(x, q, scale, nullptr, nullptr, y, S, I, O, st);
+  void* sp;
+  const size_t xb = al256((size_t)S * I);
+  int rc = arena_get(d->scratch, xb + al256((size_t)S * 4), &sp);
+  if (rc) return rc;
+  int8_t* xq = (int8_t*)sp;
+  float* sx = (float*)((char*)sp + xb);
+  rc = launch_qrow_i8(x, xq, sx, nullptr, S, I, I, I, st);
+  if (rc) return rc;
+  return launch_gemm_q8(xq, sx, q, scale, y, S, I, O, st);
+}
+
+int moty_hip_matmul_i4_grouped_s_dev(float* y, const float* x, const uint8_t* q4, const float* scale, int S,
+                                     int I, int O, int gs, int idot4, void* stream) {
+  CUR(d);
+  if (S < 0 || I <= 0 || O < 0 || gs <= 0 || !y || !x || !q4 || !scale)
+    return set_error("matmul_i4_grouped_s: bad arguments"), MOTY_EINVAL;
+  if (S == 0 || O == 0) return MOTY_OK;
+  hipStream_t st = STREAM(stream);
+  if (idot4 && gs == 32 && (I % 64) == 0 && I <= 16384) {
+    if (S <= 4) return launch_gemv_i4g(x, q4, scale, y, S, I, O, st);
+    void* sp;
+    const size_t xb = al256((size_t)S * I);
+    int rc = arena_get(d->scratch, xb + al256((size_t)S * 4), &sp);
+    if (rc) return rc;
+    int8_t* xq = (int8_t*)sp;
+    float* sx = (float*)((char*)sp + xb);
+    rc = launch_qrow_i8(x, xq, sx, nullptr, S, I, I, I, st);
+    if (rc) return rc;
+    return launch_gemm_i4g(xq, sx, q4, scale, y, S, I, O, st);
+  }
+  if (gs == 32 && (I % 32) == 0) return launch_i4g_f32(x, q4, scale, y, S, I, O, st);
+  set_error("matmul_i4_grouped_s: gs=%d I=%d unsupported (exact path needs gs == 32, I %% 32 == 0)", gs, I);
+  return MOTY_EUNSUP;
+}
+
+int moty_hip_matmul_dev(float* y, const float* x, const float* W, int S, int I, int O, void* stream) {
+  CUR(d);
+  if (S < 0 || I <= 0 || O < 0 || !y || !x || !W) return set_error("matmul: bad arguments"), MOTY_EINVAL;
+  return launch_matmul_f32(x, W, y, S, I, O, STREAM(stream));
+}
+
+int moty_hip_silu_mul_dev(float* g, const float* u, int64_t n, void* stream) {
+  CUR(d);
+  if (n < 0 || !g || !u) return set_error("silu_mul: bad arguments"), MOTY_EINVAL;
+  return launch_silu_mul(g, u, n, STREAM(stream));
+}
+
+int moty_hip_softmax_rows_dev(float* x, int S, int n, void* stream) {
+  CUR(d);
+  if (S < 0 || n <= 0 || !x) return set_error("softmax_rows: bad arguments"), MOTY_EINVAL;
+  return launch_softmax_rows(x, S, n, STREAM(stream));
+}
+
+int moty_hip_expf_dev(const float* x, float* y, int64_t n, void* stream) {
+  CUR(d);
+  if (n < 0 || !x || !y) return set_error("expf: bad arguments"), MOTY_EINVAL;
+  return launch_expf(x, y, n, STREAM(stream));
+}
+
+int moty_hip_dense_ffn_q8_dev(float* out, const float* x, int S, const int8_t* gate, const float* gs,
+                              const int8_t* up, const float* us, const int8_t* down, const float* ds, int D, int I,
+                              void* stream) {
+  CUR(d);
+  if (S < 0 || D <= 0 || I <= 0) return set_error("dense_ffn_q8: bad shape"), MOTY_EINVAL;
+  if (S == 0) return MOTY_OK;
+  if ((D % 16) || (I % 16) || D > 16384 || I > 16384) {
+    set_error("dense_ffn_q8: D=%d I=%d unsupported", D, I);
+    return MOTY_EUNSUP;
+  }
+  hipStream_t st = STREAM(stream);
+  void* sp;
+  if (S <= GEMV_MAX_S) {
+    int rc = arena_get(d->scratch, al256((size_t)S * I * 4), &sp);
+    if (rc) return rc;
+    float* h = (float*)sp;
+    rc = launch_gemv_q8(x, gate, gs, up, us, h, S, D, I, st);
+    if (rc) return rc;
+    return launch_gemv_q8(h, down, ds, nullptr, nullptr, out, S, I, D, st);
+  }
+  const size_t b_xq = al256((size_t)S * (D > I ? D : I)), b_sx = al256((size_t)S * 4);
+  const size_t b_g = al256((size_t)S * I * 4);
+  int rc = arena_get(d->scratch, b_xq + b_sx + 2 * b_g, &sp);
+  if (rc) return rc;
+  int8_t* xq = (int8_t*)sp;
+  float* sx = (float*)((char*)sp + b_xq);
+  float* g = (float*)((char*)sp + b_xq + b_sx);
+  float* u = (float*)((char*)sp + b_xq + b_sx + b_g);
+  if ((rc = launch_qrow_i8(x, xq, sx, nullptr, S, D, D, D, st))) return rc;
+  if ((rc = launch_gemm_q8(xq, sx, gate, gs, g, S, D, I, st))) return rc;
+  if ((rc = launch_gemm_q8(xq, sx, up, us, u, S, D, I, st))) return rc;
+  if ((rc = launch_silu_mul(g, u, (int64_t)S * I, st))) return rc;
+  if ((rc = launch_qrow_i8(g, xq, sx, nullptr, S, I, I, I, st))) return rc;
+  return launch_gemm_q8(xq, sx, down, ds, out, S, I, D, st);
+}
+
+int moty_hip_moe_topk_dev(const MotyHipMoe* m, const float* x, int S, float* out, void* stream) {
+  CUR(d);
+  if (!m || !x || !out || S < 0) return set_error("moe_topk: bad arguments"), MOTY_EINVAL;
+  if (m->E <= 0 || m->K <= 0 || m->K > m->E || m->K > 64 || m->I <= 0 || m->D <= 0)
+    return set_error("moe_topk: bad shape E=%d K=%d I=%d D=%d", m->E, m->K, m->I, m->D), MOTY_EINVAL;
+  if (S == 0) return MOTY_OK;
+  if ((m->D % 32) || (m->I % 32) || m->E > 4096 || (size_t)(m->D + m->E) * 4 > 64 * 1024) {
+    set_error("moe_topk: D=%d I=%d E=%d unsupported (D, I multiples of 32)", m->D, m->I, m->E);
+    return MOTY_EUNSUP;
+  }
+  size_t offs[MOE_NBUF];
+  const size_t need = moe_scratch_size(S, m->D, m->E, m->K, m->I, offs);
+  void* sp;
+  int rc = arena_get(d->scratch, need, &sp);
+  if (rc) return rc;
+  MoeArgs a;
+  a.x = x;
+  a.Wr = m->router;
+  a.bias = m->logit_bias;
+  a.G = m->g;
+  a.U = m->u;
+  a.Dn = m->d;
+  a.GS = m->gs;
+  a.US = m->us;
+  a.DS = m->ds;
+  a.out = out;
+  a.T = S;
+  a.D = m->D;
+  a.E = m->E;
+  a.K = m->K;
+  a.I = m->I;
+  a.norm = m->norm_topk;
+  a.order = m->combine_order;
+  a.idx_out = m->idx_out;
+  a.w_out = m->w_out;
+  a.counts_out = m->counts_out;
+  a.probs_out = nullptr;
+  rc = launch_moe(a, sp, STREAM(stream));
+  if (rc == MOTY_EUNSUP) set_error("moe_topk: unsupported shape");
+  return rc;
+}
+
+// ---------------- host-pointer drop-ins ----------------
+
+// Stage host x into the transfer arena; returns device x and y pointers.
+static int stage_io(Dev* d, const void* x, size_t xbytes, size_t ybytes, void** dx, void** dy) {
+  void* p;
+  int rc = arena_get(d->io, al256(xbytes) + al256(ybytes), &p);
+  if (rc) return rc;
+  *dx = p;
+  *dy = (char*)p + al256(xbytes);
+  HIP_TRY(hipMemcpyAsync(*dx, x, xbytes, hipMemcpyHostToDevice, d->stream));
+  return MOTY_OK;
+}
+
+static int finish_io(Dev* d, void* y, const void* dy, size_t ybytes) {
+  HIP_TRY(hipMemcpyAsync(y, dy, ybytes, hipMemcpyDeviceToHost, d->stream));
+  HIP_TRY(hipStreamSynchronize(d->stream));
+  return MOTY_OK;
+}
+
+int moty_hip_matmul_q_s(float* y, const float* x, const int8_t* q, const float* scale, int S, int I, int O) {
+  CUR(d);
+  if (S < 0 || I <= 0 || O < 0 || !y || !x || !q || !scale) return set_error("matmul_q_s: bad arguments"), MOTY_EINVAL;
+  static const int idot = [] {
+    const char* e = getenv("IDOT");
+    return !(e && *e == '0');
+  }();
+  if (!idot) return set_error("matmul_q_s: IDOT=0 (f32 x int8) is served by the CPU path"), MOTY_EUNSUP;
+  if (S == 0 || O == 0) return MOTY_OK;
+  const void *dq, *ds;
+  int rc;
+  if ((rc = weight(d, q, (size_t)O * I, &dq))) return rc;
+  if ((rc = weight(d, scale, (size_t)O * 4, &ds))) return rc;
+  void *dx, *dy;
+  if ((rc = stage_io(d, x, (size_t)S * I * 4, (size_t)S * O * 4, &dx, &dy))) return rc;
+  if ((rc = moty_hip_matmul_q_s_dev((float*)dy, (const float*)dx, (const int8_t*)dq, (const float*)ds, S, I, O,
+                                    d->stream)))
+    return rc;
+  return finish_io(d, y, dy, (size_t)S * O * 4);
+}
+
+void moty_hip_hw_matmul_i8(float* y, const float* x, const int8_t* q, const float* scale, int S, int I, int O) {
+  (void)moty_hip_matmul_q_s(y, x, q, scale, S, I, O);
+}
+
+int moty_hip_matmul_i4_grouped_s(float* y, const float* x, const uint8_t* q4, const float* scale, int S, int I,
+                                 int O, int gs) {
+  CUR(d);
+  if (S < 0 || I <= 0 || O < 0 || gs <= 0 || !y || !x || !q4 || !scale)
+    return set_error("matmul_i4_grouped_s: bad arguments"), MOTY_EINVAL;
+  static const int idot4 = env_int("IDOT4", 0);
+  if (S == 0 || O == 0) return MOTY_OK;
+  const int ng = (I + gs - 1) / gs;
+  const void *dq, *ds;
+  int rc;
+  if ((rc = weight(d, q4, (size_t)O * ((I + 1) / 2), &dq))) return rc;
+  if ((rc = weight(d, scale, (size_t)O * ng * 4, &ds))) return rc;
+  void *dx, *dy;
+  if ((rc = stage_io(d, x, (size_t)S * I * 4, (size_t)S * O * 4, &dx, &dy))) return rc;
+  if ((rc = moty_hip_matmul_i4_grouped_s_dev((float*)dy, (const float*)dx, (const uint8_t*)dq, (const float*)ds, S,
+                                             I, O, gs, idot4, d->stream)))
+    return rc;
+  return finish_io(d, y, dy, (size_t)S * O * 4);
+}
+
+int moty_hip_matmul(float* y, const float* x, const float* W, int S, int I, int O) {
+  CUR(d);
+  if (S < 0 || I <= 0 || O < 0 || !y || !x || !W) return set_error("matmul: bad arguments"), MOTY_EINVAL;
+  if (S == 0 || O == 0) return MOTY_OK;
+  const void* dw;
+  int rc;
+  if ((rc = weight(d, W, (size_t)O * I * 4, &dw))) return rc;
+  void *dx, *dy;
+  if ((rc = stage_io(d, x, (size_t)S * I * 4, (size_t)S * O * 4, &dx, &dy))) return rc;
+  if ((rc = moty_hip_matmul_dev((float*)dy, (const float*)dx, (const float*)dw, S, I, O, d->stream))) return rc;
+  return finish_io(d, y, dy, (size_t)S * O * 4);
+}
+
+int moty_hip_moe_topk(const MotyHipMoe* m, const float* x, int S, float* out) {
+  CUR(d);
+  if (!m || !x || !out || S < 0 || m->E <= 0 || m->K <= 0 || m->I <= 0 || m->D <= 0)
+    return set_error("moe_topk: bad arguments"), MOTY_EINVAL;
+  if (S == 0) return MOTY_OK;
+  const int E = m->E, I = m->I, D = m->D, K = m->K;
+  const size_t ne = (size_t)E * I * D;
+  MotyHipMoe dm = *m;
+  const void* p;
+  int rc;
+  if ((rc = weight(d, m->router, (size_t)E * D * 4, &p))) return rc;
+  dm.router = (const float*)p;
+  if (m->logit_bias) {
+    if ((rc = weight(d, m->logit_bias, (size_t)E * 4, &p))) return rc;
+    dm.logit_bias = (const float*)p;
+  }
+  if ((rc = weight(d, m->g, ne, &p))) return rc;
+  dm.g = (const int8_t*)p;
+  if ((rc = weight(d, m->u, ne, &p))) return rc;
+  dm.u = (const int8_t*)p;
+  if ((rc = weight(d, m->d, ne, &p))) return rc;
+  dm.d = (const int8_t*)p;
+  if ((rc = weight(d, m->gs, (size_t)E * I * 4, &p))) return rc;
+  dm.gs = (const float*)p;
+  if ((rc = weight(d, m->us, (size_t)E * I * 4, &p))) return rc;
+  dm.us = (const float*)p;
+  if ((rc = weight(d, m->ds, (size_t)E * D * 4, &p))) return rc;
+  dm.ds = (const float*)p;
+  // outputs: out, then optional idx/w/counts after it in the transfer arena
+  const size_t b_out = al256((size_t)S * D * 4), b_kw = al256((size_t)S * K * 4), b_c = al256((size_t)E * 4);
+  void *dx, *dy;
+  if ((rc = stage_io(d, x, (size_t)S * D * 4, b_out + 2 * b_kw + b_c, &dx, &dy))) return rc;
+  char* extra = (char*)dy + b_out;
+  dm.idx_out = m->idx_out ? (int32_t*)extra : nullptr;
+  dm.w_out = m->w_out ? (float*)(extra + b_kw) : nullptr;
+  dm.counts_out = m->counts_out ? (int32_t*)(extra + 2 * b_kw) : nullptr;
+  if ((rc = moty_hip_moe_topk_dev(&dm, (const float*)dx, S, (float*)dy, d->stream))) return rc;
+  if (m->idx_out) HIP_TRY(hipMemcpyAsync(m->idx_out, dm.idx_out, (size_t)S * K * 4, hipMemcpyDeviceToHost, d->stream));
+  if (m->w_out) HIP_TRY(hipMemcpyAsync(m->w_out, dm.w_out, (size_t)S * K * 4, hipMemcpyDeviceToHost, d->stream));
+  if (m->counts_out)
+    HIP_TRY(hipMemcpyAsync(m->counts_out, dm.counts_out, (size_t)E * 4, hipMemcpyDeviceToHost, d->stream));
+  return finish_io(d, out, dy, (size_t)S * D * 4);
+}
+
+int moty_hip_weight_forget(const void* host_ptr) {
+  CUR(d);
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = d->wcache.find(host_ptr);
+  if (it == d->wcache.end()) return MOTY_OK;
+  HIP_TRY(hipStreamSynchronize(d->stream));
+  HIP_TRY(hipFree(it->second.dev));
+  d->wcache.erase(it);
+  return MOTY_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,172 @@
+// common.h -- shared device helpers for libmoty-hw-hip (gfx950, wave64).
+//
+// Everything in this library is compiled with -ffp-contract=off: every FMA
+// is written explicitly where the reference's x86-64 build forms one, so
+// the float results match the reference bit for bit.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define MOTY_WAVE 64
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// ---------------------------------------------------------------------------
+// expf, bit-identical to glibc 2.35 expf on x86-64 (hw/hw_ops.h:20 calls it).
+// Method: ARM optimized-routines expf (Szabolcs Nagy), as glibc builds it with
+// FMA contraction: k = round(x*32/ln2), r = x*32/ln2 - k,
+// exp(x) = 2^(k/32) * (1 + C2 r + C1 r^2 + C0 r^3) in double, rounded once
+// to float.  T2[i] = bits(2^(i/32)) - (i << 47).  The same steps, checked on
+// every one of the 2^32 float inputs against libm, are the test oracle.
+__constant__ static const uint64_t kExp2Tab[32] = {
+    0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
+    0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL,
+    0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,
+    0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL, 0x3feea47eb03a5585ULL,
+    0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL, 0x3feea11473eb0187ULL, 0x3feea589994cce13ULL,
+    0x3feeace5422aa0dbULL, 0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL,
+    0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
+    0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL};
+
+__device__ __forceinline__ float ref_expf(float x) {
+  const double kC0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+  const double kC1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+  const double kC2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+  const double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
+  const double kShift = 0x1.8p+52;
+  uint32_t ux = __float_as_uint(x);
+  uint32_t abstop = (ux >> 20) & 0x7ff;
+  if (abstop >= 0x42b) {                 // |x| >= 88, inf or nan
+    if (ux == 0xff800000u) return 0.f;   // -inf
+    if (abstop >= 0x7f8) return x + x;   // inf / nan
+    if (x > 0x1.62e42ep6f) return __builtin_inff();
+    if (x < -0x1.9fe368p6f) return 0.f;
+  }
+  double xd = (double)x;
+  double kd = __fma_rn(kInvLn2N, xd, kShift);
+  uint64_t ki = (uint64_t)__double_as_longlong(kd);
+  kd = kd - kShift;
+  double r = __fma_rn(kInvLn2N, xd, -kd);
+  uint64_t t = kExp2Tab[ki & 31] + (ki << 47);
+  double s = __longlong_as_double((long long)t);
+  double z = __fma_rn(kC0, r, kC1);
+  double r2 = r * r;
+  double y = __fma_rn(kC2, r, 1.0);
+  y = __fma_rn(z, r2, y);
+  y = y * s;
+  return (float)y;
+}
+
+// g / (1 + expf(-g)) * u  (hw/hw_ops.h:19-21); division correctly rounded.
+__device__ __forceinline__ float ref_silu_mul(float g, float u) {
+  return (g / (1.f + ref_expf(-g))) * u;
+}
+
+// lrintf under the default round-to-nearest-even mode, as an int.
+__device__ __forceinline__ int rne_int(float v) { return (int)__builtin_rintf(v); }
+
+// ---------------------------------------------------------------------------
+// wave64 reductions
+__device__ __forceinline__ int wave_sum_i32(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// 4 signed int8 x 4 signed int8 -> int32 accumulate (v_dot4_i32_i8)
+__device__ __forceinline__ int dot4(int a, int b, int c) {
+  return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+__device__ __forceinline__ int dot16(const int4 a, const int4 b, int c) {
+  c = dot4(a.x, b.x, c);
+  c = dot4(a.y, b.y, c);
+  c = dot4(a.z, b.z, c);
+  c = dot4(a.w, b.w, c);
+  return c;
+}
+
+// 8 packed int4 bytes (16 nibbles, even element in the low nibble, value
+// n in 0..15 standing for n-8) -> 16 signed int8 (n-8) in element order.
+__device__ __forceinline__ uint32_t nib_lo_bytes(uint32_t w) {
+  // w holds 4 packed bytes b0..b3 = elements 0..7; returns elements 0..3
+  // as bytes (n-8): byte j = nibble j of the little-endian stream.
+  uint32_t b0 = w & 0xffu, b1 = (w >> 8) & 0xffu;
+  uint32_t r = (b0 & 0xfu) | ((b0 >> 4) << 8) | ((b1 & 0xfu) << 16) | ((b1 >> 4) << 24);
+  return r;
+}
+__device__ __forceinline__ uint32_t nib_signed(uint32_t t) {
+  // per byte n in 0..15 -> (n-8) as int8: n^8 then sign-extend bit 3
+  t ^= 0x08080808u;
+  return t | ((t & 0x08080808u) * 0x1Eu);
+}
+__device__ __forceinline__ int4 unpack_nib16(uint2 w) {
+  int4 r;
+  r.x = (int)nib_signed(nib_lo_bytes(w.x));
+  r.y = (int)nib_signed(nib_lo_bytes(w.x >> 16));
+  r.z = (int)nib_signed(nib_lo_bytes(w.y));
+  r.w = (int)nib_signed(nib_lo_bytes(w.y >> 16));
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// 16-lane horizontal sum with gcc's _mm512_reduce_add_ps association:
+// v[j+8]+v[j], then [j+4]+[j], then (b0+b2)+(b1+b3).  `v` is lane c's value
+// for c in 0..15 of a 32-lane half (lanes 16..31 unused).  Returns the sum
+// in every lane of the half.
+__device__ __forceinline__ float hsum16_half(float v, int base) {
+  const int c = threadIdx.x % 32;
+  float a = __shfl(v, base + ((c + 8) & 15), 64) + v;  // valid for c < 8
+  float b = __shfl(a, base + ((c + 4) & 7), 64) + a;   // valid for c < 4
+  float b2 = __shfl(b, base + 2, 64), b0 = __shfl(b, base + 0, 64);
+  float b3 = __shfl(b, base + 3, 64), b1 = __shfl(b, base + 1, 64);
+  return (b0 + b2) + (b1 + b3);
+}
+
+// exact dot_f32 (AVX512 order) of x (LDS) with W row (global), computed by a
+// 32-lane half-wave; returns the dot in every lane of the half.
+__device__ __forceinline__ float dot_f32_half(const float* __restrict__ xs, const float* __restrict__ wr, int n) {
+  const int c = threadIdx.x % 32;
+  const int base = (threadIdx.x % MOTY_WAVE) & 32;
+  float s = 0.f;  // chain c: s0[c] for c < 16, s1[c-16] for c >= 16
+  int i = 0;
+  for (; i + 32 <= n; i += 32) s = __fmaf_rn(xs[i + c], wr[i + c], s);
+  if (i + 16 <= n) {
+    if (c < 16) s = __fmaf_rn(xs[i + c], wr[i + c], s);
+    i += 16;
+  }
+  const float t = s + __shfl(s, base + ((c + 16) & 31), 64);  // s0[c] + s1[c]
+  float r = hsum16_half(t, base);
+  for (; i < n; i++) r = __fmaf_rn(xs[i], wr[i], r);
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// host-side plumbing shared by the translation units
+namespace moty {
+void set_error(const char* fmt, ...);
+int check_hip(hipError_t e, const char* what);
+}  // namespace moty
+
+#define MOTY_OK 0
+#define MOTY_EINVAL 1   // bad argument / shape
+#define MOTY_EHIP 2     // HIP runtime error
+#define MOTY_ENOMEM 3   // device allocation failed
+#define MOTY_EUNSUP 4   // shape/format not supported by this backend
+
+#define HIP_TRY(call)                                           \
+  do {                                                          \
+    hipError_t _e = (call);                                     \
+    if (_e != hipSuccess) return moty::check_hip(_e, #call);    \
+  } while (0)
+
+#define LAUNCH_TRY(what)                                        \
+  do {                                                          \
+    hipError_t _e = hipGetLastError();                          \
+    if (_e != hipSuccess) return moty::check_hip(_e, what);     \
+  } while (0)

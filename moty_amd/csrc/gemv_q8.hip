@@ -1,0 +1,177 @@
+// gemv_q8.hip -- Q8_0 GEMV for decode (S <= 4 token rows).
+//
+// Reference: moty_matmul_q_s (nn/matmul.c:51-66) -> q8_idot_rows (:29-36)
+// -> dot_i8i8 (hw/hw_avx512.h:24-54):
+//     xq[s] = qrow_i8(x[s]);  y[s*O+o] = (scale[o]*sx[s]) * (float)dot(W[o], xq[s])
+//
+// MI355X design (HBM-bound, one pass over W):
+//  * a wave owns RPW weight rows; each lane streams 16 contiguous bytes per
+//    1 KiB chunk of a row (global_load_dwordx4, fully coalesced), up to four
+//    chunks per row in flight;
+//  * the block issues its first weight loads, then quantizes the S
+//    activation rows into LDS while those loads are in flight (every block
+//    re-derives the same int8 activations: the quantization is a pure
+//    function of x, so this is bit-identical to quantizing once);
+//  * int8 dot products on v_dot4_i32_i8, int32 wave reduction (exact);
+//  * epilogue: (scale*sx)*float(acc), two plain multiplies, as the reference.
+// PAIR mode (decode FFN gate+up): the wave reads row o of W and of W2 and
+// writes silu(g)*u (hw/hw_ops.h:19-21) -- the SwiGLU of nn/ffn.c:26-55.
+#include "common.h"
+#include "kernels.h"
+
+namespace moty {
+
+constexpr int GEMV_NT = 256;
+constexpr int GEMV_WAVES = GEMV_NT / MOTY_WAVE;
+constexpr int CHUNK = 16 * MOTY_WAVE;  // bytes of a row one wave-load covers
+constexpr int CB = 4;                  // chunks in flight per row
+
+template <int S_, int RPW, bool PAIR>
+__global__ __launch_bounds__(GEMV_NT) void k_gemv_q8(const float* __restrict__ x, const int8_t* __restrict__ W,
+                                                     const float* __restrict__ scale,
+                                                     const int8_t* __restrict__ W2,
+                                                     const float* __restrict__ scale2, float* __restrict__ y,
+                                                     int I, int O) {
+  extern __shared__ __align__(16) int8_t xq_s[];  // [S_][Ipad]
+  __shared__ float red[GEMV_WAVES][S_];
+  __shared__ float sx_s[S_];
+  const int lane = threadIdx.x % MOTY_WAVE, wv = threadIdx.x / MOTY_WAVE;
+  const int Ipad = (I + CHUNK - 1) / CHUNK * CHUNK;
+  const int nch = Ipad / CHUNK;
+  const int o0 = (blockIdx.x * GEMV_WAVES + wv) * RPW;
+
+  int acc[RPW][S_];
+  int acc2[RPW][S_];
+#pragma unroll
+  for (int r = 0; r < RPW; r++)
+#pragma unroll
+    for (int s = 0; s < S_; s++) acc[r][s] = acc2[r][s] = 0;
+
+  for (int cb = 0; cb < nch; cb += CB) {
+    int4 wq[RPW][CB], wq2[RPW][CB];
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+      const int o = o0 + r;
+#pragma unroll
+      for (int j = 0; j < CB; j++) {
+        const int k = (cb + j) * CHUNK + lane * 16;
+        const bool ok = (o < O) && (cb + j < nch) && (k < I);
+        wq[r][j] = ok ? *(const int4*)(W + (int64_t)o * I + k) : int4{0, 0, 0, 0};
+        if (PAIR) wq2[r][j] = ok ? *(const int4*)(W2 + (int64_t)o * I + k) : int4{0, 0, 0, 0};
+      }
+    }
+    if (cb == 0) {
+      // quantize the activation rows into LDS while the loads above fly
+#pragma unroll
+      for (int s = 0; s < S_; s++) {
+        const float* xr = x + (int64_t)s * I;
+        float amax = 0.f;
+        for (int i = threadIdx.x * 4; i < I; i += GEMV_NT * 4) {
+          float4 v = *(const float4*)(xr + i);
+          amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+        amax = wave_max_f32(amax);
+        if (lane == 0) red[wv][s] = amax;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int s = 0; s < S_; s++) {
+        float amax = red[0][s];
+#pragma unroll
+        for (int i = 1; i < GEMV_WAVES; i++) amax = fmaxf(amax, red[i][s]);
+        float sc = amax / 127.f;
+        if (sc < 1e-12f) sc = 1e-12f;
+        const float inv = 1.f / sc;
+        if (threadIdx.x == 0) sx_s[s] = sc;
+        const float* xr = x + (int64_t)s * I;
+        for (int i = threadIdx.x * 4; i < Ipad; i += GEMV_NT * 4) {
+          uint32_t p = 0;
+          if (i < I) {
+            float4 v = *(const float4*)(xr + i);
+            p = (uint32_t)(rne_int(v.x * inv) & 0xff) | ((uint32_t)(rne_int(v.y * inv) & 0xff) << 8) |
+                ((uint32_t)(rne_int(v.z * inv) & 0xff) << 16) | ((uint32_t)(rne_int(v.w * inv) & 0xff) << 24);
+          }
+          *(uint32_t*)(xq_s + s * Ipad + i) = p;
+        }
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < CB; j++) {
+      if (cb + j >= nch) break;
+#pragma unroll
+      for (int s = 0; s < S_; s++) {
+        const int4 xv = *(const int4*)(xq_s + s * Ipad + (cb + j) * CHUNK + lane * 16);
+#pragma unroll
+        for (int r = 0; r < RPW; r++) {
+          acc[r][s] = dot16(wq[r][j], xv, acc[r][s]);
+          if (PAIR) acc2[r][s] = dot16(wq2[r][j], xv, acc2[r][s]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RPW; r++)
+#pragma unroll
+    for (int s = 0; s < S_; s++) {
+      acc[r][s] = wave_sum_i32(acc[r][s]);
+      if (PAIR) acc2[r][s] = wave_sum_i32(acc2[r][s]);
+    }
+  // lane (r*S_ + s) writes element (r, s)
+#pragma unroll
+  for (int r = 0; r < RPW; r++)
+#pragma unroll
+    for (int s = 0; s < S_; s++) {
+      const int o = o0 + r;
+      if (lane == r * S_ + s && o < O) {
+        const float sxv = sx_s[s];
+        float v = (scale[o] * sxv) * (float)acc[r][s];
+        if (PAIR) {
+          const float u = (scale2[o] * sxv) * (float)acc2[r][s];
+          v = ref_silu_mul(v, u);
+        }
+        y[(int64_t)s * O + o] = v;
+      }
+    }
+}
+
+template <int S_, bool PAIR>
+static int launch_s(const float* x, const int8_t* W, const float* scale, const int8_t* W2, const float* scale2,
+                    float* y, int S, int I, int O, hipStream_t st) {
+  const int Ipad = (I + CHUNK - 1) / CHUNK * CHUNK;
+  const size_t lds = (size_t)S_ * Ipad;
+  // rows per wave: keep >= ~2 blocks per CU on the 256-CU part
+  const int rpw = (O >= 32768) ? 4 : (O >= 8192 ? 2 : 1);
+  auto go = [&](auto kern, int r) {
+    const int rows_per_block = GEMV_WAVES * r;
+    const unsigned nb = (unsigned)((O + rows_per_block - 1) / rows_per_block);
+    hipLaunchKernelGGL(kern, dim3(nb), dim3(GEMV_NT), lds, st, x, W, scale, W2, scale2, y, I, O);
+  };
+  if (rpw == 4) go(k_gemv_q8<S_, 4, PAIR>, 4);
+  else if (rpw == 2) go(k_gemv_q8<S_, 2, PAIR>, 2);
+  else go(k_gemv_q8<S_, 1, PAIR>, 1);
+  LAUNCH_TRY("k_gemv_q8");
+  return MOTY_OK;
+}
+
+// y [S][O] = Q8 GEMV of x [S][I]; PAIR: y = silu(x.W^T) * (x.W2^T)
+int launch_gemv_q8(const float* x, const int8_t* W, const float* scale, const int8_t* W2, const float* scale2,
+                   float* y, int S, int I, int O, hipStream_t st) {
+  if (S < 1 || S > GEMV_MAX_S || (I % 16) || I > 16384) return MOTY_EUNSUP;
+  if (O <= 0) return MOTY_OK;
+  const bool pair = (W2 != nullptr);
+#define CASE(n)                                                                              \
+  case n:                                                                                    \
+    return pair ? launch_s<n, true>(x, W, scale, W2, scale2, y, S, I, O, st)                 \
+                : launch_s<n, false>(x, W, scale, W2, scale2, y, S, I, O, st);
+  switch (S) {
+    CASE(1)
+    CASE(2)
+    CASE(3)
+    CASE(4)
+  }
+#undef CASE
+  return MOTY_EUNSUP;
+}
+
+}  // namespace moty

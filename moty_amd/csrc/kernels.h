@@ -1,0 +1,54 @@
+// kernels.h -- launchers shared between the kernel translation units and the
+// C-ABI layer (api.cpp).  Every launcher is asynchronous on `st` and returns
+// MOTY_OK or an error code; none allocates.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace moty {
+
+constexpr int GEMV_MAX_S = 4;  // token rows served by the decode GEMVs
+constexpr int MOE_BM = 32;     // slots per M-tile of the grouped MoE GEMMs
+constexpr int MOE_NBUF = 14;   // MoE scratch sub-buffers
+
+int launch_qrow_i8(const float* x, int8_t* q, float* sx, int32_t* xg, int S, int I, int64_t ldx, int64_t ldq,
+                   hipStream_t st);
+int launch_quantize_rows(const float* w, int8_t* q, float* scale, int O, int I, int bits, hipStream_t st);
+int launch_pack_i4g(const float* w, uint8_t* q4, float* scale, int O, int I, int gs, hipStream_t st);
+
+int launch_gemv_q8(const float* x, const int8_t* W, const float* scale, const int8_t* W2, const float* scale2,
+                   float* y, int S, int I, int O, hipStream_t st);
+int launch_gemm_q8(const int8_t* xq, const float* sx, const int8_t* W, const float* scale, float* y, int M, int K,
+                   int O, hipStream_t st);
+
+int launch_gemv_i4g(const float* x, const uint8_t* q4, const float* scl, float* y, int S, int I, int O,
+                    hipStream_t st);
+int launch_gemm_i4g(const int8_t* xq, const float* sx, const uint8_t* q4, const float* scl, float* y, int M, int I,
+                    int O, hipStream_t st);
+int launch_i4g_f32(const float* x, const uint8_t* q4, const float* scl, float* y, int S, int I, int O,
+                   hipStream_t st);
+
+int launch_matmul_f32(const float* x, const float* W, float* y, int S, int I, int O, hipStream_t st);
+int launch_silu_mul(float* g, const float* u, int64_t n, hipStream_t st);
+int launch_expf(const float* x, float* y, int64_t n, hipStream_t st);
+int launch_softmax_rows(float* x, int S, int n, hipStream_t st);
+
+struct MoeArgs {
+  const float* x;
+  const float* Wr;
+  const float* bias;
+  const int8_t *G, *U, *Dn;
+  const float *GS, *US, *DS;
+  float* out;
+  int T, D, E, K, I;
+  int norm, order;
+  int* idx_out;
+  float* w_out;
+  int* counts_out;
+  float* probs_out;
+};
+size_t moe_scratch_size(int T, int D, int E, int K, int I, size_t* offsets);
+int launch_moe(const MoeArgs& a, void* scratch, hipStream_t st);
+
+}  // namespace moty

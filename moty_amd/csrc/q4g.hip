@@ -1,0 +1,241 @@
+// q4g.hip -- grouped int4 (group 32, f32 group scales) GEMV/GEMM.
+//
+// Reference: moty_matmul_i4_grouped_s (nn/matmul.c:164-197).
+//  IDOT4=1 (gs == 32, I % 64 == 0):  xq = qrow_i8(x), then per output
+//    acc = 0; for g ascending: acc = fma(scl[o][g], (float)(d_g - 8*xg_g), acc)
+//    y = sx * acc                      (hw/hw_avx512.h:155-176, matmul.c:148-160)
+//  default (exact f32 activations):  per group
+//    t[j] = fma(x[j], w[j], x[j+16]*w[j+16]), j < 16; r = hsum16(t);
+//    a = fma(r, scl[o][g], a)           (nn/matmul.c:199-253)
+//
+// The integer group dot d_g - 8*xg_g equals sum (n-8)*x exactly, so the
+// kernels expand nibbles straight to signed int8 (n-8) and never need the
+// group sums xg.  Group scales multiply a float chain whose order is fixed,
+// so each output's chain runs in ascending group order in one lane.
+#include "common.h"
+#include "kernels.h"
+
+namespace moty {
+
+// ---------------------------------------------------------------------------
+// IDOT4 GEMV, S <= 4.  Workgroup: 4 waves, RB rows.  Per 64-group chunk:
+// phase 1 -- every lane computes one group's integer dot for each token
+// (16 B of nibbles, coalesced) and parks it with the group scale in LDS;
+// phase 2 -- one lane per (row, token) extends its FMA chain over the chunk's
+// 64 groups in order.  Activations are quantized into LDS at the start.
+constexpr int Q4V_NT = 256;
+constexpr int Q4V_ROWS = 16;  // rows per workgroup
+
+template <int S_>
+__global__ __launch_bounds__(Q4V_NT) void k_gemv_i4g(const float* __restrict__ x, const uint8_t* __restrict__ q4,
+                                                     const float* __restrict__ scl, float* __restrict__ y, int I,
+                                                     int O) {
+  extern __shared__ __align__(16) int8_t xq_s[];  // [S_][I]
+  __shared__ int dv[Q4V_ROWS][S_][65];
+  __shared__ float sv[Q4V_ROWS][65];
+  __shared__ float red[Q4V_NT / MOTY_WAVE][S_];
+  __shared__ float sx_s[S_];
+  const int lane = threadIdx.x % MOTY_WAVE, wv = threadIdx.x / MOTY_WAVE;
+  const int ng = I / 32, rb = I / 2;
+  const int ob = blockIdx.x * Q4V_ROWS;
+  // activation quantization (qrow_i8) into LDS
+#pragma unroll
+  for (int s = 0; s < S_; s++) {
+    float amax = 0.f;
+    for (int i = threadIdx.x * 4; i < I; i += Q4V_NT * 4) {
+      const float4 v = *(const float4*)(x + (int64_t)s * I + i);
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    amax = wave_max_f32(amax);
+    if (lane == 0) red[wv][s] = amax;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int s = 0; s < S_; s++) {
+    float amax = red[0][s];
+    for (int i = 1; i < Q4V_NT / MOTY_WAVE; i++) amax = fmaxf(amax, red[i][s]);
+    float sc = amax / 127.f;
+    if (sc < 1e-12f) sc = 1e-12f;
+    const float inv = 1.f / sc;
+    if (threadIdx.x == 0) sx_s[s] = sc;
+    for (int i = threadIdx.x * 4; i < I; i += Q4V_NT * 4) {
+      const float4 v = *(const float4*)(x + (int64_t)s * I + i);
+      const uint32_t p = (uint32_t)(rne_int(v.x * inv) & 0xff) | ((uint32_t)(rne_int(v.y * inv) & 0xff) << 8) |
+                         ((uint32_t)(rne_int(v.z * inv) & 0xff) << 16) |
+                         ((uint32_t)(rne_int(v.w * inv) & 0xff) << 24);
+      *(uint32_t*)(xq_s + s * I + i) = p;
+    }
+  }
+  __syncthreads();
+  float acc = 0.f;  // chain of lane j = r*S_ + s (j < Q4V_ROWS*S_)
+  const int cr = threadIdx.x / S_, cs = threadIdx.x % S_;
+  for (int c0 = 0; c0 < ng; c0 += 64) {
+    const int g = c0 + lane;
+    for (int r = wv; r < Q4V_ROWS; r += Q4V_NT / MOTY_WAVE) {
+      const int o = ob + r;
+      const bool ok = (o < O) && (g < ng);
+      const int4 wb = ok ? *(const int4*)(q4 + (int64_t)o * rb + g * 16) : int4{0, 0, 0, 0};
+      const float sc = ok ? scl[(int64_t)o * ng + g] : 0.f;
+      const int4 w0 = unpack_nib16(uint2{(uint32_t)wb.x, (uint32_t)wb.y});
+      const int4 w1 = unpack_nib16(uint2{(uint32_t)wb.z, (uint32_t)wb.w});
+#pragma unroll
+      for (int s = 0; s < S_; s++) {
+        int d = 0;
+        if (g < ng) {
+          const int4 x0 = *(const int4*)(xq_s + s * I + g * 32);
+          const int4 x1 = *(const int4*)(xq_s + s * I + g * 32 + 16);
+          d = dot16(w0, x0, 0);
+          d = dot16(w1, x1, d);
+        }
+        dv[r][s][lane] = d;
+      }
+      sv[r][lane] = sc;
+    }
+    __syncthreads();
+    if (threadIdx.x < Q4V_ROWS * S_) {
+      const int n = (ng - c0) < 64 ? (ng - c0) : 64;
+      for (int j = 0; j < n; j++) acc = __fmaf_rn(sv[cr][j], (float)dv[cr][cs][j], acc);
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x < Q4V_ROWS * S_) {
+    const int o = ob + cr;
+    if (o < O) y[(int64_t)cs * O + o] = sx_s[cs] * acc;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// IDOT4 GEMM on v_mfma_i32_32x32x32_i8: one MFMA per group (K = 32 exactly),
+// so each group's integer dot comes out separately and is folded into a
+// float accumulator per output, in group order:
+//     accf = fma(scl[o][g], (float)d, accf)
+// Lane l holds weight row (l % 32) -- one scale per lane per group.
+// Workgroup: 4 waves as 2 (tokens) x 2 (rows), block tile 64 x 64.
+constexpr int Q4M_NT = 256;
+
+__global__ __launch_bounds__(Q4M_NT) void k_gemm_i4g(const int8_t* __restrict__ xq, const float* __restrict__ sx,
+                                                     const uint8_t* __restrict__ q4,
+                                                     const float* __restrict__ scl, float* __restrict__ y, int M,
+                                                     int I, int O) {
+  const int lane = threadIdx.x % MOTY_WAVE, wv = threadIdx.x / MOTY_WAVE;
+  const int m0 = blockIdx.y * 64 + (wv >> 1) * 32;
+  const int n0 = blockIdx.x * 64 + (wv & 1) * 32;
+  const int r32 = lane & 31, hk = lane >> 5;
+  const int ng = I / 32, rb = I / 2;
+  int m = m0 + r32;
+  m = m < M ? m : M - 1;
+  int n = n0 + r32;
+  n = n < O ? n : O - 1;
+  const int8_t* ap = xq + (int64_t)m * I + hk * 16;
+  const uint8_t* bp = q4 + (int64_t)n * rb + hk * 8;
+  const float* sp = scl + (int64_t)n * ng;
+  float accf[16];
+#pragma unroll
+  for (int r = 0; r < 16; r++) accf[r] = 0.f;
+  int4 a = *(const int4*)ap;
+  uint2 b = *(const uint2*)bp;
+  float sc = sp[0];
+  for (int g = 0; g < ng; g++) {
+    int4 an = a;
+    uint2 bn = b;
+    float scn = sc;
+    if (g + 1 < ng) {
+      an = *(const int4*)(ap + (g + 1) * 32);
+      bn = *(const uint2*)(bp + (g + 1) * 16);
+      scn = sp[g + 1];
+    }
+    const int4 w = unpack_nib16(b);
+    v16i d = {};
+    d = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(v4i*)&a, *(const v4i*)&w, d, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 16; r++) accf[r] = __fmaf_rn(sc, (float)d[r], accf[r]);
+    a = an;
+    b = bn;
+    sc = scn;
+  }
+  const int col = n0 + r32;
+  if (col >= O) return;
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    const int row = m0 + 8 * (r >> 2) + 4 * hk + (r & 3);
+    if (row < M) y[(int64_t)row * O + col] = sx[row] * accf[r];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Exact f32 path, any S: one lane per (row, token); x rows staged in LDS.
+constexpr int Q4F_NT = 256;
+
+__global__ __launch_bounds__(Q4F_NT) void k_i4g_f32(const float* __restrict__ x, const uint8_t* __restrict__ q4,
+                                                    const float* __restrict__ scl, float* __restrict__ y, int S,
+                                                    int I, int O) {
+  const int s = blockIdx.y;
+  const int o = blockIdx.x * Q4F_NT + threadIdx.x;
+  if (o >= O) return;
+  const int ng = I / 32, rb = I / 2;
+  const float* xs = x + (int64_t)s * I;
+  const uint8_t* w = q4 + (int64_t)o * rb;
+  const float* sp = scl + (int64_t)o * ng;
+  float a = 0.f;
+  for (int g = 0; g < ng; g++) {
+    const int4 wb = *(const int4*)(w + g * 16);
+    const uint32_t wd[4] = {(uint32_t)wb.x, (uint32_t)wb.y, (uint32_t)wb.z, (uint32_t)wb.w};
+    float t[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      // element j (bytes 0..7) and element 16+j (bytes 8..15)
+      const uint32_t b0 = (wd[j >> 3] >> (8 * ((j >> 1) & 3))) & 0xffu;
+      const uint32_t b1 = (wd[2 + (j >> 3)] >> (8 * ((j >> 1) & 3))) & 0xffu;
+      const int n0 = (j & 1) ? (int)(b0 >> 4) : (int)(b0 & 0xf);
+      const int n1 = (j & 1) ? (int)(b1 >> 4) : (int)(b1 & 0xf);
+      const float p1 = xs[g * 32 + 16 + j] * (float)(n1 - 8);
+      t[j] = __fmaf_rn(xs[g * 32 + j], (float)(n0 - 8), p1);
+    }
+    float u[8], v[4];
+#pragma unroll
+    for (int j = 0; j < 8; j++) u[j] = t[j + 8] + t[j];
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] = u[j + 4] + u[j];
+    const float r = (v[0] + v[2]) + (v[1] + v[3]);
+    a = __fmaf_rn(r, sp[g], a);
+  }
+  y[(int64_t)s * O + o] = a;
+}
+
+int launch_gemv_i4g(const float* x, const uint8_t* q4, const float* scl, float* y, int S, int I, int O,
+                    hipStream_t st) {
+  if (S < 1 || S > 4 || (I % 64) || I > 16384) return MOTY_EUNSUP;
+  if (O <= 0) return MOTY_OK;
+  const unsigned nb = (unsigned)((O + Q4V_ROWS - 1) / Q4V_ROWS);
+  const size_t lds = (size_t)S * I;
+  switch (S) {
+    case 1: hipLaunchKernelGGL(k_gemv_i4g<1>, dim3(nb), dim3(Q4V_NT), lds, st, x, q4, scl, y, I, O); break;
+    case 2: hipLaunchKernelGGL(k_gemv_i4g<2>, dim3(nb), dim3(Q4V_NT), lds, st, x, q4, scl, y, I, O); break;
+    case 3: hipLaunchKernelGGL(k_gemv_i4g<3>, dim3(nb), dim3(Q4V_NT), lds, st, x, q4, scl, y, I, O); break;
+    default: hipLaunchKernelGGL(k_gemv_i4g<4>, dim3(nb), dim3(Q4V_NT), lds, st, x, q4, scl, y, I, O); break;
+  }
+  LAUNCH_TRY("k_gemv_i4g");
+  return MOTY_OK;
+}
+
+int launch_gemm_i4g(const int8_t* xq, const float* sx, const uint8_t* q4, const float* scl, float* y, int M,
+                    int I, int O, hipStream_t st) {
+  if (I % 64) return MOTY_EUNSUP;
+  if (M <= 0 || O <= 0) return MOTY_OK;
+  dim3 grid((O + 63) / 64, (M + 63) / 64);
+  hipLaunchKernelGGL(k_gemm_i4g, grid, dim3(Q4M_NT), 0, st, xq, sx, q4, scl, y, M, I, O);
+  LAUNCH_TRY("k_gemm_i4g");
+  return MOTY_OK;
+}
+
+int launch_i4g_f32(const float* x, const uint8_t* q4, const float* scl, float* y, int S, int I, int O,
+                   hipStream_t st) {
+  if (I % 32) return MOTY_EUNSUP;
+  if (S <= 0 || O <= 0) return MOTY_OK;
+  dim3 grid((O + Q4F_NT - 1) / Q4F_NT, S);
+  hipLaunchKernelGGL(k_i4g_f32, grid, dim3(Q4F_NT), 0, st, x, q4, scl, y, S, I, O);
+  LAUNCH_TRY("k_i4g_f32");
+  return MOTY_OK;
+}
+
+}  // namespace moty

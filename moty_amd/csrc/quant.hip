@@ -1,0 +1,160 @@
+// quant.hip -- activation and weight quantization kernels.
+//
+//  k_qrow_i8        per-row symmetric int8 activations  (hw/hw_quant.h:9-16)
+//  k_quantize_rows  per-row int8 weights, division by s (nn/quant.c:12-33)
+//  k_pack_i4g       group-32 int4 weights + f32 scales  (nn/quant.c:57-83)
+//
+// All three are HBM-streaming kernels: one workgroup per row, a max
+// reduction (order-free, exact), then one rounding pass.  The float steps
+// are the reference's: s = amax/127.f (correctly rounded divide),
+// clamp, inv = 1.f/s, q = rint(x*inv); weights use w/s per element.
+#include "common.h"
+#include "kernels.h"
+
+namespace moty {
+
+template <int NT>
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = wave_max_f32(v);
+  const int w = threadIdx.x / MOTY_WAVE, l = threadIdx.x % MOTY_WAVE;
+  if (l == 0) red[w] = v;
+  __syncthreads();
+  float m = red[0];
+#pragma unroll
+  for (int i = 1; i < NT / MOTY_WAVE; i++) m = fmaxf(m, red[i]);
+  __syncthreads();
+  return m;
+}
+
+// One workgroup per row.  x [S][I] f32 -> q [S][I] int8, sx [S];
+// xg [S][I/32] int32 group sums when non-null (requires I % 32 == 0).
+template <int NT>
+__global__ __launch_bounds__(NT) void k_qrow_i8(const float* __restrict__ x, int8_t* __restrict__ q,
+                                                float* __restrict__ sx, int32_t* __restrict__ xg,
+                                                int I, int64_t ldx, int64_t ldq) {
+  __shared__ float red[NT / MOTY_WAVE];
+  const int64_t row = blockIdx.x;
+  const float* xr = x + row * ldx;
+  int8_t* qr = q + row * ldq;
+  float amax = 0.f;
+  const bool vec = ((I & 3) == 0) && ((((uintptr_t)xr) & 15) == 0) && ((((uintptr_t)qr) & 3) == 0);
+  if (vec) {
+    for (int i = threadIdx.x * 4; i < I; i += NT * 4) {
+      float4 v = *(const float4*)(xr + i);
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+  } else {
+    for (int i = threadIdx.x; i < I; i += NT) amax = fmaxf(amax, fabsf(xr[i]));
+  }
+  amax = block_max<NT>(amax, red);
+  float s = amax / 127.f;
+  if (s < 1e-12f) s = 1e-12f;
+  const float inv = 1.f / s;
+  if (threadIdx.x == 0) sx[row] = s;
+  if (vec) {
+    for (int i = threadIdx.x * 4; i < I; i += NT * 4) {
+      float4 v = *(const float4*)(xr + i);
+      int a = rne_int(v.x * inv), b = rne_int(v.y * inv), c = rne_int(v.z * inv), d = rne_int(v.w * inv);
+      uint32_t p = (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+                   ((uint32_t)(d & 0xff) << 24);
+      *(uint32_t*)(qr + i) = p;
+      if (xg) {
+        // 8 consecutive threads cover one group of 32
+        int gsum = a + b + c + d;
+        gsum += __shfl_xor(gsum, 1, 64);
+        gsum += __shfl_xor(gsum, 2, 64);
+        gsum += __shfl_xor(gsum, 4, 64);
+        if ((threadIdx.x & 7) == 0) xg[row * (I / 32) + i / 32] = gsum;
+      }
+    }
+  } else {
+    for (int i = threadIdx.x; i < I; i += NT) qr[i] = (int8_t)rne_int(xr[i] * inv);
+    if (xg) {
+      __syncthreads();
+      for (int g = threadIdx.x; g < I / 32; g += NT) {
+        int a = 0;
+        for (int j = 0; j < 32; j++) a += qr[g * 32 + j];
+        xg[row * (I / 32) + g] = a;
+      }
+    }
+  }
+}
+
+// Weight rows: s = amax/qmax clamped at 1e-8, v = clip(rint(w/s)).
+template <int NT>
+__global__ __launch_bounds__(NT) void k_quantize_rows(const float* __restrict__ w, int8_t* __restrict__ q,
+                                                      float* __restrict__ scale, int I, int bits) {
+  __shared__ float red[NT / MOTY_WAVE];
+  const int64_t row = blockIdx.x;
+  const float* wr = w + row * (int64_t)I;
+  int8_t* qr = q + row * (int64_t)I;
+  const int qmax = (1 << (bits - 1)) - 1;
+  float amax = 0.f;
+  for (int i = threadIdx.x; i < I; i += NT) amax = fmaxf(amax, fabsf(wr[i]));
+  amax = block_max<NT>(amax, red);
+  float s = amax / (float)qmax;
+  if (s < 1e-8f) s = 1e-8f;
+  if (threadIdx.x == 0) scale[row] = s;
+  for (int i = threadIdx.x; i < I; i += NT) {
+    int v = rne_int(wr[i] / s);
+    v = v > qmax ? qmax : v;
+    v = v < -qmax - 1 ? -qmax - 1 : v;
+    qr[i] = (int8_t)v;
+  }
+}
+
+// One thread per (row, group).  Odd trailing elements pair with a zero code.
+__global__ void k_pack_i4g(const float* __restrict__ w, uint8_t* __restrict__ q4, float* __restrict__ scale,
+                           int O, int I, int gs) {
+  const int ng = (I + gs - 1) / gs, rb = (I + 1) / 2;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)O * ng) return;
+  const int64_t o = t / ng;
+  const int g = (int)(t % ng);
+  const float* wr = w + o * I;
+  const int base = g * gs;
+  const int glen = base + gs > I ? I - base : gs;
+  float amax = 0.f;
+  for (int i = base; i < base + glen; i++) amax = fmaxf(amax, fabsf(wr[i]));
+  float s = amax / 7.f;
+  if (s < 1e-8f) s = 1e-8f;
+  scale[o * ng + g] = s;
+  uint8_t* qr = q4 + o * rb;
+  for (int i = base; i < base + glen; i += 2) {
+    int v0 = rne_int(wr[i] / s);
+    v0 = v0 > 7 ? 7 : (v0 < -8 ? -8 : v0);
+    int v1 = 0;
+    if (i + 1 < base + glen) {
+      v1 = rne_int(wr[i + 1] / s);
+      v1 = v1 > 7 ? 7 : (v1 < -8 ? -8 : v1);
+    }
+    qr[i >> 1] = (uint8_t)((v0 + 8) | ((v1 + 8) << 4));
+  }
+}
+
+int launch_qrow_i8(const float* x, int8_t* q, float* sx, int32_t* xg, int S, int I, int64_t ldx,
+                   int64_t ldq, hipStream_t st) {
+  if (S <= 0) return MOTY_OK;
+  if (xg && (I % 32)) return MOTY_EINVAL;
+  hipLaunchKernelGGL(k_qrow_i8<256>, dim3(S), dim3(256), 0, st, x, q, sx, xg, I, ldx, ldq);
+  LAUNCH_TRY("k_qrow_i8");
+  return MOTY_OK;
+}
+
+int launch_quantize_rows(const float* w, int8_t* q, float* scale, int O, int I, int bits, hipStream_t st) {
+  if (O <= 0) return MOTY_OK;
+  hipLaunchKernelGGL(k_quantize_rows<256>, dim3(O), dim3(256), 0, st, w, q, scale, I, bits);
+  LAUNCH_TRY("k_quantize_rows");
+  return MOTY_OK;
+}
+
+int launch_pack_i4g(const float* w, uint8_t* q4, float* scale, int O, int I, int gs, hipStream_t st) {
+  const int ng = (I + gs - 1) / gs;
+  const int64_t n = (int64_t)O * ng;
+  if (n <= 0) return MOTY_OK;
+  hipLaunchKernelGGL(k_pack_i4g, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, w, q4, scale, O, I, gs);
+  LAUNCH_TRY("k_pack_i4g");
+  return MOTY_OK;
+}
+
+}  // namespace moty

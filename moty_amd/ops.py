@@ -1,0 +1,159 @@
+"""torch-tensor wrappers over the device entry points of libmoty_hw_hip.
+
+Each function mirrors one reference function (same name without the moty_
+prefix, same argument meaning); tensors must live on the GPU, outputs are
+allocated here, and work is queued on torch's current stream."""
+import ctypes as C
+
+import torch
+
+from . import MotyHipMoe, ORDER_EXPERT, check, lib
+
+
+def _p(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _dev(*ts):
+    for t in ts:
+        if t is not None and (not t.is_cuda or not t.is_contiguous()):
+            raise ValueError("expected contiguous GPU tensors")
+
+
+def qrow_i8(x, group_sums=False):
+    """hw/hw_quant.h:9-16 over every row: returns (q int8 [S,I], sx [S], xg)."""
+    _dev(x)
+    S, I = x.shape
+    q = torch.empty((S, I), dtype=torch.int8, device=x.device)
+    sx = torch.empty(S, dtype=torch.float32, device=x.device)
+    xg = torch.empty((S, I // 32), dtype=torch.int32, device=x.device) if group_sums else None
+    check(lib().moty_hip_qrow_i8_dev(_p(x), _p(q), _p(sx), _p(xg), S, I, _stream()), "qrow_i8")
+    return q, sx, xg
+
+
+def quantize_rows(w, bits=8):
+    """nn/quant.c:12-33: (q int8 [O,I], scale [O])."""
+    _dev(w)
+    O, I = w.shape
+    q = torch.empty((O, I), dtype=torch.int8, device=w.device)
+    s = torch.empty(O, dtype=torch.float32, device=w.device)
+    check(lib().moty_hip_quantize_rows_dev(_p(w), _p(q), _p(s), O, I, bits, _stream()), "quantize_rows")
+    return q, s
+
+
+def pack_int4_grouped(w, gs=32):
+    """nn/quant.c:57-83: (q4 uint8 [O,(I+1)/2], scale [O, ceil(I/gs)])."""
+    _dev(w)
+    O, I = w.shape
+    q4 = torch.empty((O, (I + 1) // 2), dtype=torch.uint8, device=w.device)
+    s = torch.empty((O, (I + gs - 1) // gs), dtype=torch.float32, device=w.device)
+    check(lib().moty_hip_pack_int4_grouped_dev(_p(w), _p(q4), _p(s), O, I, gs, _stream()), "pack_int4_grouped")
+    return q4, s
+
+
+def matmul_q_s(x, q, scale, out=None):
+    """nn/matmul.c:51-66: y [S,O] = Q8 matmul of x [S,I]."""
+    _dev(x, q, scale)
+    S, I = x.shape
+    O = q.shape[0]
+    y = out if out is not None else torch.empty((S, O), dtype=torch.float32, device=x.device)
+    check(lib().moty_hip_matmul_q_s_dev(_p(y), _p(x), _p(q), _p(scale), S, I, O, _stream()), "matmul_q_s")
+    return y
+
+
+def matmul_q8_preq(xq, sx, q, scale, out=None):
+    _dev(xq, sx, q, scale)
+    S, I = xq.shape
+    O = q.shape[0]
+    y = out if out is not None else torch.empty((S, O), dtype=torch.float32, device=xq.device)
+    check(lib().moty_hip_matmul_q8_preq_dev(_p(y), _p(xq), _p(sx), _p(q), _p(scale), S, I, O, _stream()),
+          "matmul_q8_preq")
+    return y
+
+
+def matmul_i4_grouped_s(x, q4, scale, gs=32, idot4=True, out=None):
+    """nn/matmul.c:164-197 (idot4 picks the IDOT4=1 branch)."""
+    _dev(x, q4, scale)
+    S, I = x.shape
+    O = q4.shape[0]
+    y = out if out is not None else torch.empty((S, O), dtype=torch.float32, device=x.device)
+    check(lib().moty_hip_matmul_i4_grouped_s_dev(_p(y), _p(x), _p(q4), _p(scale), S, I, O, gs, int(bool(idot4)),
+                                                 _stream()), "matmul_i4_grouped_s")
+    return y
+
+
+def matmul(x, W, out=None):
+    """nn/matmul.c:15-27 (f32, dot_f32 AVX512 order)."""
+    _dev(x, W)
+    S, I = x.shape
+    O = W.shape[0]
+    y = out if out is not None else torch.empty((S, O), dtype=torch.float32, device=x.device)
+    check(lib().moty_hip_matmul_dev(_p(y), _p(x), _p(W), S, I, O, _stream()), "matmul")
+    return y
+
+
+def silu_mul(g, u):
+    """hw/hw_ops.h:19-21, in place on g."""
+    _dev(g, u)
+    check(lib().moty_hip_silu_mul_dev(_p(g), _p(u), g.numel(), _stream()), "silu_mul")
+    return g
+
+
+def softmax_rows(x):
+    """nn/norm.c:10 per row, in place."""
+    _dev(x)
+    S, n = x.shape
+    check(lib().moty_hip_softmax_rows_dev(_p(x), S, n, _stream()), "softmax_rows")
+    return x
+
+
+def expf(x):
+    _dev(x)
+    y = torch.empty_like(x)
+    check(lib().moty_hip_expf_dev(_p(x), _p(y), x.numel(), _stream()), "expf")
+    return y
+
+
+def dense_ffn_q8(x, gate, gs, up, us, down, ds, out=None):
+    """nn/ffn.c:26-55 over Q8 weights."""
+    _dev(x, gate, gs, up, us, down, ds)
+    S, D = x.shape
+    I = gate.shape[0]
+    y = out if out is not None else torch.empty((S, D), dtype=torch.float32, device=x.device)
+    check(lib().moty_hip_dense_ffn_q8_dev(_p(y), _p(x), S, _p(gate), _p(gs), _p(up), _p(us), _p(down), _p(ds),
+                                          D, I, _stream()), "dense_ffn_q8")
+    return y
+
+
+class MoeLayer:
+    """Device-resident MoE layer (MotyMoeView analogue, nn/moe.h:19-33)."""
+
+    def __init__(self, router, g, gs, u, us, d, ds, K, norm_topk=1, order=ORDER_EXPERT, logit_bias=None):
+        _dev(router, g, gs, u, us, d, ds, logit_bias)
+        self.keep = (router, g, gs, u, us, d, ds, logit_bias)
+        E, I, D = g.shape
+        self.E, self.I, self.D, self.K = E, I, D, K
+        self.view = MotyHipMoe(router=router.data_ptr(), logit_bias=None if logit_bias is None else logit_bias.data_ptr(),
+                               g=g.data_ptr(), u=u.data_ptr(), d=d.data_ptr(),
+                               gs=gs.data_ptr(), us=us.data_ptr(), ds=ds.data_ptr(),
+                               E=E, K=K, I=I, D=D, norm_topk=norm_topk, combine_order=order)
+
+    def __call__(self, x, out=None, want_routing=False):
+        _dev(x)
+        S = x.shape[0]
+        y = out if out is not None else torch.empty((S, self.D), dtype=torch.float32, device=x.device)
+        v = MotyHipMoe.from_buffer_copy(self.view)
+        idx = w = cnt = None
+        if want_routing:
+            idx = torch.empty((S, self.K), dtype=torch.int32, device=x.device)
+            w = torch.empty((S, self.K), dtype=torch.float32, device=x.device)
+            cnt = torch.empty(self.E, dtype=torch.int32, device=x.device)
+            v.idx_out, v.w_out, v.counts_out = idx.data_ptr(), w.data_ptr(), cnt.data_ptr()
+        check(lib().moty_hip_moe_topk_dev(C.byref(v), _p(x), S, _p(y), _stream()), "moe_topk")
+        if want_routing:
+            return y, idx, w, cnt
+        return y

@@ -1,0 +1,169 @@
+"""GPU parity: every HIP kernel against the oracle on the same seeded inputs,
+bit-exact (int8 activations, int32 accumulators, f32 outputs)."""
+import numpy as np
+import pytest
+import torch
+
+from cpu_libs import (o_matmul_f32, o_matmul_i4g, o_matmul_q_s, o_pack_int4_grouped, o_qrow, o_quantize_rows,
+                      oracle, ptr, randn, rng)
+from gpu_util import mismatch, same_bits, say, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ops(dev):
+    import moty_amd
+    moty_amd.lib()
+    from moty_amd import ops
+    return ops
+
+
+def test_expf_matches_oracle(ops):
+    say("expf sweep")
+    # strided sweep over all bit patterns plus dense blocks where silu/softmax live
+    pats = np.concatenate([
+        np.arange(0, 1 << 32, 4093, dtype=np.uint64).astype(np.uint32),
+        np.arange(0x3f000000, 0x3f000000 + (1 << 21), dtype=np.uint32),
+        np.arange(0xc0000000, 0xc0000000 + (1 << 21), dtype=np.uint32),
+        np.array([0x42b17217, 0x42b17218, 0xc2cff1b4, 0xc2cff1b5, 0xc2aeac50, 0xc2b00000, 0xc2c80000,
+                  0x7f800000, 0xff800000, 0, 0x80000000, 1], dtype=np.uint32)])
+    x = pats.view(np.float32)
+    x = x[~np.isnan(x)]
+    y = to_np(ops.expf(to_dev(x)))
+    o = oracle()
+    ref = np.array([o.o_expf(float(v)) for v in x[:20000]], np.float32)
+    assert same_bits(y[:20000], ref), mismatch(y[:20000], ref)
+    ref_all = np.exp(x.astype(np.float64)).astype(np.float32)
+    # the restated algorithm is within 1 ulp of the correctly rounded value everywhere
+    fin = np.isfinite(ref_all) & (ref_all > 1e-37)
+    ulp = np.abs(y[fin].view(np.int32).astype(np.int64) - ref_all[fin].view(np.int32).astype(np.int64))
+    assert ulp.max() <= 1
+
+
+def test_expf_full_against_oracle_blocks(ops):
+    # 2^24 consecutive patterns in each of 4 blocks, checked against the
+    # oracle's libm-identical expf via the oracle's own range check
+    o = oracle()
+    for lo in (0x3e800000, 0x40000000, 0xbf000000, 0xc1000000):
+        say("expf block", hex(lo))
+        pats = np.arange(lo, lo + (1 << 22), dtype=np.uint64).astype(np.uint32)
+        y = to_np(ops.expf(to_dev(pats.view(np.float32))))
+        ref = np.empty_like(y)
+        xs = pats.view(np.float32)
+        ref = np.frompyfunc(lambda v: o.o_expf(float(v)), 1, 1)(xs[::97]).astype(np.float32)
+        assert same_bits(y[::97], ref)
+
+
+@pytest.mark.parametrize("S,I", [(1, 1024), (3, 3072), (7, 100), (2, 16384)])
+def test_qrow_i8(ops, S, I):
+    say("qrow", S, I)
+    x = randn(S * I, (S, I)) * 3
+    x[0, :5] = [0.0, -0.0, 1e-30, 5.5, -5.5]
+    q, sx, xg = ops.qrow_i8(to_dev(x), group_sums=(I % 32 == 0))
+    q2, sx2 = o_qrow(x)
+    assert same_bits(to_np(sx), sx2) and same_bits(to_np(q), q2)
+    if xg is not None:
+        assert (to_np(xg) == q2.reshape(S, -1, 32).astype(np.int32).sum(-1)).all()
+
+
+def test_qrow_zero_row(ops):
+    q, sx, _ = ops.qrow_i8(torch.zeros((2, 64), device="cuda:0"))
+    assert (to_np(sx) == np.float32(1e-12)).all() and not to_np(q).any()
+
+
+@pytest.mark.parametrize("O,I", [(64, 1024), (7, 33), (3, 3072)])
+def test_quantize_rows(ops, O, I):
+    say("quantize_rows", O, I)
+    w = randn(O + I, (O, I), 0.02)
+    q, s = ops.quantize_rows(to_dev(w))
+    q2, s2 = o_quantize_rows(w)
+    assert same_bits(to_np(q), q2) and same_bits(to_np(s), s2)
+
+
+@pytest.mark.parametrize("O,I,gs", [(64, 4096, 32), (5, 31, 16), (8, 100, 32)])
+def test_pack_int4_grouped(ops, O, I, gs):
+    say("pack_i4g", O, I, gs)
+    w = randn(O * 7 + I, (O, I), 0.02)
+    q4, s = ops.pack_int4_grouped(to_dev(w), gs)
+    q42, s2 = o_pack_int4_grouped(w, gs)
+    assert same_bits(to_np(q4), q42) and same_bits(to_np(s), s2)
+
+
+Q8_CASES = [(1, 1024, 3072), (1, 3072, 1024), (2, 1024, 100), (3, 48, 24), (4, 2048, 1024),
+            (1, 16384, 64), (5, 1024, 256), (8, 3072, 96), (64, 1024, 1024), (512, 1024, 2048),
+            (130, 2048, 200), (33, 16, 17)]
+
+
+@pytest.mark.parametrize("S,I,O", Q8_CASES)
+def test_matmul_q_s(ops, S, I, O):
+    say("matmul_q_s", S, I, O)
+    w = randn(O + 3 * I, (O, I), 0.02)
+    q, s = o_quantize_rows(w)
+    x = randn(S + I, (S, I))
+    y = to_np(ops.matmul_q_s(to_dev(x), to_dev(q), to_dev(s)))
+    y2 = o_matmul_q_s(x, q, s)
+    assert same_bits(y, y2), mismatch(y, y2)
+
+
+def test_matmul_q8_extremes(ops):
+    # w = -128 everywhere and activations at +-127 (simd_tests.c rep 0)
+    S, I, O = 9, 4096, 40
+    q = np.full((O, I), -128, np.int8)
+    s = np.full(O, 0.01, np.float32)
+    x = np.where(rng(1).integers(0, 2, (S, I)) > 0, 1.0, -1.0).astype(np.float32)
+    for SS in (1, S):
+        y = to_np(ops.matmul_q_s(to_dev(x[:SS]), to_dev(q), to_dev(s)))
+        assert same_bits(y, o_matmul_q_s(x[:SS], q, s))
+
+
+@pytest.mark.parametrize("S,I,O", [(1, 4096, 256), (2, 1024, 64), (4, 12288, 128), (1, 64, 5),
+                                   (256, 4096, 192), (37, 1024, 100), (5, 128, 64)])
+def test_i4g_idot4(ops, S, I, O):
+    say("i4g idot4", S, I, O)
+    w = randn(O + I, (O, I), 0.02)
+    q4, s = o_pack_int4_grouped(w)
+    x = randn(S + 2 * I, (S, I))
+    y = to_np(ops.matmul_i4_grouped_s(to_dev(x), to_dev(q4), to_dev(s), 32, True))
+    y2 = o_matmul_i4g(x, q4, s, True)
+    assert same_bits(y, y2), mismatch(y, y2)
+
+
+@pytest.mark.parametrize("S,I,O", [(1, 4096, 256), (3, 96, 40), (16, 1024, 64)])
+def test_i4g_f32(ops, S, I, O):
+    say("i4g f32", S, I, O)
+    w = randn(O + I, (O, I), 0.02)
+    q4, s = o_pack_int4_grouped(w)
+    x = randn(S + 2 * I, (S, I))
+    y = to_np(ops.matmul_i4_grouped_s(to_dev(x), to_dev(q4), to_dev(s), 32, False))
+    y2 = o_matmul_i4g(x, q4, s, False)
+    assert same_bits(y, y2), mismatch(y, y2)
+
+
+@pytest.mark.parametrize("S,I,O", [(8, 2048, 64), (3, 33, 5), (2, 16, 3), (1, 100, 7), (5, 2049, 128)])
+def test_matmul_f32(ops, S, I, O):
+    say("matmul_f32", S, I, O)
+    W = randn(I, (O, I), 0.02)
+    x = randn(I + 1, (S, I))
+    y = to_np(ops.matmul(to_dev(x), to_dev(W)))
+    assert same_bits(y, o_matmul_f32(x, W))
+
+
+def test_silu_and_softmax(ops):
+    say("silu/softmax")
+    g = randn(1, 100000) * 6
+    g[:6] = [0.0, -0.0, 100.0, -100.0, -90.0, 89.0]
+    u = randn(2, 100000)
+    gd = to_dev(g)
+    ops.silu_mul(gd, to_dev(u))
+    g2 = g.copy()
+    oracle().o_silu_mul(ptr(g2), ptr(u), g.size)
+    assert same_bits(to_np(gd), g2)
+    for E in (8, 64, 128, 300):
+        x = randn(E, (4, E)) * 3
+        xd = to_dev(x)
+        ops.softmax_rows(xd)
+        x2 = x.copy()
+        for r in range(4):
+            oracle().o_softmax(ptr(x2[r]), E)
+        assert same_bits(to_np(xd), x2)
