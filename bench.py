@@ -1,0 +1,372 @@
+"""bench.py -- one-GPU benchmark of libmoty-hw-hip on BASELINE.json's configs.
+
+Headline (`value`): C1, the Qwen3-0.6B-shaped decode FFN through the Q8_0
+path (fused gate/up GEMV with the SiLU epilogue, then the down GEMV), as
+whole-FFN algorithmic GB/s.  The MoE metric (C4, OLMoE-shaped layer at
+T=256, tokens/s) is the `moe` object; C2, C3 and C5 are under `extra`.
+Every figure is kernel work on inputs already resident in HBM: weights
+rotate over distinct copies totalling more than the 256 MB Infinity Cache,
+so each step streams its weights from HBM, and steps replay from HIP graphs.
+The reference's CPU path (oracle/_ref, built from the reference's sources)
+is timed on the host cores beside it (`cpu_baseline`).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+# the reference engines' own OpenMP tuning (runtime/env.c:43-78), for the
+# CPU baseline; set before any OpenMP runtime loads
+for _k, _v in (("OMP_WAIT_POLICY", "active"), ("OMP_PROC_BIND", "close"), ("GOMP_SPINCOUNT", "200000")):
+    os.environ.setdefault(_k, _v)
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA
+METRIC = "Q8 GEMV HBM GB/s (% peak); MoE layer tokens/s at T=256 (1 GPU)"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1024)
+    ap.add_argument("--warmup", type=int, default=128)
+    ap.add_argument("--quick", action="store_true", help="C1 and C4 only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU reference baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on each CPU baseline sample")
+    return ap.parse_args()
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def roofline(bound, achieved, peak, unit, traffic=None):
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic}
+
+
+class Ctx:
+    def __init__(self, torch, ops):
+        self.torch, self.ops = torch, ops
+
+    def gen(self, cfg, tensor):
+        return self.torch.Generator(device="cuda:0").manual_seed(0x4D4F5459 ^ (cfg << 8) ^ tensor)
+
+    def randn(self, shape, g, std=1.0):
+        return self.torch.randn(shape, generator=g, device="cuda:0", dtype=self.torch.float32) * std
+
+    def q8(self, shape, g):
+        """W ~ N(0, 0.02) on the device, quantized by the library's
+        moty_quantize_rows kernel (QBITS=8)."""
+        w = self.randn(shape, g, 0.02)
+        q, s = self.ops.quantize_rows(w.reshape(-1, shape[-1]))
+        return q.reshape(shape), s.reshape(shape[:-1])
+
+    def q4(self, shape, g):
+        w = self.randn(shape, g, 0.02)
+        return self.ops.pack_int4_grouped(w, 32)
+
+    def time_steps(self, fns, steps, warmup):
+        """Capture one step per callable into a HIP graph, replay it; returns
+        (seconds per step, steps timed).  Events sit on the stream the library
+        launches on (torch's current stream)."""
+        torch = self.torch
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for f in fns:  # eager pass sizes the library's scratch before capture
+                f()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for f in fns:
+                f()
+        reps = max(1, -(-steps // len(fns)))
+        for _ in range(max(1, -(-warmup // len(fns)))):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        n = reps * len(fns)
+        return e0.elapsed_time(e1) / 1e3 / n, n
+
+
+def n_copies(bytes_per_copy, target=1200 << 20, lo=2):
+    return max(lo, -(-target // bytes_per_copy))
+
+
+# --------------------------------------------------------------------------
+def bench_c1(c, steps, warmup):
+    """Qwen3-0.6B FFN decode: D=1024, I=3072, S=1 (configs[0] shape)."""
+    torch, ops = c.torch, c.ops
+    D, I = 1024, 3072
+    wbytes = 3 * D * I + (2 * I + D) * 4           # int8 weights + f32 row scales
+    algo = wbytes + 2 * D * 4                      # + x in, out
+    ncopy = n_copies(wbytes)
+    g = c.gen(0, 1)
+    copies = [c.q8((I, D), g) + c.q8((I, D), g) + c.q8((D, I), g) for _ in range(ncopy)]
+    x = c.randn((1, D), c.gen(0, 2))
+    out = torch.empty((1, D), device="cuda:0")
+    h = torch.empty((1, I), device="cuda:0")
+    t, n = c.time_steps([lambda w=w: ops.dense_ffn_q8(x, *w, out=out) for w in copies], steps, warmup)
+    # dominant kernel alone: the fused gate+up GEMV (k_gemv_q8 PAIR mode)
+    tg, _ = c.time_steps([lambda w=w: ops.gate_up_silu_q8(x, w[0], w[1], w[2], w[3], out=h) for w in copies],
+                         steps, warmup)
+    gu_algo = 2 * I * D + 2 * I * 4 + D * 4 + I * 4
+    torch.cuda.synchronize()
+    return {
+        "workload": "C1 Qwen3-0.6B FFN decode, Q8_0 (fused gate/up GEMV + SiLU, down GEMV), S=1, D=1024, I=3072",
+        "gbs": algo / t / 1e9, "ms_per_step": t * 1e3, "steps": n, "algo_bytes": algo,
+        "weight_copies": ncopy, "x": x, "w0": copies[0],
+        "kernel": {"name": "k_gemv_q8<1,1,PAIR> gate+up+SiLU", "us": tg * 1e6, "algo_bytes": gu_algo,
+                   "gbs": gu_algo / tg / 1e9},
+    }
+
+
+def moe_weights(c, cfg, E, I, D):
+    g = c.gen(cfg, 10)
+    G, GS = c.q8((E, I, D), g)
+    U, US = c.q8((E, I, D), g)
+    Dn, DS = c.q8((E, D, I), g)
+    return G, GS, U, US, Dn, DS
+
+
+def bench_moe(c, cfg, T, E, K, I, D, norm, order, steps, warmup, bias=None, label=""):
+    torch, ops = c.torch, c.ops
+    from moty_amd.ops import MoeLayer
+    ebytes = 3 * E * I * D + E * (2 * I + D) * 4
+    ncopy = n_copies(ebytes, lo=2)
+    Wr = c.randn((E, D), c.gen(cfg, 1), 0.02)
+    x = c.randn((T, D), c.gen(cfg, 2))
+    layers = [MoeLayer(Wr, *moe_weights(c, cfg + 16 * k, E, I, D), K, norm_topk=norm, order=order,
+                       logit_bias=bias) for k in range(ncopy)]
+    out = torch.empty((T, D), device="cuda:0")
+    # routing statistics (same router for every copy)
+    _, idx, w, cnt = layers[0](x, want_routing=True)
+    cnt = cnt.cpu()
+    active = int((cnt > 0).sum())
+    algo = 3 * active * I * D + active * (2 * I + D) * 4 + E * D * 4 + 2 * T * D * 4
+    ops_int = 2 * T * K * 3 * I * D
+    t, n = c.time_steps([lambda L=L: L(x, out=out) for L in layers], max(8, steps // 16), max(4, warmup // 16))
+    gbs = algo / t / 1e9
+    return {
+        "workload": label, "tokens_per_s": T / t, "ms_per_layer": t * 1e3, "steps": n, "weight_copies": ncopy,
+        "active_experts": active, "load_max": int(cnt.max()), "load_mean": round(float(cnt.float().mean()), 2),
+        "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s"),
+        "int_tops": round(ops_int / t / 1e12, 2),
+        "x": x, "Wr": Wr, "layer0": layers[0],
+    }
+
+
+def bench_c2(c, steps, warmup):
+    """Qwen3-0.6B layer, the seven projections as Q8 prefill GEMMs, M=512."""
+    torch, ops = c.torch, c.ops
+    M = 512
+    shapes = [("q", 2048, 1024), ("k", 1024, 1024), ("v", 1024, 1024), ("gate", 3072, 1024), ("up", 3072, 1024),
+              ("o", 1024, 2048), ("down", 1024, 3072)]
+    wbytes = sum(O * I + O * 4 for _, O, I in shapes)
+    ncopy = n_copies(wbytes, target=1100 << 20)
+    g = c.gen(1, 1)
+    copies = [[c.q8((O, I), g) for _, O, I in shapes] for _ in range(ncopy)]
+    xs = {I: c.randn((M, I), c.gen(1, 2 + I)) for I in (1024, 2048, 3072)}
+    ys = [torch.empty((M, O), device="cuda:0") for _, O, _ in shapes]
+    xq = {I: torch.empty((M, I), dtype=torch.int8, device="cuda:0") for I in xs}
+    sx = {I: torch.empty(M, device="cuda:0") for I in xs}
+    lib = ops.lib()
+
+    def step(ws):
+        def f():
+            for I in xs:  # one activation quantization per distinct input
+                ops.check(lib.moty_hip_qrow_i8_dev(ops._p(xs[I]), ops._p(xq[I]), ops._p(sx[I]), None, M, I,
+                                                   ops._stream()), "qrow")
+            for (name, O, I), (q, s), y in zip(shapes, ws, ys):
+                ops.matmul_q8_preq(xq[I], sx[I], q, s, out=y)
+        return f
+    t, n = c.time_steps([step(w) for w in copies], max(16, steps // 8), max(4, warmup // 8))
+    ops_int = 2 * M * sum(O * I for _, O, I in shapes)
+    algo = wbytes + sum(M * I * 4 for I in (1024, 1024, 1024, 1024, 1024, 2048, 3072)) + sum(M * O * 4 for _, O, _ in shapes)
+    return {"workload": "C2 Qwen3-0.6B layer, 7 Q8 projections as prefill GEMMs, M=512", "ms_per_step": t * 1e3,
+            "steps": n, "roofline": roofline("mfma", ops_int / t / 1e12, INT8_PEAK_TOPS, "TOP/s"),
+            "hbm_gbs": round(algo / t / 1e9, 1)}
+
+
+def bench_c3(c, steps, warmup):
+    """8B-dense FFN in grouped int4 (Q4FMT=g, IDOT4=1): M=1 GEMV and M=256 GEMM."""
+    torch, ops = c.torch, c.ops
+    D, I = 4096, 12288
+    wbytes = 3 * (I * D // 2 + I * D // 32 * 4)
+    ncopy = n_copies(wbytes)
+    g = c.gen(2, 1)
+    copies = [(c.q4((I, D), g), c.q4((I, D), g), c.q4((D, I), g)) for _ in range(ncopy)]
+    res = {}
+    for M in (1, 256):
+        x = c.randn((M, D), c.gen(2, 2))
+        gy = torch.empty((M, I), device="cuda:0")
+        uy = torch.empty((M, I), device="cuda:0")
+        y = torch.empty((M, D), device="cuda:0")
+
+        def step(w):
+            def f():
+                ops.matmul_i4_grouped_s(x, w[0][0], w[0][1], out=gy)
+                ops.matmul_i4_grouped_s(x, w[1][0], w[1][1], out=uy)
+                ops.silu_mul(gy, uy)
+                ops.matmul_i4_grouped_s(gy, w[2][0], w[2][1], out=y)
+            return f
+        t, n = c.time_steps([step(w) for w in copies], max(8, steps // (8 if M == 1 else 64)), 8)
+        ops_int = 2 * M * 3 * I * D
+        algo = wbytes + M * (D + I + I + D) * 4
+        res["M%d" % M] = {"ms_per_step": t * 1e3, "steps": n,
+                          "hbm": roofline("hbm", algo / t / 1e9, HBM_PEAK_GBS, "GB/s"),
+                          "mfma": roofline("mfma", ops_int / t / 1e12, INT8_PEAK_TOPS, "TOP/s")}
+    return {"workload": "C3 8B-dense FFN, grouped int4 g32 (IDOT4=1), D=4096, I=12288, M=1 and M=256", **res}
+
+
+# --------------------------------------------------------------------------
+def cpu_baseline(c1, c4, budget):
+    """The reference's own CPU kernels (oracle/_ref, kind 'reference'), or the
+    oracle restatement ('port') when the reference build is absent."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import cpu_libs as cl
+    r = cl.ref(True)
+    kind = "reference" if r is not None else "port"
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    x = c1["x"].cpu().numpy()
+    G, GS, U, US, Dn, DS = [t.cpu().numpy() for t in c1["w0"]]
+    D, I = 1024, 3072
+
+    def ffn():
+        if r is not None:
+            g = np.empty((1, I), np.float32)
+            u = np.empty((1, I), np.float32)
+            y = np.empty((1, D), np.float32)
+            r.ref_matmul_q_s(cl.ptr(g), cl.ptr(x), cl.ptr(G), cl.ptr(GS), 1, D, I)
+            r.ref_matmul_q_s(cl.ptr(u), cl.ptr(x), cl.ptr(U), cl.ptr(US), 1, D, I)
+            r.ref_silu_mul(cl.ptr(g), cl.ptr(u), I)
+            r.ref_matmul_q_s(cl.ptr(y), cl.ptr(g), cl.ptr(Dn), cl.ptr(DS), 1, I, D)
+        else:
+            cl.o_dense_ffn_q8(x, G, GS, U, US, Dn, DS)
+
+    def med(fn, seconds, warm=3, nmin=20):
+        for _ in range(warm):
+            fn()
+        ts = []
+        t0 = time.perf_counter()
+        while len(ts) < nmin or time.perf_counter() - t0 < seconds:
+            a = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - a)
+            if time.perf_counter() - t0 > seconds and len(ts) >= 3:
+                break
+        return float(np.median(ts)), len(ts)
+
+    t1, n1 = med(ffn, min(3.0, budget))
+    out = {"value": round(c1["algo_bytes"] / t1 / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": kind,
+           "sample": "C1 decode FFN (3 matmul_q_s + silu_mul), median of %d runs after 3 warm-ups" % n1}
+    if c4 is not None:
+        lay = c4["layer0"]
+        xs = c4["x"].cpu().numpy()
+        Wr = c4["Wr"].cpu().numpy()
+        ws = [t.cpu().numpy() for t in lay.keep[1:7]]
+        T, D4 = xs.shape
+        E, I4, K = lay.E, lay.I, lay.K
+        Tb = 64  # bounded sample: the first 64 tokens of the T=256 batch
+
+        def moe():
+            o = np.empty((Tb, D4), np.float32)
+            if r is not None:
+                i2 = np.empty((Tb, K), np.int32)
+                r.ref_moe_olmoe(cl.ptr(o), cl.ptr(xs[:Tb]), Tb, cl.ptr(Wr), *[cl.ptr(a) for a in ws], E, K, I4, D4,
+                                0, cl.ptr(i2))
+            else:
+                cl.o_moe(xs[:Tb], Wr, dict(zip(("G", "GS", "U", "US", "Dn", "DS"), ws)), K, "olmoe", norm=0)
+        t4, n4 = med(moe, budget, warm=1, nmin=3)
+        out["moe"] = {"value": round(Tb / t4, 1), "unit": "tokens/s", "cores": cores, "kind": kind,
+                      "sample": "C4 OLMoE layer, olmoe engine call sequence (engines/olmoe.c:219-244), "
+                                "first %d of the 256 tokens, median of %d runs" % (Tb, n4)}
+    return out
+
+
+# --------------------------------------------------------------------------
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: every box in this pool has a single MI355X, so --gpus %d is not "
+              "supported. Run with --gpus 1." % args.gpus, file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import moty_amd
+    from moty_amd import ops
+    moty_amd.lib()
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    c = Ctx(torch, ops)
+
+    log("C1 decode FFN")
+    c1 = bench_c1(c, args.steps, args.warmup)
+    log("C1: %.1f GB/s, %.2f us/step; gate/up kernel %.2f us (%.1f GB/s)" % (
+        c1["gbs"], c1["ms_per_step"] * 1e3, c1["kernel"]["us"], c1["kernel"]["gbs"]))
+    log("C4 OLMoE MoE T=256")
+    c4 = bench_moe(c, 3, 256, 64, 8, 1024, 2048, 0, moty_amd.ORDER_TOPK, args.steps, args.warmup,
+                   label="C4 OLMoE MoE layer Q8, T=256, E=64, top-8 softmax (norm_topk_prob=false), I=1024, D=2048")
+    log("C4: %.0f tokens/s, %.3f ms/layer" % (c4["tokens_per_s"], c4["ms_per_layer"]))
+    extra = []
+    if not args.quick:
+        log("C2")
+        extra.append(bench_c2(c, args.steps, args.warmup))
+        log("C3")
+        extra.append(bench_c3(c, args.steps, args.warmup))
+        log("C5")
+        E5 = 128
+        bias = torch.zeros(E5, device="cuda:0")
+        bias[torch.arange(0, 128, 16, device="cuda:0")] = 2.0
+        for b, lab in ((None, "uniform"), (bias, "skewed (+2.0 on 8 hot experts)")):
+            r5 = bench_moe(c, 4, 1072, E5, 8, 768, 2048, 1, moty_amd.ORDER_EXPERT, args.steps, args.warmup, bias=b,
+                           label="C5 Qwen3-30B-A3B MoE layer Q8, T=1072 ragged batch (48 decode + 1024 prefill), "
+                                 "E=128, top-8, I=768, D=2048, " + lab)
+            for k in ("x", "Wr", "layer0"):
+                r5.pop(k)
+            extra.append(r5)
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline")
+        try:
+            cpu = cpu_baseline(c1, c4, args.cpu_seconds)
+        except Exception as e:  # the baseline is reported, never required
+            log("cpu baseline failed:", e)
+    k = c1["kernel"]
+    moe = {k2: v for k2, v in c4.items() if k2 not in ("x", "Wr", "layer0")}
+    moe["metric"] = "MoE layer tokens/s at T=256 (1 GPU)"
+    moe["value"] = round(moe.pop("tokens_per_s"), 1)
+    moe["unit"] = "tokens/s"
+    if cpu and "moe" in cpu:
+        moe["cpu_baseline"] = cpu.pop("moe")
+    line = {
+        "metric": METRIC, "value": round(c1["gbs"], 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": c1["steps"], "warmup": args.warmup, "ms_per_step": round(c1["ms_per_step"], 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (W ~ N(0,0.02) quantized by the library's QBITS=8 kernels, x ~ N(0,1)); "
+                "weights rotate over %d copies" % c1["weight_copies"],
+        "config": {"workload": c1["workload"]},
+        "roofline": dict(roofline("hbm", k["gbs"], HBM_PEAK_GBS, "GB/s"), kernel=k["name"],
+                         kernel_us=round(k["us"], 3)),
+        "whole_ffn_roofline": roofline("hbm", c1["gbs"], HBM_PEAK_GBS, "GB/s"),
+        "cpu_baseline": cpu,
+        "moe": moe,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -135,6 +135,11 @@ int moty_hip_expf_dev(const float *x, float *y, int64_t n, void *stream);
 int moty_hip_dense_ffn_q8_dev(float *out, const float *x, int S, const int8_t *gate, const float *gs,
                               const int8_t *up, const float *us, const int8_t *down, const float *ds, int D, int I,
                               void *stream);
+/* The decode half of that FFN before the down projection, fused: one pass
+ * over the gate and up rows, h [S][I] = silu(x.gate^T) * (x.up^T) -- the
+ * gate_up + silu_rows step of nn/ffn.c:28-37.  S <= 4. */
+int moty_hip_gate_up_silu_q8_dev(float *h, const float *x, int S, const int8_t *gate, const float *gs,
+                                 const int8_t *up, const float *us, int D, int I, void *stream);
 /* the MoE layer, all pointers in m and x/out on the device */
 int moty_hip_moe_topk_dev(const MotyHipMoe *m, const float *x, int S, float *out, void *stream);
 

@@ -282,6 +282,19 @@ int moty_hip_expf_dev(const float* x, float* y, int64_t n, void* stream) {
   return launch_expf(x, y, n, STREAM(stream));
 }
 
+int moty_hip_gate_up_silu_q8_dev(float* h, const float* x, int S, const int8_t* gate, const float* gs,
+                                 const int8_t* up, const float* us, int D, int I, void* stream) {
+  CUR(d);
+  if (S < 0 || D <= 0 || I <= 0 || !h || !x || !gate || !gs || !up || !us)
+    return set_error("gate_up_silu_q8: bad arguments"), MOTY_EINVAL;
+  if (S == 0) return MOTY_OK;
+  if (S > GEMV_MAX_S || (D % 16) || D > 16384) {
+    set_error("gate_up_silu_q8: S=%d D=%d unsupported (S <= %d, D %% 16 == 0)", S, D, GEMV_MAX_S);
+    return MOTY_EUNSUP;
+  }
+  return launch_gemv_q8(x, gate, gs, up, us, h, S, D, I, STREAM(stream));
+}
+
 int moty_hip_dense_ffn_q8_dev(float* out, const float* x, int S, const int8_t* gate, const float* gs,
                               const int8_t* up, const float* us, const int8_t* down, const float* ds, int D, int I,
                               void* stream) {

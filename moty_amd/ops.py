@@ -129,6 +129,17 @@ def dense_ffn_q8(x, gate, gs, up, us, down, ds, out=None):
     return y
 
 
+def gate_up_silu_q8(x, gate, gs, up, us, out=None):
+    """nn/ffn.c:28-37 for decode: h = silu(x.gate^T) * (x.up^T), one pass."""
+    _dev(x, gate, gs, up, us)
+    S, D = x.shape
+    I = gate.shape[0]
+    h = out if out is not None else torch.empty((S, I), dtype=torch.float32, device=x.device)
+    check(lib().moty_hip_gate_up_silu_q8_dev(_p(h), _p(x), S, _p(gate), _p(gs), _p(up), _p(us), D, I, _stream()),
+          "gate_up_silu_q8")
+    return h
+
+
 class MoeLayer:
     """Device-resident MoE layer (MotyMoeView analogue, nn/moe.h:19-33)."""
 
