@@ -128,13 +128,25 @@ __device__ __forceinline__ float hsum16_half(float v, int base) {
   return (b0 + b2) + (b1 + b3);
 }
 
-// exact dot_f32 (AVX512 order) of x (LDS) with W row (global), computed by a
-// 32-lane half-wave; returns the dot in every lane of the half.
+// exact dot_f32 (AVX512 order) of x with a W row, computed by a 32-lane
+// half-wave; returns the dot in every lane of the half.  Lane c owns chain c
+// (s0[c] for c < 16, s1[c-16] for c >= 16); loads are batched 16 steps ahead
+// of the FMA chain, which keeps the reference's order.
 __device__ __forceinline__ float dot_f32_half(const float* __restrict__ xs, const float* __restrict__ wr, int n) {
   const int c = threadIdx.x % 32;
   const int base = (threadIdx.x % MOTY_WAVE) & 32;
-  float s = 0.f;  // chain c: s0[c] for c < 16, s1[c-16] for c >= 16
+  float s = 0.f;
   int i = 0;
+  for (; i + 32 * 16 <= n; i += 32 * 16) {
+    float w[16], x[16];
+#pragma unroll
+    for (int u = 0; u < 16; u++) {
+      w[u] = wr[i + 32 * u + c];
+      x[u] = xs[i + 32 * u + c];
+    }
+#pragma unroll
+    for (int u = 0; u < 16; u++) s = __fmaf_rn(x[u], w[u], s);
+  }
   for (; i + 32 <= n; i += 32) s = __fmaf_rn(xs[i + c], wr[i + c], s);
   if (i + 16 <= n) {
     if (c < 16) s = __fmaf_rn(xs[i + c], wr[i + c], s);

@@ -1,4 +1,4 @@
-// gemm_q8.hip -- Q8_0 prefill GEMM on int8 MFMA (v_mfma_i32_16x16x64_i8).
+// gemm_q8.hip -- Q8_0 prefill GEMM on int8 MFMA (v_mfma_i32_32x32x32_i8).
 //
 // Reference: moty_matmul_q_s (nn/matmul.c:51-66) for S > 1 token rows:
 //     y[s*O+o] = (scale[o]*sx[s]) * (float)sum_i W[o][i]*xq[s][i]
@@ -7,89 +7,103 @@
 // reference's two multiplies.
 //
 // Both operands are K-contiguous (xq [S][I] token-major, W [O][I] row-major),
-// which is exactly the MFMA operand layout: lane l of a 16x16x64 step holds
-// 16 consecutive k-bytes of row (l % 16) at k offset 16*(l / 16), for A
-// (tokens) and B (weight rows) alike.  Fragments load straight from global
-// memory (16 B per lane, 64 B contiguous per row) with the next K step
-// prefetched while the current one runs on the matrix cores.
+// so both stage into LDS the same way and feed the matrix cores alike.
 #include "common.h"
 #include "kernels.h"
 
 namespace moty {
 
-constexpr int GM_NT = 256;  // 4 waves, 2x2 over the block tile
-constexpr int GM_BM = 64, GM_BN = 64, GM_BK = 64;
+constexpr int GM_NT = 256;  // 4 waves, 2 x 2 over the block tile
+constexpr int GM_KB = 128;  // K bytes per stage
+constexpr int GM_LS = 144;  // padded LDS row stride
 
 __device__ __forceinline__ int4 ld16(const int8_t* p, bool ok) {
   return ok ? *(const int4*)p : int4{0, 0, 0, 0};
 }
 
-// One problem: y[M][O] from xq[M][K] (ld = K), W[O][K]; K % 16 == 0.
-__global__ __launch_bounds__(GM_NT) void k_gemm_q8(const int8_t* __restrict__ xq, const float* __restrict__ sx,
-                                                   const int8_t* __restrict__ W, const float* __restrict__ scale,
-                                                   float* __restrict__ y, int M, int K, int O) {
-  const int lane = threadIdx.x % MOTY_WAVE, wv = threadIdx.x / MOTY_WAVE;
+// y[M][O] from xq[M][K], W[O][K]; K % 16 == 0.  Block tile BM x BN with
+// BM = 64*WM, BN = 64*WN; wave (wm, wn) owns (32*WM) x (32*WN) outputs as
+// WM x WN v_mfma_i32_32x32x32_i8 tiles.  Per 128-byte K block the tile is
+// staged in LDS by whole-line loads (8 lanes x 16 B per row), the next
+// block's loads in flight during the MFMAs.  MFMA step j takes, in lane l,
+// bytes [64*(l/32) + 16j, +16) of row (l % 32): a k-permutation shared by
+// both operands, exact for integer dots.
+template <int WM, int WN>
+__global__ __launch_bounds__(GM_NT, 2) void k_gemm_q8(const int8_t* __restrict__ xq, const float* __restrict__ sx,
+                                                      const int8_t* __restrict__ W, const float* __restrict__ scale,
+                                                      float* __restrict__ y, int M, int K, int O) {
+  constexpr int BM = 64 * WM, BN = 64 * WN;
+  constexpr int NA = BM * 8 / GM_NT, NB = BN * 8 / GM_NT;
+  __shared__ __align__(16) int8_t sA[BM * GM_LS];
+  __shared__ __align__(16) int8_t sB[BN * GM_LS];
+  const int tid = threadIdx.x, lane = tid % MOTY_WAVE, wv = tid / MOTY_WAVE;
   const int wm = wv >> 1, wn = wv & 1;
-  // blockIdx.x walks N tiles fastest so consecutive blocks share the same
-  // activation rows (hot in L2) while streaming different weight rows
-  const int m0 = blockIdx.y * GM_BM + wm * 32;
-  const int n0 = blockIdx.x * GM_BN + wn * 32;
-  const int r16 = lane & 15, kq = (lane >> 4) * 16;
-
-  const int8_t* ap[2];
-  const int8_t* bp[2];
+  const int r32 = lane & 31, h = lane >> 5;
+  // blockIdx.x walks N tiles fastest: consecutive workgroups share activation rows
+  const int mb = blockIdx.y * BM, nb = blockIdx.x * BN;
+  const int col = (tid & 7) * 16;
+  const int8_t* srcA[NA];
+  const int8_t* srcB[NB];
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
-    int m = m0 + i * 16 + r16;
+  for (int i = 0; i < NA; i++) {
+    int m = mb + ((tid + i * GM_NT) >> 3);
     m = m < M ? m : M - 1;
-    ap[i] = xq + (int64_t)m * K + kq;
-    int n = n0 + i * 16 + r16;
+    srcA[i] = xq + (int64_t)m * K + col;
+  }
+#pragma unroll
+  for (int i = 0; i < NB; i++) {
+    int n = nb + ((tid + i * GM_NT) >> 3);
     n = n < O ? n : O - 1;
-    bp[i] = W + (int64_t)n * K + kq;
+    srcB[i] = W + (int64_t)n * K + col;
   }
-  v4i acc[2][2];
+  int4 ra[NA], rb[NB];
+  auto gload = [&](int k0) {
+    const bool ok = (k0 + col) < K;
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+    for (int i = 0; i < NA; i++) ra[i] = ld16(srcA[i] + k0, ok);
 #pragma unroll
-    for (int j = 0; j < 2; j++) acc[i][j] = v4i{0, 0, 0, 0};
-
-  int4 a[2], b[2];
+    for (int i = 0; i < NB; i++) rb[i] = ld16(srcB[i] + k0, ok);
+  };
+  v16i acc[WM][WN];
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
-    a[i] = ld16(ap[i], kq < K);
-    b[i] = ld16(bp[i], kq < K);
-  }
-  for (int k0 = 0; k0 < K; k0 += GM_BK) {
-    int4 an[2], bn[2];
-    const int kn = k0 + GM_BK;
-    const bool ok = (kn + kq) < K;
+  for (int i = 0; i < WM; i++)
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      an[i] = ld16(ap[i] + kn, ok);
-      bn[i] = ld16(bp[i] + kn, ok);
+    for (int j = 0; j < WN; j++) acc[i][j] = v16i{};
+  gload(0);
+  for (int k0 = 0; k0 < K; k0 += GM_KB) {
+#pragma unroll
+    for (int i = 0; i < NA; i++) *(int4*)(sA + ((tid + i * GM_NT) >> 3) * GM_LS + col) = ra[i];
+#pragma unroll
+    for (int i = 0; i < NB; i++) *(int4*)(sB + ((tid + i * GM_NT) >> 3) * GM_LS + col) = rb[i];
+    __syncthreads();
+    if (k0 + GM_KB < K) gload(k0 + GM_KB);
+#pragma unroll
+    for (int st = 0; st < 4; st++) {
+      v4i fa[WM], fb[WN];
+#pragma unroll
+      for (int i = 0; i < WM; i++)
+        fa[i] = *(const v4i*)(sA + (wm * 32 * WM + i * 32 + r32) * GM_LS + h * 64 + 16 * st);
+#pragma unroll
+      for (int j = 0; j < WN; j++)
+        fb[j] = *(const v4i*)(sB + (wn * 32 * WN + j * 32 + r32) * GM_LS + h * 64 + 16 * st);
+#pragma unroll
+      for (int i = 0; i < WM; i++)
+#pragma unroll
+        for (int j = 0; j < WN; j++) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
     }
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-      for (int j = 0; j < 2; j++)
-        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(*(v4i*)&a[i], *(v4i*)&b[j], acc[i][j], 0, 0, 0);
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-      a[i] = an[i];
-      b[i] = bn[i];
-    }
+    __syncthreads();
   }
-  // D layout: lane l holds column (l % 16), rows 4*(l / 16) + r
+  // D layout: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, column l%32
 #pragma unroll
-  for (int j = 0; j < 2; j++) {
-    const int n = n0 + j * 16 + r16;
+  for (int j = 0; j < WN; j++) {
+    const int n = nb + wn * 32 * WN + j * 32 + r32;
     if (n >= O) continue;
     const float sc = scale[n];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < WM; i++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int m = m0 + i * 16 + (lane >> 4) * 4 + r;
+      for (int r = 0; r < 16; r++) {
+        const int m = mb + wm * 32 * WM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
         if (m < M) y[(int64_t)m * O + n] = (sc * sx[m]) * (float)acc[i][j][r];
       }
   }
@@ -99,8 +113,18 @@ int launch_gemm_q8(const int8_t* xq, const float* sx, const int8_t* W, const flo
                    int K, int O, hipStream_t st) {
   if (K % 16) return MOTY_EUNSUP;
   if (M <= 0 || O <= 0) return MOTY_OK;
-  dim3 grid((O + GM_BN - 1) / GM_BN, (M + GM_BM - 1) / GM_BM);
-  hipLaunchKernelGGL(k_gemm_q8, grid, dim3(GM_NT), 0, st, xq, sx, W, scale, y, M, K, O);
+  // largest tile that still yields a workgroup per CU on the 256-CU part
+  auto nblk = [&](int bm, int bn) { return (int64_t)((M + bm - 1) / bm) * ((O + bn - 1) / bn); };
+  if (nblk(128, 128) >= 256) {
+    hipLaunchKernelGGL((k_gemm_q8<2, 2>), dim3((O + 127) / 128, (M + 127) / 128), dim3(GM_NT), 0, st, xq, sx, W,
+                       scale, y, M, K, O);
+  } else if (nblk(64, 128) >= 256) {
+    hipLaunchKernelGGL((k_gemm_q8<1, 2>), dim3((O + 127) / 128, (M + 63) / 64), dim3(GM_NT), 0, st, xq, sx, W,
+                       scale, y, M, K, O);
+  } else {
+    hipLaunchKernelGGL((k_gemm_q8<1, 1>), dim3((O + 63) / 64, (M + 63) / 64), dim3(GM_NT), 0, st, xq, sx, W, scale,
+                       y, M, K, O);
+  }
   LAUNCH_TRY("k_gemm_q8");
   return MOTY_OK;
 }

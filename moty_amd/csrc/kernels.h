@@ -9,8 +9,8 @@
 namespace moty {
 
 constexpr int GEMV_MAX_S = 4;  // token rows served by the decode GEMVs
-constexpr int MOE_BM = 32;     // slots per M-tile of the grouped MoE GEMMs
-constexpr int MOE_NBUF = 14;   // MoE scratch sub-buffers
+constexpr int MOE_BM = 64;     // slots per M-tile of the grouped MoE GEMMs
+constexpr int MOE_NBUF = 15;   // MoE scratch sub-buffers
 
 int launch_qrow_i8(const float* x, int8_t* q, float* sx, int32_t* xg, int S, int I, int64_t ldx, int64_t ldq,
                    hipStream_t st);

@@ -10,10 +10,11 @@
 //   combine   out[t] += w * hh, fused multiply-add (nn/moe.c:200-202 in
 //             ascending expert id; engines/olmoe.c:241-242 in top-k order)
 //
-// Pipeline (5 launches, no host synchronisation):
-//   k_route        one workgroup per token: f32 router logits in the exact
-//                  AVX512 lane order, optional logit bias, softmax, greedy
-//                  top-k, and the token's int8 activation row (qrow_i8)
+// Pipeline (7 launches, no host synchronisation):
+//   k_router_logits  workgroup per (token, 8 experts): f32 router logits in
+//                  the exact AVX512 lane order, optional logit bias, and the
+//                  token's int8 activation row (qrow_i8)
+//   k_route_topk   wave per token: softmax, greedy top-k
 //   k_group        one workgroup: per-expert histogram, exclusive scan, slot
 //                  scatter (pairs grouped by expert), M-tile list
 //   k_moe_gateup   grouped GEMM, v_mfma_i32_32x32x32_i8, gate and up rows of
@@ -31,90 +32,99 @@
 namespace moty {
 
 constexpr int RT_NT = 256;
+constexpr int RT_EPB = RT_NT / 32;  // experts per workgroup (one per half-wave)
 
-// One workgroup per token.  Writes idx[t][K], w[t][K], xq[t][D], sx[t].
-__global__ __launch_bounds__(RT_NT) void k_route(const float* __restrict__ x, const float* __restrict__ Wr,
-                                                 const float* __restrict__ bias, int D, int E, int K, int norm,
-                                                 int* __restrict__ idx, float* __restrict__ wout,
-                                                 int8_t* __restrict__ xq, float* __restrict__ sx,
-                                                 float* __restrict__ probs_out) {
-  extern __shared__ __align__(16) float sm[];
-  float* xs = sm;           // [D]
-  float* pr = sm + D;       // [E]
+// Router logits, workgroup (token t, group of 8 experts).  The x row is
+// staged in LDS; each half-wave computes one expert's dot_f32 in the AVX512
+// order, plus the optional logit bias.  Workgroups of column 0 also write
+// the token's int8 activation row for the expert GEMMs (qrow_i8).
+__global__ __launch_bounds__(RT_NT) void k_router_logits(const float* __restrict__ x, const float* __restrict__ Wr,
+                                                         const float* __restrict__ bias, int D, int E,
+                                                         float* __restrict__ logits, int8_t* __restrict__ xq,
+                                                         float* __restrict__ sx) {
+  extern __shared__ __align__(16) float xs[];  // [D]
   __shared__ float red[RT_NT / MOTY_WAVE];
-  __shared__ int sel[64];
-  __shared__ float selw[64];
   const int t = blockIdx.x;
   const int lane = threadIdx.x % MOTY_WAVE, wv = threadIdx.x / MOTY_WAVE;
   const float* xr = x + (int64_t)t * D;
   float amax = 0.f;
-  for (int i = threadIdx.x; i < D; i += RT_NT) {
-    const float v = xr[i];
-    xs[i] = v;
-    amax = fmaxf(amax, fabsf(v));
+  for (int i = threadIdx.x * 4; i < D; i += RT_NT * 4) {
+    const float4 v = *(const float4*)(xr + i);
+    *(float4*)(xs + i) = v;
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
   }
   amax = wave_max_f32(amax);
   if (lane == 0) red[wv] = amax;
   __syncthreads();
-  // activation row for the expert GEMMs: qrow_i8 (hw/hw_quant.h:9-16)
-  {
+  if (blockIdx.y == 0) {  // qrow_i8 (hw/hw_quant.h:9-16)
     float m = red[0];
     for (int i = 1; i < RT_NT / MOTY_WAVE; i++) m = fmaxf(m, red[i]);
     float s = m / 127.f;
     if (s < 1e-12f) s = 1e-12f;
     const float inv = 1.f / s;
     if (threadIdx.x == 0) sx[t] = s;
-    for (int i = threadIdx.x; i < D; i += RT_NT) xq[(int64_t)t * D + i] = (int8_t)rne_int(xs[i] * inv);
+    for (int i = threadIdx.x * 4; i < D; i += RT_NT * 4) {
+      const float4 v = *(const float4*)(xs + i);
+      const uint32_t p = (uint32_t)(rne_int(v.x * inv) & 0xff) | ((uint32_t)(rne_int(v.y * inv) & 0xff) << 8) |
+                         ((uint32_t)(rne_int(v.z * inv) & 0xff) << 16) | ((uint32_t)(rne_int(v.w * inv) & 0xff) << 24);
+      *(uint32_t*)(xq + (int64_t)t * D + i) = p;
+    }
   }
-  // router logits: each half-wave owns one expert at a time
-  const int half = threadIdx.x / 32, nhalf = RT_NT / 32;
-  for (int e = half; e < E; e += nhalf) {
-    float l = dot_f32_half(xs, Wr + (int64_t)e * D, D);
-    if (bias) l = l + bias[e];
-    if ((threadIdx.x % 32) == 0) pr[e] = l;
-  }
-  __syncthreads();
-  // softmax (wave 0): max is order-free; the sum runs serially in lane 0.
-  // The other waves stay alive for the workgroup barriers below.
+  const int e = blockIdx.y * RT_EPB + threadIdx.x / 32;
+  if (e >= E) return;
+  float l = dot_f32_half(xs, Wr + (int64_t)e * D, D);
+  if (bias) l = l + bias[e];
+  if ((threadIdx.x % 32) == 0) logits[(int64_t)t * E + e] = l;
+}
+
+// Softmax + greedy top-k, one wave per token (nn/norm.c:10 + hw/hw_ops.h:22-26,
+// runtime/moecache.c:97-111): max is order-free, the sum runs serially in
+// lane 0; top-k picks the largest value, lowest index on ties (the strict
+// '>' scan); the normalisation sum is serial over k.
+__global__ __launch_bounds__(MOTY_WAVE) void k_route_topk(const float* __restrict__ logits, int E, int K, int norm,
+                                                          int* __restrict__ idx, float* __restrict__ wout,
+                                                          float* __restrict__ probs_out) {
+  extern __shared__ float pr[];  // [E]
+  __shared__ int sel[64];
+  __shared__ float selw[64];
+  const int t = blockIdx.x, lane = threadIdx.x;
+  const float* lr = logits + (int64_t)t * E;
   float m = -1e30f;
-  if (wv == 0) {
-    for (int e = lane; e < E; e += MOTY_WAVE) m = pr[e] > m ? pr[e] : m;
-    m = wave_max_f32(m);
-    for (int e = lane; e < E; e += MOTY_WAVE) pr[e] = ref_expf(pr[e] - m);
+  for (int e = lane; e < E; e += MOTY_WAVE) {
+    const float v = lr[e];
+    pr[e] = v;
+    m = v > m ? v : m;
   }
+  m = wave_max_f32(m);
+  for (int e = lane; e < E; e += MOTY_WAVE) pr[e] = ref_expf(pr[e] - m);
   __syncthreads();
-  if (wv == 0) {
-    float ssum = 0.f;
-    if (lane == 0)
-      for (int e = 0; e < E; e++) ssum += pr[e];
-    ssum = __shfl(ssum, 0, 64);
-    for (int e = lane; e < E; e += MOTY_WAVE) pr[e] = pr[e] / ssum;
-  }
+  float ssum = 0.f;
+  if (lane == 0)
+    for (int e = 0; e < E; e++) ssum += pr[e];
+  ssum = __shfl(ssum, 0, 64);
+  for (int e = lane; e < E; e += MOTY_WAVE) pr[e] = pr[e] / ssum;
   __syncthreads();
   if (probs_out)
-    for (int e = threadIdx.x; e < E; e += RT_NT) probs_out[(int64_t)t * E + e] = pr[e];
-  // greedy top-k: largest value, lowest index on ties (the strict '>' scan)
+    for (int e = lane; e < E; e += MOTY_WAVE) probs_out[(int64_t)t * E + e] = pr[e];
   for (int kk = 0; kk < K; kk++) {
-    if (wv == 0) {
-      float bv = -1e30f;
-      int be = -1;
-      for (int e = lane; e < E; e += MOTY_WAVE) {
-        bool taken = false;
-        for (int j = 0; j < kk; j++) taken |= (sel[j] == e);
-        const float v = pr[e];
-        if (!taken && v > bv) { bv = v; be = e; }
-      }
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o, 64);
-        const int oe = __shfl_xor(be, o, 64);
-        if (oe >= 0 && (ov > bv || (ov == bv && (be < 0 || oe < be)))) { bv = ov; be = oe; }
-      }
-      if (lane == 0) { sel[kk] = be; selw[kk] = bv; }
+    float bv = -1e30f;
+    int be = -1;
+    for (int e = lane; e < E; e += MOTY_WAVE) {
+      bool taken = false;
+      for (int j = 0; j < kk; j++) taken |= (sel[j] == e);
+      const float v = pr[e];
+      if (!taken && v > bv) { bv = v; be = e; }
     }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, 64);
+      const int oe = __shfl_xor(be, o, 64);
+      if (oe >= 0 && (ov > bv || (ov == bv && (be < 0 || oe < be)))) { bv = ov; be = oe; }
+    }
+    if (lane == 0) { sel[kk] = be; selw[kk] = bv; }
     __syncthreads();
   }
-  if (threadIdx.x == 0) {
+  if (lane == 0) {
     if (norm) {
       float s = 0.f;
       for (int kk = 0; kk < K; kk++) s += selw[kk];
@@ -178,18 +188,28 @@ __global__ __launch_bounds__(GR_NT) void k_group(const int* __restrict__ idx, in
 }
 
 // ---------------------------------------------------------------------------
-// Grouped GEMMs.  Workgroup = 4 waves; each wave computes a 32 (slots) x 32
-// (weight rows) tile with v_mfma_i32_32x32x32_i8; the workgroup covers
-// MOE_BM slots x 128 weight rows of one expert.  Lane l holds A row l%32 and
-// B row l%32, 16 k-bytes at offset 16*(l/32) of each 32-byte K step.
+// Grouped GEMMs.  Workgroup = 4 waves over one (expert, 64-slot M-tile,
+// 128-row N-tile).  Per 128-byte K block the workgroup stages the tile in
+// LDS: every global load instruction reads whole 128 B lines (8 lanes per
+// row, 16 B each) -- activation rows gathered through slot -> token for the
+// gate/up GEMM -- into rows padded to 144 B.  Each wave then owns 32 weight
+// rows (of gate and up, or of down) for both 32-slot halves of the M-tile
+// and runs v_mfma_i32_32x32x32_i8 on fragments read back from LDS.  The next
+// K block's global loads are in flight (in registers) during the MFMAs.
+//
+// Fragment k-order: MFMA step j of a K block takes, in lane l, bytes
+// [64*(l/32) + 16j, +16) of row (l % 32).  An integer dot is order-free, so
+// this k-permutation, shared by A and B, gives the exact sum.
 // D layout: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, column l%32.
 constexpr int MG_NT = 256;
 constexpr int MG_BN = 128;
+constexpr int MG_KB = 128;   // K bytes per stage
+constexpr int MG_LS = 144;   // padded LDS row stride
 
 __device__ __forceinline__ int4 ldg16(const int8_t* p) { return *(const int4*)p; }
 
 template <bool GATEUP>
-__global__ __launch_bounds__(MG_NT) void k_moe_gemm(
+__global__ __launch_bounds__(MG_NT, 2) void k_moe_gemm(
     const int2* __restrict__ tiles, const int* __restrict__ ntiles, const int* __restrict__ offs,
     const int* __restrict__ slot_tok,
     const int8_t* __restrict__ act, const float* __restrict__ act_s,  // GATEUP: xq[T][K], sx[T]; else hq[P][K], sh[P]
@@ -197,54 +217,105 @@ __global__ __launch_bounds__(MG_NT) void k_moe_gemm(
     const int8_t* __restrict__ W2, const float* __restrict__ S2,      // up (GATEUP only)
     float* __restrict__ out,                                          // [P][N]
     int N, int Kd) {
+  constexpr int BROWS = GATEUP ? 2 * MG_BN : MG_BN;  // staged weight rows
+  constexpr int NA = 64 * 8 / MG_NT;                 // 16 B chunks per thread: A
+  constexpr int NBW = BROWS * 8 / MG_NT;             // and B
+  __shared__ __align__(16) int8_t sA[64 * MG_LS];
+  __shared__ __align__(16) int8_t sB[BROWS * MG_LS];
   const int tile = blockIdx.y;
   if (tile >= ntiles[0]) return;
   const int2 tm = tiles[tile];
   const int e = tm.x, mb = tm.y;
   const int seg0 = offs[e], nseg = offs[e + 1] - seg0;
-  const int lane = threadIdx.x % MOTY_WAVE, wv = threadIdx.x / MOTY_WAVE;
-  const int r32 = lane & 31, kq = (lane >> 5) * 16;
-  const int n0 = blockIdx.x * MG_BN + wv * 32;
-  // A row of this lane (clamped inside the segment; extra rows are not stored)
-  int mrow = mb + r32;
-  mrow = mrow < nseg ? mrow : nseg - 1;
-  const int slot = seg0 + mrow;
-  const int64_t arow = GATEUP ? (int64_t)slot_tok[slot] : (int64_t)slot;
-  const int8_t* ap = act + arow * Kd + kq;
-  int nrow = n0 + r32;
-  nrow = nrow < N ? nrow : N - 1;
-  const int8_t* b1 = W1 + ((int64_t)e * N + nrow) * Kd + kq;
-  const int8_t* b2 = GATEUP ? W2 + ((int64_t)e * N + nrow) * Kd + kq : nullptr;
+  const int tid = threadIdx.x, lane = tid % MOTY_WAVE, wv = tid / MOTY_WAVE;
+  const int r32 = lane & 31, h = lane >> 5;
+  const int nb0 = blockIdx.x * MG_BN;
+  const bool two = (nseg - mb) > 32;  // second 32-slot half has rows (uniform)
 
-  v16i acc1 = {}, acc2 = {};
-  int4 a = ldg16(ap), w1 = ldg16(b1), w2 = GATEUP ? ldg16(b2) : int4{0, 0, 0, 0};
-  for (int k0 = 32; k0 <= Kd; k0 += 32) {
-    int4 an = a, w1n = w1, w2n = w2;
-    if (k0 < Kd) {
-      an = ldg16(ap + k0);
-      w1n = ldg16(b1 + k0);
-      if (GATEUP) w2n = ldg16(b2 + k0);
-    }
-    acc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(v4i*)&a, *(v4i*)&w1, acc1, 0, 0, 0);
-    if (GATEUP) acc2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(v4i*)&a, *(v4i*)&w2, acc2, 0, 0, 0);
-    a = an; w1 = w1n; w2 = w2n;
+  // this thread's copy assignments: chunk q -> (row q/8, 16 B column q%8)
+  const int8_t* srcA[NA];
+  const int8_t* srcB[NBW];
+  const int col = (tid & 7) * 16;
+#pragma unroll
+  for (int i = 0; i < NA; i++) {
+    const int row = (tid + i * MG_NT) >> 3;
+    int m = mb + row;
+    m = m < nseg ? m : nseg - 1;
+    const int slot = seg0 + m;
+    const int64_t arow = GATEUP ? (int64_t)slot_tok[slot] : (int64_t)slot;
+    srcA[i] = act + arow * Kd + col;
   }
-  const int ncol = n0 + r32;
+#pragma unroll
+  for (int i = 0; i < NBW; i++) {
+    const int row = (tid + i * MG_NT) >> 3;
+    const int8_t* W = (GATEUP && row >= MG_BN) ? W2 : W1;
+    int n = nb0 + (row & (MG_BN - 1));
+    n = n < N ? n : N - 1;
+    srcB[i] = W + ((int64_t)e * N + n) * Kd + col;
+  }
+  int4 ra[NA], rb[NBW];
+  auto gload = [&](int k0) {
+    const bool ok = (k0 + col) < Kd;  // K % 16 == 0: a chunk is all in or all out
+#pragma unroll
+    for (int i = 0; i < NA; i++) ra[i] = ok ? ldg16(srcA[i] + k0) : int4{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < NBW; i++) rb[i] = ok ? ldg16(srcB[i] + k0) : int4{0, 0, 0, 0};
+  };
+  auto lstore = [&]() {
+#pragma unroll
+    for (int i = 0; i < NA; i++) *(int4*)(sA + ((tid + i * MG_NT) >> 3) * MG_LS + col) = ra[i];
+#pragma unroll
+    for (int i = 0; i < NBW; i++) *(int4*)(sB + ((tid + i * MG_NT) >> 3) * MG_LS + col) = rb[i];
+  };
+
+  v16i acc1[2] = {}, acc2[2] = {};
+  gload(0);
+  for (int k0 = 0; k0 < Kd; k0 += MG_KB) {
+    lstore();
+    __syncthreads();
+    if (k0 + MG_KB < Kd) gload(k0 + MG_KB);  // in flight during the MFMAs below
+    const int8_t* a0 = sA + r32 * MG_LS + h * 64;
+    const int8_t* a1 = a0 + 32 * MG_LS;
+    const int8_t* bg = sB + (wv * 32 + r32) * MG_LS + h * 64;
+    const int8_t* bu = bg + MG_BN * MG_LS;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const v4i fa0 = *(const v4i*)(a0 + 16 * j);
+      const v4i fg = *(const v4i*)(bg + 16 * j);
+      acc1[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0, fg, acc1[0], 0, 0, 0);
+      v4i fu = {};
+      if (GATEUP) {
+        fu = *(const v4i*)(bu + 16 * j);
+        acc2[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0, fu, acc2[0], 0, 0, 0);
+      }
+      if (two) {
+        const v4i fa1 = *(const v4i*)(a1 + 16 * j);
+        acc1[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1, fg, acc1[1], 0, 0, 0);
+        if (GATEUP) acc2[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1, fu, acc2[1], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+  const int ncol = nb0 + wv * 32 + r32;
   if (ncol >= N) return;
   const float s1 = S1[(int64_t)e * N + ncol];
   const float s2 = GATEUP ? S2[(int64_t)e * N + ncol] : 0.f;
 #pragma unroll
-  for (int r = 0; r < 16; r++) {
-    const int m = mb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-    if (m >= nseg) continue;
-    const int sl = seg0 + m;
-    if (GATEUP) {
-      const float sxv = act_s[slot_tok[sl]];
-      const float g = (s1 * sxv) * (float)acc1[r];
-      const float u = (s2 * sxv) * (float)acc2[r];
-      out[(int64_t)sl * N + ncol] = ref_silu_mul(g, u);
-    } else {
-      out[(int64_t)sl * N + ncol] = (s1 * act_s[sl]) * (float)acc1[r];
+  for (int i = 0; i < 2; i++) {
+    if (i == 1 && !two) break;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int m = mb + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+      if (m >= nseg) continue;
+      const int sl = seg0 + m;
+      if (GATEUP) {
+        const float sxv = act_s[slot_tok[sl]];
+        const float g = (s1 * sxv) * (float)acc1[i][r];
+        const float u = (s2 * sxv) * (float)acc2[i][r];
+        out[(int64_t)sl * N + ncol] = ref_silu_mul(g, u);
+      } else {
+        out[(int64_t)sl * N + ncol] = (s1 * act_s[sl]) * (float)acc1[i][r];
+      }
     }
   }
 }
@@ -252,9 +323,9 @@ __global__ __launch_bounds__(MG_NT) void k_moe_gemm(
 // ---------------------------------------------------------------------------
 // out[t][d] = sum over the token's K rows, FMA in the reference's order:
 // order 0 = top-k order (engines/olmoe.c), 1 = ascending expert id (nn/moe.c).
-__global__ void k_moe_combine(const float* __restrict__ y, const int* __restrict__ idx,
-                              const float* __restrict__ w, const int* __restrict__ pair_slot,
-                              float* __restrict__ out, int D, int K, int order) {
+__global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ y, const int* __restrict__ idx,
+                                                     const float* __restrict__ w, const int* __restrict__ pair_slot,
+                                                     float* __restrict__ out, int D, int K, int order) {
   __shared__ int slot_s[64];
   __shared__ float w_s[64];
   const int t = blockIdx.x;
@@ -272,20 +343,27 @@ __global__ void k_moe_combine(const float* __restrict__ y, const int* __restrict
     }
   }
   __syncthreads();
-  for (int d = threadIdx.x * 4; d < D; d += blockDim.x * 4) {
-    float4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int j = 0; j < K; j++) {
-      const int sl = slot_s[j];
-      if (sl < 0) continue;
-      const float wk = w_s[j];
-      const float4 v = *(const float4*)(y + (int64_t)sl * D + d);
-      acc.x = __fmaf_rn(wk, v.x, acc.x);
-      acc.y = __fmaf_rn(wk, v.y, acc.y);
-      acc.z = __fmaf_rn(wk, v.z, acc.z);
-      acc.w = __fmaf_rn(wk, v.w, acc.w);
+  const int d = (blockIdx.y * 256 + threadIdx.x) * 4;
+  if (d >= D) return;
+  float4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int j0 = 0; j0 < K; j0 += 8) {
+    float4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int sl = (j0 + u < K) ? slot_s[j0 + u] : -1;
+      v[u] = sl >= 0 ? *(const float4*)(y + (int64_t)sl * D + d) : float4{0.f, 0.f, 0.f, 0.f};
     }
-    *(float4*)(out + (int64_t)t * D + d) = acc;
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      if (j0 + u >= K || slot_s[j0 + u] < 0) continue;
+      const float wk = w_s[j0 + u];
+      acc.x = __fmaf_rn(wk, v[u].x, acc.x);
+      acc.y = __fmaf_rn(wk, v[u].y, acc.y);
+      acc.z = __fmaf_rn(wk, v[u].z, acc.z);
+      acc.w = __fmaf_rn(wk, v[u].w, acc.w);
+    }
   }
+  *(float4*)(out + (int64_t)t * D + d) = acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -295,7 +373,7 @@ size_t moe_scratch_size(int T, int D, int E, int K, int I, size_t* offsets) {
   size_t sz[MOE_NBUF] = {(size_t)T * D,       (size_t)T * 4,     (size_t)P * 4, (size_t)P * 4,
                          (size_t)(E + 1) * 4, (size_t)P * 4,     (size_t)P * 4, (size_t)maxt * 8,
                          16,                  (size_t)P * I * 4, (size_t)P * I, (size_t)P * 4,
-                         (size_t)P * D * 4,   (size_t)E * 4};
+                         (size_t)P * D * 4,   (size_t)E * 4,     (size_t)T * E * 4};
   size_t o = 0;
   for (int i = 0; i < MOE_NBUF; i++) {
     offsets[i] = o;
@@ -328,11 +406,14 @@ int launch_moe(const MoeArgs& a, void* scratch, hipStream_t st) {
   const int P = T * K;
   const int maxt = P / MOE_BM + E + 1;
 
-  const size_t lds_route = (size_t)(D + E) * 4;
-  if (lds_route > 64 * 1024) return MOTY_EUNSUP;
-  hipLaunchKernelGGL(k_route, dim3(T), dim3(RT_NT), lds_route, st, a.x, a.Wr, a.bias, D, E, K, a.norm, idx, w,
-                     xq, sx, a.probs_out);
-  LAUNCH_TRY("k_route");
+  if ((size_t)D * 4 > 64 * 1024 || (size_t)E * 4 > 64 * 1024) return MOTY_EUNSUP;
+  float* logits = (float*)(b + off[14]);
+  hipLaunchKernelGGL(k_router_logits, dim3(T, (E + RT_EPB - 1) / RT_EPB), dim3(RT_NT), (size_t)D * 4, st, a.x, a.Wr,
+                     a.bias, D, E, logits, xq, sx);
+  LAUNCH_TRY("k_router_logits");
+  hipLaunchKernelGGL(k_route_topk, dim3(T), dim3(MOTY_WAVE), (size_t)E * 4, st, logits, E, K, a.norm, idx, w,
+                     a.probs_out);
+  LAUNCH_TRY("k_route_topk");
   hipLaunchKernelGGL(k_group, dim3(1), dim3(GR_NT), (size_t)(3 * E + 1) * 4, st, idx, P, K, E, offs, slot_tok,
                      pair_slot, tiles, ntiles, counts);
   LAUNCH_TRY("k_group");
@@ -344,7 +425,8 @@ int launch_moe(const MoeArgs& a, void* scratch, hipStream_t st) {
   hipLaunchKernelGGL(k_moe_gemm<false>, dim3((D + MG_BN - 1) / MG_BN, maxt), dim3(MG_NT), 0, st, tiles, ntiles,
                      offs, slot_tok, hq, sh, a.Dn, a.DS, nullptr, nullptr, y, D, I);
   LAUNCH_TRY("k_moe_gemm<down>");
-  hipLaunchKernelGGL(k_moe_combine, dim3(T), dim3(256), 0, st, y, idx, w, pair_slot, a.out, D, K, a.order);
+  hipLaunchKernelGGL(k_moe_combine, dim3(T, (D / 4 + 255) / 256), dim3(256), 0, st, y, idx, w, pair_slot, a.out, D,
+                     K, a.order);
   LAUNCH_TRY("k_moe_combine");
   if (a.idx_out) HIP_TRY(hipMemcpyAsync(a.idx_out, idx, (size_t)P * 4, hipMemcpyDeviceToDevice, st));
   if (a.w_out) HIP_TRY(hipMemcpyAsync(a.w_out, w, (size_t)P * 4, hipMemcpyDeviceToDevice, st));

@@ -49,7 +49,8 @@ def layer(ops, Wr, ex, K, norm, order, bias=None):
 
 
 @pytest.mark.parametrize("E,K,I,D,S", [(16, 4, 128, 256, 24), (8, 2, 64, 64, 1), (64, 8, 1024, 2048, 32),
-                                       (128, 8, 768, 2048, 20), (5, 5, 32, 32, 7)])
+                                       (128, 8, 768, 2048, 20), (5, 5, 32, 32, 7), (8, 2, 64, 128, 300),
+                                       (6, 2, 96, 160, 50)])
 @pytest.mark.parametrize("order", ["batch", "olmoe"])
 def test_moe_layer(ops, E, K, I, D, S, order):
     say("moe", E, K, I, D, S, order)
