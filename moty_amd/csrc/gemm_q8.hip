@@ -24,8 +24,8 @@ __device__ __forceinline__ int4 ld16(const int8_t* p, bool ok) {
 // y[M][O] from xq[M][K], W[O][K]; K % 16 == 0.  Block tile BM x BN with
 // BM = 64*WM, BN = 64*WN; wave (wm, wn) owns (32*WM) x (32*WN) outputs as
 // WM x WN v_mfma_i32_32x32x32_i8 tiles.  Per 128-byte K block the tile is
-// staged in LDS by whole-line loads (8 lanes x 16 B per row), the next
-// block's loads in flight during the MFMAs.  MFMA step j takes, in lane l,
+// staged in LDS by whole-line loads (8 lanes x 16 B per row); two register
+// sets keep the next two blocks' loads in flight during the MFMAs.  MFMA step j takes, in lane l,
 // bytes [64*(l/32) + 16j, +16) of row (l % 32): a k-permutation shared by
 // both operands, exact for integer dots.
 template <int WM, int WN>
@@ -56,8 +56,10 @@ __global__ __launch_bounds__(GM_NT, 2) void k_gemm_q8(const int8_t* __restrict__
     n = n < O ? n : O - 1;
     srcB[i] = W + (int64_t)n * K + col;
   }
-  int4 ra[NA], rb[NB];
-  auto gload = [&](int k0) {
+  // two register sets: while one K block is consumed from LDS, the next two
+  // are in flight from HBM
+  int4 ra0[NA], rb0[NB], ra1[NA], rb1[NB];
+  auto gload = [&](int k0, int4(&ra)[NA], int4(&rb)[NB]) {
     const bool ok = (k0 + col) < K;
 #pragma unroll
     for (int i = 0; i < NA; i++) ra[i] = ld16(srcA[i] + k0, ok);
@@ -69,14 +71,13 @@ __global__ __launch_bounds__(GM_NT, 2) void k_gemm_q8(const int8_t* __restrict__
   for (int i = 0; i < WM; i++)
 #pragma unroll
     for (int j = 0; j < WN; j++) acc[i][j] = v16i{};
-  gload(0);
-  for (int k0 = 0; k0 < K; k0 += GM_KB) {
+  auto stage = [&](int k0, int4(&ra)[NA], int4(&rb)[NB]) {
 #pragma unroll
     for (int i = 0; i < NA; i++) *(int4*)(sA + ((tid + i * GM_NT) >> 3) * GM_LS + col) = ra[i];
 #pragma unroll
     for (int i = 0; i < NB; i++) *(int4*)(sB + ((tid + i * GM_NT) >> 3) * GM_LS + col) = rb[i];
     __syncthreads();
-    if (k0 + GM_KB < K) gload(k0 + GM_KB);
+    if (k0 + 2 * GM_KB < K) gload(k0 + 2 * GM_KB, ra, rb);
 #pragma unroll
     for (int st = 0; st < 4; st++) {
       v4i fa[WM], fb[WN];
@@ -92,6 +93,12 @@ __global__ __launch_bounds__(GM_NT, 2) void k_gemm_q8(const int8_t* __restrict__
         for (int j = 0; j < WN; j++) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
     }
     __syncthreads();
+  };
+  gload(0, ra0, rb0);
+  if (GM_KB < K) gload(GM_KB, ra1, rb1);
+  for (int k0 = 0; k0 < K; k0 += 2 * GM_KB) {
+    stage(k0, ra0, rb0);
+    if (k0 + GM_KB < K) stage(k0 + GM_KB, ra1, rb1);
   }
   // D layout: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, column l%32
 #pragma unroll

@@ -194,8 +194,9 @@ __global__ __launch_bounds__(GR_NT) void k_group(const int* __restrict__ idx, in
 // row, 16 B each) -- activation rows gathered through slot -> token for the
 // gate/up GEMM -- into rows padded to 144 B.  Each wave then owns 32 weight
 // rows (of gate and up, or of down) for both 32-slot halves of the M-tile
-// and runs v_mfma_i32_32x32x32_i8 on fragments read back from LDS.  The next
-// K block's global loads are in flight (in registers) during the MFMAs.
+// and runs v_mfma_i32_32x32x32_i8 on fragments read back from LDS.  Two
+// register sets keep the next two K blocks' global loads in flight during
+// the MFMAs.
 //
 // Fragment k-order: MFMA step j of a K block takes, in lane l, bytes
 // [64*(l/32) + 16j, +16) of row (l % 32).  An integer dot is order-free, so
@@ -253,27 +254,24 @@ __global__ __launch_bounds__(MG_NT, 2) void k_moe_gemm(
     n = n < N ? n : N - 1;
     srcB[i] = W + ((int64_t)e * N + n) * Kd + col;
   }
-  int4 ra[NA], rb[NBW];
-  auto gload = [&](int k0) {
+  // two register sets: while one K block is consumed from LDS, the next two
+  // are in flight from HBM
+  int4 ra0[NA], rb0[NBW], ra1[NA], rb1[NBW];
+  auto gload = [&](int k0, int4(&ra)[NA], int4(&rb)[NBW]) {
     const bool ok = (k0 + col) < Kd;  // K % 16 == 0: a chunk is all in or all out
 #pragma unroll
     for (int i = 0; i < NA; i++) ra[i] = ok ? ldg16(srcA[i] + k0) : int4{0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < NBW; i++) rb[i] = ok ? ldg16(srcB[i] + k0) : int4{0, 0, 0, 0};
   };
-  auto lstore = [&]() {
+  v16i acc1[2] = {}, acc2[2] = {};
+  auto stage = [&](int k0, int4(&ra)[NA], int4(&rb)[NBW]) {
 #pragma unroll
     for (int i = 0; i < NA; i++) *(int4*)(sA + ((tid + i * MG_NT) >> 3) * MG_LS + col) = ra[i];
 #pragma unroll
     for (int i = 0; i < NBW; i++) *(int4*)(sB + ((tid + i * MG_NT) >> 3) * MG_LS + col) = rb[i];
-  };
-
-  v16i acc1[2] = {}, acc2[2] = {};
-  gload(0);
-  for (int k0 = 0; k0 < Kd; k0 += MG_KB) {
-    lstore();
     __syncthreads();
-    if (k0 + MG_KB < Kd) gload(k0 + MG_KB);  // in flight during the MFMAs below
+    if (k0 + 2 * MG_KB < Kd) gload(k0 + 2 * MG_KB, ra, rb);
     const int8_t* a0 = sA + r32 * MG_LS + h * 64;
     const int8_t* a1 = a0 + 32 * MG_LS;
     const int8_t* bg = sB + (wv * 32 + r32) * MG_LS + h * 64;
@@ -295,6 +293,12 @@ __global__ __launch_bounds__(MG_NT, 2) void k_moe_gemm(
       }
     }
     __syncthreads();
+  };
+  gload(0, ra0, rb0);
+  if (MG_KB < Kd) gload(MG_KB, ra1, rb1);
+  for (int k0 = 0; k0 < Kd; k0 += 2 * MG_KB) {
+    stage(k0, ra0, rb0);
+    if (k0 + MG_KB < Kd) stage(k0 + MG_KB, ra1, rb1);
   }
   const int ncol = nb0 + wv * 32 + r32;
   if (ncol >= N) return;
