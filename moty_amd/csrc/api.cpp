@@ -45,6 +45,7 @@ struct Arena {
 
 struct Dev {
   bool ready = false;
+  int cus = 0;  // compute units
   hipStream_t stream = nullptr;
   Arena scratch, io;
   std::unordered_map<const void*, WEntry> wcache;
@@ -65,6 +66,9 @@ static int dev_init(int d) {
   HIP_TRY(hipSetDevice(d));
   std::lock_guard<std::mutex> lk(g_mu);
   if (!g_dev[d].ready) {
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, d));
+    g_dev[d].cus = prop.multiProcessorCount;
     HIP_TRY(hipStreamCreateWithFlags(&g_dev[d].stream, hipStreamNonBlocking));
     g_dev[d].ready = true;
   }

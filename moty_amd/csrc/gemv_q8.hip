@@ -4,7 +4,8 @@
 // -> dot_i8i8 (hw/hw_avx512.h:24-54):
 //     xq[s] = qrow_i8(x[s]);  y[s*O+o] = (scale[o]*sx[s]) * (float)dot(W[o], xq[s])
 //
-// MI355X design (HBM-bound, one pass over W):
+// MI355X design (HBM-bound, one pass over W).  S = 1 with I <= 4096 takes
+// k_gemv1_q8 (activations quantized per wave in registers); otherwise:
 //  * a wave owns RPW weight rows; each lane streams 16 contiguous bytes per
 //    1 KiB chunk of a row (global_load_dwordx4, fully coalesced), up to four
 //    chunks per row in flight;
@@ -25,6 +26,37 @@ constexpr int GEMV_NT = 256;
 constexpr int GEMV_WAVES = GEMV_NT / MOTY_WAVE;
 constexpr int CHUNK = 16 * MOTY_WAVE;  // bytes of a row one wave-load covers
 constexpr int CB = 4;                  // chunks in flight per row
+
+__device__ __forceinline__ int4 ldnt16(const int8_t* p) {
+  const v4i v = __builtin_nontemporal_load((const v4i*)p);
+  return int4{v.x, v.y, v.z, v.w};
+}
+
+// qrow_i8 of a row held across a wave (lane l: 16 values per 1 KiB chunk):
+// the wave-max is the row's amax; returns the scale, int8 values in place.
+template <int NC>
+__device__ __forceinline__ float wave_qrow(const float4 (&v)[NC][4], int4 (&q)[NC]) {
+  float amax = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; c++)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[c][j].x), fabsf(v[c][j].y)), fmaxf(fabsf(v[c][j].z), fabsf(v[c][j].w))));
+  amax = wave_max_f32(amax);
+  float s = amax / 127.f;
+  if (s < 1e-12f) s = 1e-12f;
+  const float inv = 1.f / s;
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    int* qp = (int*)&q[c];
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      qp[j] = (int)((uint32_t)(rne_int(v[c][j].x * inv) & 0xff) | ((uint32_t)(rne_int(v[c][j].y * inv) & 0xff) << 8) |
+                    ((uint32_t)(rne_int(v[c][j].z * inv) & 0xff) << 16) |
+                    ((uint32_t)(rne_int(v[c][j].w * inv) & 0xff) << 24));
+  }
+  return s;
+}
 
 template <int S_, int RPW, bool PAIR>
 __global__ __launch_bounds__(GEMV_NT) void k_gemv_q8(const float* __restrict__ x, const int8_t* __restrict__ W,
@@ -56,8 +88,8 @@ __global__ __launch_bounds__(GEMV_NT) void k_gemv_q8(const float* __restrict__ x
       for (int j = 0; j < CB; j++) {
         const int k = (cb + j) * CHUNK + lane * 16;
         const bool ok = (o < O) && (cb + j < nch) && (k < I);
-        wq[r][j] = ok ? *(const int4*)(W + (int64_t)o * I + k) : int4{0, 0, 0, 0};
-        if (PAIR) wq2[r][j] = ok ? *(const int4*)(W2 + (int64_t)o * I + k) : int4{0, 0, 0, 0};
+        wq[r][j] = ok ? ldnt16(W + (int64_t)o * I + k) : int4{0, 0, 0, 0};
+        if (PAIR) wq2[r][j] = ok ? ldnt16(W2 + (int64_t)o * I + k) : int4{0, 0, 0, 0};
       }
     }
     if (cb == 0) {
@@ -135,6 +167,81 @@ __global__ __launch_bounds__(GEMV_NT) void k_gemv_q8(const float* __restrict__ x
     }
 }
 
+// S = 1, I <= 4096: the activation row never touches LDS.  Lane l of every
+// wave loads elements [c*1024 + 16l, +16) of each 1 KiB chunk c -- exactly
+// its dot inputs -- so a wave-max gives the row's amax and each wave
+// quantizes in registers (qrow_i8 bit for bit), with no workgroup barrier.
+// The activation loads are issued before the weight loads, so waiting for
+// them does not wait for the weights.  Weights stream with non-temporal
+// loads (read once, kept out of the caches' way).
+template <int NC, int RPW, bool PAIR>
+__global__ __launch_bounds__(GEMV_NT) void k_gemv1_q8(const float* __restrict__ x, const int8_t* __restrict__ W,
+                                                      const float* __restrict__ scale,
+                                                      const int8_t* __restrict__ W2,
+                                                      const float* __restrict__ scale2, float* __restrict__ y,
+                                                      int I, int O) {
+  const int lane = threadIdx.x % MOTY_WAVE;
+  const int o0 = (blockIdx.x * GEMV_WAVES + threadIdx.x / MOTY_WAVE) * RPW;
+  float4 xv[NC][4];
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    const int k = c * CHUNK + lane * 16;
+#pragma unroll
+    for (int j = 0; j < 4; j++) xv[c][j] = (k < I) ? *(const float4*)(x + k + 4 * j) : float4{0.f, 0.f, 0.f, 0.f};
+  }
+  int4 wq[RPW][NC], wq2[RPW][NC];
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const int o = o0 + r < O ? o0 + r : O - 1;
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+      const int k = c * CHUNK + lane * 16;
+      wq[r][c] = k < I ? ldnt16(W + (int64_t)o * I + k) : int4{0, 0, 0, 0};
+      if (PAIR) wq2[r][c] = k < I ? ldnt16(W2 + (int64_t)o * I + k) : int4{0, 0, 0, 0};
+    }
+  }
+  int4 xq[NC];
+  const float sx = wave_qrow<NC>(xv, xq);
+  int acc[RPW], acc2[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    acc[r] = 0;
+    acc2[r] = 0;
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+      acc[r] = dot16(wq[r][c], xq[c], acc[r]);
+      if (PAIR) acc2[r] = dot16(wq2[r][c], xq[c], acc2[r]);
+    }
+    acc[r] = wave_sum_i32(acc[r]);
+    if (PAIR) acc2[r] = wave_sum_i32(acc2[r]);
+  }
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const int o = o0 + r;
+    if (lane == r && o < O) {
+      float v = (scale[o] * sx) * (float)acc[r];
+      if (PAIR) v = ref_silu_mul(v, (scale2[o] * sx) * (float)acc2[r]);
+      y[o] = v;
+    }
+  }
+}
+
+template <int NC, bool PAIR>
+static int launch_1(const float* x, const int8_t* W, const float* scale, const int8_t* W2, const float* scale2,
+                    float* y, int I, int O, hipStream_t st) {
+  // rows per wave: keep >= ~2 workgroups per CU on the 256-CU part
+  const int rpw = (O >= 16384) ? 4 : (O >= 8192 ? 2 : 1);
+  auto go = [&](auto kern, int r) {
+    const unsigned nb = (unsigned)((O + GEMV_WAVES * r - 1) / (GEMV_WAVES * r));
+    hipLaunchKernelGGL(kern, dim3(nb), dim3(GEMV_NT), 0, st, x, W, scale, W2, scale2, y, I, O);
+  };
+  if (rpw == 4) go(k_gemv1_q8<NC, 4, PAIR>, 4);
+  else if (rpw == 2) go(k_gemv1_q8<NC, 2, PAIR>, 2);
+  else go(k_gemv1_q8<NC, 1, PAIR>, 1);
+  LAUNCH_TRY("k_gemv1_q8");
+  return MOTY_OK;
+}
+
 template <int S_, bool PAIR>
 static int launch_s(const float* x, const int8_t* W, const float* scale, const int8_t* W2, const float* scale2,
                     float* y, int S, int I, int O, hipStream_t st) {
@@ -160,6 +267,20 @@ int launch_gemv_q8(const float* x, const int8_t* W, const float* scale, const in
   if (S < 1 || S > GEMV_MAX_S || (I % 16) || I > 16384) return MOTY_EUNSUP;
   if (O <= 0) return MOTY_OK;
   const bool pair = (W2 != nullptr);
+  if (S == 1 && I <= 4 * CHUNK) {
+    const int nc = (I + CHUNK - 1) / CHUNK;
+#define CASE1(n)                                                                                             \
+  case n:                                                                                                    \
+    return pair ? launch_1<n, true>(x, W, scale, W2, scale2, y, I, O, st)                                    \
+                : launch_1<n, false>(x, W, scale, W2, scale2, y, I, O, st);
+    switch (nc) {
+      CASE1(1)
+      CASE1(2)
+      CASE1(3)
+      CASE1(4)
+    }
+#undef CASE1
+  }
 #define CASE(n)                                                                              \
   case n:                                                                                    \
     return pair ? launch_s<n, true>(x, W, scale, W2, scale2, y, S, I, O, st)                 \

@@ -22,7 +22,8 @@ def q8(seed, shape):
     return q.reshape(shape), s.reshape(shape[:-1])
 
 
-@pytest.mark.parametrize("S,D,I", [(1, 1024, 3072), (4, 1024, 3072), (9, 256, 512), (1, 64, 32)])
+@pytest.mark.parametrize("S,D,I", [(1, 1024, 3072), (4, 1024, 3072), (9, 256, 512), (1, 64, 32), (1, 2048, 6144),
+                                   (1, 4096, 1024), (1, 1040, 2000)])
 def test_dense_ffn_q8(ops, S, D, I):
     say("dense_ffn", S, D, I)
     G, GS = q8(1, (I, D))
@@ -32,6 +33,41 @@ def test_dense_ffn_q8(ops, S, D, I):
     y = to_np(ops.dense_ffn_q8(to_dev(x), to_dev(G), to_dev(GS), to_dev(U), to_dev(US), to_dev(Dn), to_dev(DS)))
     y2 = o_dense_ffn_q8(x, G, GS, U, US, Dn, DS)
     assert same_bits(y, y2), mismatch(y, y2)
+
+
+def test_dense_ffn_decode_repeated_and_graph(ops):
+    # many back-to-back launches, eager and replayed from a HIP graph (with
+    # eager work between replays), all give the oracle's bits
+    say("ffn repeated")
+    D, I = 1024, 3072
+    G, GS = q8(1, (I, D))
+    U, US = q8(2, (I, D))
+    Dn, DS = q8(3, (D, I))
+    xs = [randn(40 + k, (1, D)) for k in range(4)]
+    ref = [o_dense_ffn_q8(x, G, GS, U, US, Dn, DS) for x in xs]
+    w = [to_dev(a) for a in (G, GS, U, US, Dn, DS)]
+    xd = [to_dev(x) for x in xs]
+    outs = [torch.empty((1, D), device="cuda:0") for _ in xs]
+    for _ in range(25):
+        for x, o in zip(xd, outs):
+            ops.dense_ffn_q8(x, *w, out=o)
+    for o, r in zip(outs, ref):
+        assert same_bits(to_np(o), r)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g):
+            for x, o in zip(xd, outs):
+                ops.dense_ffn_q8(x, *w, out=o)
+    torch.cuda.current_stream().wait_stream(s)
+    for rep in range(5):
+        for o in outs:
+            o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, r in zip(outs, ref):
+            assert same_bits(to_np(o), r), "replay %d" % rep
 
 
 def moe_weights(E, I, D, seed=10):
