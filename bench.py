@@ -37,6 +37,8 @@ def parse():
     ap.add_argument("--quick", action="store_true", help="C1 and C4 only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU reference baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on each CPU baseline sample")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="only launch the dominant kernel on distinct weights and a 64 MiB copy (for rocprofv3 --pmc)")
     return ap.parse_args()
 
 
@@ -100,6 +102,18 @@ class Ctx:
         return e0.elapsed_time(e1) / 1e3 / n, n
 
 
+def pmc_traffic(name):
+    """HBM bytes per launch of a kernel from its committed rocprofv3 PMC
+    summary (profiles/<name>.md, line `traffic_bytes_per_launch: N`)."""
+    try:
+        for line in open(os.path.join(ROOT, "profiles", name + ".md")):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def n_copies(bytes_per_copy, target=1200 << 20, lo=2):
     return max(lo, -(-target // bytes_per_copy))
 
@@ -127,7 +141,7 @@ def bench_c1(c, steps, warmup):
         "workload": "C1 Qwen3-0.6B FFN decode, Q8_0 (fused gate/up GEMV + SiLU, down GEMV), S=1, D=1024, I=3072",
         "gbs": algo / t / 1e9, "ms_per_step": t * 1e3, "steps": n, "algo_bytes": algo,
         "weight_copies": ncopy, "x": x, "w0": copies[0],
-        "kernel": {"name": "k_gemv_q8<1,1,PAIR> gate+up+SiLU", "us": tg * 1e6, "algo_bytes": gu_algo,
+        "kernel": {"name": "k_gemv1_q8<1,1,PAIR> gate+up+SiLU", "us": tg * 1e6, "algo_bytes": gu_algo,
                    "gbs": gu_algo / tg / 1e9},
     }
 
@@ -230,6 +244,29 @@ def bench_c3(c, steps, warmup):
     return {"workload": "C3 8B-dense FFN, grouped int4 g32 (IDOT4=1), D=4096, I=12288, M=1 and M=256", **res}
 
 
+def pmc_probe(c):
+    """For the rocprofv3 --pmc runs behind roofline.traffic: the C1 gate+up
+    GEMV on 8 distinct weight copies (3 rounds), then a plain 64 MiB
+    device-to-device copy whose FETCH_SIZE/WRITE_SIZE calibrate the
+    counters (64 MiB read, 64 MiB written)."""
+    torch, ops = c.torch, c.ops
+    D, I = 1024, 3072
+    g = c.gen(0, 1)
+    copies = [c.q8((I, D), g) + c.q8((I, D), g) for _ in range(8)]
+    x = c.randn((1, D), c.gen(0, 2))
+    h = torch.empty((1, I), device="cuda:0")
+    src = torch.randint(0, 255, (64 << 20,), dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        for w in copies:
+            ops.gate_up_silu_q8(x, w[0], w[1], w[2], w[3], out=h)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log("pmc probe done")
+
+
 # --------------------------------------------------------------------------
 def cpu_baseline(c1, c4, budget):
     """The reference's own CPU kernels (oracle/_ref, kind 'reference'), or the
@@ -311,6 +348,9 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
     c = Ctx(torch, ops)
+    if args.pmc_probe:
+        pmc_probe(c)
+        return
 
     log("C1 decode FFN")
     c1 = bench_c1(c, args.steps, args.warmup)
@@ -358,8 +398,8 @@ def main():
         "data": "synthetic (W ~ N(0,0.02) quantized by the library's QBITS=8 kernels, x ~ N(0,1)); "
                 "weights rotate over %d copies" % c1["weight_copies"],
         "config": {"workload": c1["workload"]},
-        "roofline": dict(roofline("hbm", k["gbs"], HBM_PEAK_GBS, "GB/s"), kernel=k["name"],
-                         kernel_us=round(k["us"], 3)),
+        "roofline": dict(roofline("hbm", k["gbs"], HBM_PEAK_GBS, "GB/s", pmc_traffic("c1_gate_up_gemv_pmc")),
+                         kernel=k["name"], kernel_us=round(k["us"], 3), algo_bytes=k["algo_bytes"]),
         "whole_ffn_roofline": roofline("hbm", c1["gbs"], HBM_PEAK_GBS, "GB/s"),
         "cpu_baseline": cpu,
         "moe": moe,
