@@ -90,7 +90,7 @@ typedef struct MotyHipMoe {
 /* moty_nn_moe_topk_batch (nn/moe.h:38, nn/moe.c:159-208; no shared expert)
  * with combine_order = EXPERT and norm_topk = 1, or the olmoe engine's
  * per-token MoE (engines/olmoe.c:219-244) with combine_order = TOPK.
- * Host pointers; out [S][D]. */
+ * Host pointers; out [S][D].  Served for D, I multiples of 32, E <= 256, K <= 64. */
 int moty_hip_moe_topk(const MotyHipMoe *m, const float *x, int S, float *out);
 
 /* Drop the cached device copy of a host weight buffer (after the caller

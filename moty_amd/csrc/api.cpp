@@ -341,8 +341,8 @@ int moty_hip_moe_topk_dev(const MotyHipMoe* m, const float* x, int S, float* out
   if (m->E <= 0 || m->K <= 0 || m->K > m->E || m->K > 64 || m->I <= 0 || m->D <= 0)
     return set_error("moe_topk: bad shape E=%d K=%d I=%d D=%d", m->E, m->K, m->I, m->D), MOTY_EINVAL;
   if (S == 0) return MOTY_OK;
-  if ((m->D % 32) || (m->I % 32) || m->E > 4096 || (size_t)(m->D + m->E) * 4 > 64 * 1024) {
-    set_error("moe_topk: D=%d I=%d E=%d unsupported (D, I multiples of 32)", m->D, m->I, m->E);
+  if ((m->D % 32) || (m->I % 32) || m->E > 256 || (size_t)(m->D + m->E) * 4 > 64 * 1024) {
+    set_error("moe_topk: D=%d I=%d E=%d unsupported (D, I multiples of 32, E <= 256)", m->D, m->I, m->E);
     return MOTY_EUNSUP;
   }
   size_t offs[MOE_NBUF];

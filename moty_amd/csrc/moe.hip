@@ -11,10 +11,10 @@
 //             ascending expert id; engines/olmoe.c:241-242 in top-k order)
 //
 // Pipeline (7 launches, no host synchronisation):
-//   k_router_logits  workgroup per (token, 8 experts): f32 router logits in
-//                  the exact AVX512 lane order, optional logit bias, and the
-//                  token's int8 activation row (qrow_i8)
-//   k_route_topk   wave per token: softmax, greedy top-k
+//   k_router_logits  tiled f32 GEMM (16 tokens x 16 experts per workgroup)
+//                  keeping dot_f32's AVX512 chain order, plus logit bias
+//   k_route_topk   wave per token: int8 row (qrow_i8), softmax, greedy top-k
+//                  as ranks
 //   k_group        one workgroup: per-expert histogram, exclusive scan, slot
 //                  scatter (pairs grouped by expert), M-tile list
 //   k_moe_gateup   grouped GEMM, v_mfma_i32_32x32x32_i8, gate and up rows of
@@ -31,109 +31,237 @@
 
 namespace moty {
 
-constexpr int RT_NT = 256;
-constexpr int RT_EPB = RT_NT / 32;  // experts per workgroup (one per half-wave)
+// ---------------------------------------------------------------------------
+// Router logits as a tiled f32 GEMM that keeps dot_f32's AVX512 order
+// (nn/matmul.c:15-27 -> hw/hw_avx512.h:231-243): every (token, expert) dot is
+// 32 FMA chains -- chain c takes elements c, c+32, c+64, ... in order (s0[c]
+// for c < 16, s1[c-16] else) -- then s0+s1 and the reduce_add tree.
+// Thread (pair group g, chain c) accumulates chain c of PT x RG_PE
+// (token, expert) pairs; x and router K-chunks are staged in LDS, so each
+// router row is read once per workgroup's tokens and each x row once per
+// RG_TE experts.
+constexpr int RG_NT = 256;                       // 8 pair groups x 32 chains
+constexpr int RG_TE = 16;                        // experts per workgroup
+constexpr int RG_PE = 8;                         // experts per thread
+constexpr int RG_KS = 8;                         // chain steps (of 32 elements) per LDS chunk
+constexpr int RG_KC = RG_KS * 32;                // elements per chunk
+constexpr int RG_LS = RG_KC + 4;                 // padded LDS row (floats)
 
-// Router logits, workgroup (token t, group of 8 experts).  The x row is
-// staged in LDS; each half-wave computes one expert's dot_f32 in the AVX512
-// order, plus the optional logit bias.  Workgroups of column 0 also write
-// the token's int8 activation row for the expert GEMMs (qrow_i8).
-__global__ __launch_bounds__(RT_NT) void k_router_logits(const float* __restrict__ x, const float* __restrict__ Wr,
-                                                         const float* __restrict__ bias, int D, int E,
-                                                         float* __restrict__ logits, int8_t* __restrict__ xq,
-                                                         float* __restrict__ sx) {
-  extern __shared__ __align__(16) float xs[];  // [D]
-  __shared__ float red[RT_NT / MOTY_WAVE];
-  const int t = blockIdx.x;
-  const int lane = threadIdx.x % MOTY_WAVE, wv = threadIdx.x / MOTY_WAVE;
-  const float* xr = x + (int64_t)t * D;
-  float amax = 0.f;
-  for (int i = threadIdx.x * 4; i < D; i += RT_NT * 4) {
-    const float4 v = *(const float4*)(xr + i);
-    *(float4*)(xs + i) = v;
-    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-  }
-  amax = wave_max_f32(amax);
-  if (lane == 0) red[wv] = amax;
-  __syncthreads();
-  if (blockIdx.y == 0) {  // qrow_i8 (hw/hw_quant.h:9-16)
-    float m = red[0];
-    for (int i = 1; i < RT_NT / MOTY_WAVE; i++) m = fmaxf(m, red[i]);
-    float s = m / 127.f;
-    if (s < 1e-12f) s = 1e-12f;
-    const float inv = 1.f / s;
-    if (threadIdx.x == 0) sx[t] = s;
-    for (int i = threadIdx.x * 4; i < D; i += RT_NT * 4) {
-      const float4 v = *(const float4*)(xs + i);
-      const uint32_t p = (uint32_t)(rne_int(v.x * inv) & 0xff) | ((uint32_t)(rne_int(v.y * inv) & 0xff) << 8) |
-                         ((uint32_t)(rne_int(v.z * inv) & 0xff) << 16) | ((uint32_t)(rne_int(v.w * inv) & 0xff) << 24);
-      *(uint32_t*)(xq + (int64_t)t * D + i) = p;
-    }
-  }
-  const int e = blockIdx.y * RT_EPB + threadIdx.x / 32;
-  if (e >= E) return;
-  float l = dot_f32_half(xs, Wr + (int64_t)e * D, D);
-  if (bias) l = l + bias[e];
-  if ((threadIdx.x % 32) == 0) logits[(int64_t)t * E + e] = l;
-}
-
-// Softmax + greedy top-k, one wave per token (nn/norm.c:10 + hw/hw_ops.h:22-26,
-// runtime/moecache.c:97-111): max is order-free, the sum runs serially in
-// lane 0; top-k picks the largest value, lowest index on ties (the strict
-// '>' scan); the normalisation sum is serial over k.
-__global__ __launch_bounds__(MOTY_WAVE) void k_route_topk(const float* __restrict__ logits, int E, int K, int norm,
-                                                          int* __restrict__ idx, float* __restrict__ wout,
-                                                          float* __restrict__ probs_out) {
-  extern __shared__ float pr[];  // [E]
-  __shared__ int sel[64];
-  __shared__ float selw[64];
-  const int t = blockIdx.x, lane = threadIdx.x;
-  const float* lr = logits + (int64_t)t * E;
-  float m = -1e30f;
-  for (int e = lane; e < E; e += MOTY_WAVE) {
-    const float v = lr[e];
-    pr[e] = v;
-    m = v > m ? v : m;
-  }
-  m = wave_max_f32(m);
-  for (int e = lane; e < E; e += MOTY_WAVE) pr[e] = ref_expf(pr[e] - m);
-  __syncthreads();
-  float ssum = 0.f;
-  if (lane == 0)
-    for (int e = 0; e < E; e++) ssum += pr[e];
-  ssum = __shfl(ssum, 0, 64);
-  for (int e = lane; e < E; e += MOTY_WAVE) pr[e] = pr[e] / ssum;
-  __syncthreads();
-  if (probs_out)
-    for (int e = lane; e < E; e += MOTY_WAVE) probs_out[(int64_t)t * E + e] = pr[e];
-  for (int kk = 0; kk < K; kk++) {
-    float bv = -1e30f;
-    int be = -1;
-    for (int e = lane; e < E; e += MOTY_WAVE) {
-      bool taken = false;
-      for (int j = 0; j < kk; j++) taken |= (sel[j] == e);
-      const float v = pr[e];
-      if (!taken && v > bv) { bv = v; be = e; }
+// PT tokens per thread; workgroup = 4*PT tokens x RG_TE experts.  The next
+// K chunk's global loads are held in registers while the current chunk is
+// consumed from LDS.
+template <int PT>
+__global__ __launch_bounds__(RG_NT) void k_router_logits(const float* __restrict__ x, const float* __restrict__ Wr,
+                                                         const float* __restrict__ bias, int T, int D, int E,
+                                                         float* __restrict__ logits) {
+  constexpr int TT = 4 * PT;
+  constexpr int NX = TT * (RG_KC / 4) / RG_NT;      // float4 per thread per chunk: x
+  constexpr int NW = RG_TE * (RG_KC / 4) / RG_NT;   // and router
+  __shared__ __align__(16) float xs[TT * RG_LS];
+  __shared__ __align__(16) float ws[RG_TE * RG_LS];
+  const int tb = blockIdx.x * TT, eb = blockIdx.y * RG_TE;
+  const int c = threadIdx.x % 32, g = threadIdx.x / 32;
+  const int tq = (g % 4) * PT;        // this thread's tokens tb+tq..
+  const int eq = (g / 4) * RG_PE;     // and experts eb+eq..
+  float acc[PT][RG_PE];
+#pragma unroll
+  for (int i = 0; i < PT; i++)
+#pragma unroll
+    for (int j = 0; j < RG_PE; j++) acc[i][j] = 0.f;
+  const int nsteps = D / 32;  // D % 32 == 0
+  float4 rx[NX], rw[NW];
+  auto gload = [&](int st0) {
+    const int k0 = st0 * 32, kn = ((nsteps - st0) < RG_KS ? (nsteps - st0) : RG_KS) * 32;
+#pragma unroll
+    for (int i = 0; i < NX; i++) {
+      const int q = threadIdx.x + i * RG_NT, r = q / (RG_KC / 4), k = (q % (RG_KC / 4)) * 4;
+      rx[i] = (k < kn && tb + r < T) ? *(const float4*)(x + (int64_t)(tb + r) * D + k0 + k)
+                                     : float4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, 64);
-      const int oe = __shfl_xor(be, o, 64);
-      if (oe >= 0 && (ov > bv || (ov == bv && (be < 0 || oe < be)))) { bv = ov; be = oe; }
+    for (int i = 0; i < NW; i++) {
+      const int q = threadIdx.x + i * RG_NT, r = q / (RG_KC / 4), k = (q % (RG_KC / 4)) * 4;
+      rw[i] = (k < kn && eb + r < E) ? *(const float4*)(Wr + (int64_t)(eb + r) * D + k0 + k)
+                                     : float4{0.f, 0.f, 0.f, 0.f};
     }
-    if (lane == 0) { sel[kk] = be; selw[kk] = bv; }
+  };
+  gload(0);
+  for (int st0 = 0; st0 < nsteps; st0 += RG_KS) {
+    const int ns = (nsteps - st0) < RG_KS ? (nsteps - st0) : RG_KS;
     __syncthreads();
-  }
-  if (lane == 0) {
-    if (norm) {
-      float s = 0.f;
-      for (int kk = 0; kk < K; kk++) s += selw[kk];
-      if (s > 0)
-        for (int kk = 0; kk < K; kk++) selw[kk] = selw[kk] / s;
+#pragma unroll
+    for (int i = 0; i < NX; i++) {
+      const int q = threadIdx.x + i * RG_NT;
+      *(float4*)(xs + (q / (RG_KC / 4)) * RG_LS + (q % (RG_KC / 4)) * 4) = rx[i];
     }
+#pragma unroll
+    for (int i = 0; i < NW; i++) {
+      const int q = threadIdx.x + i * RG_NT;
+      *(float4*)(ws + (q / (RG_KC / 4)) * RG_LS + (q % (RG_KC / 4)) * 4) = rw[i];
+    }
+    __syncthreads();
+    if (st0 + RG_KS < nsteps) gload(st0 + RG_KS);
+    auto step = [&](int u) {
+      float xv[PT], wv[RG_PE];
+#pragma unroll
+      for (int i = 0; i < PT; i++) xv[i] = xs[(tq + i) * RG_LS + u * 32 + c];
+#pragma unroll
+      for (int j = 0; j < RG_PE; j++) wv[j] = ws[(eq + j) * RG_LS + u * 32 + c];
+#pragma unroll
+      for (int i = 0; i < PT; i++)
+#pragma unroll
+        for (int j = 0; j < RG_PE; j++) acc[i][j] = __fmaf_rn(xv[i], wv[j], acc[i][j]);
+    };
+    if (ns == RG_KS) {
+#pragma unroll
+      for (int u = 0; u < RG_KS; u++) step(u);
+    } else {
+      for (int u = 0; u < ns; u++) step(u);
+    }
+  }
+  // s0[c] + s1[c], then the 16-lane reduce_add tree, per pair
+  const int base = (threadIdx.x % MOTY_WAVE) & 32;
+#pragma unroll
+  for (int i = 0; i < PT; i++)
+#pragma unroll
+    for (int j = 0; j < RG_PE; j++) {
+      const float t2 = acc[i][j] + __shfl(acc[i][j], base + ((c + 16) & 31), 64);
+      float r = hsum16_half(t2, base);
+      const int t = tb + tq + i, e = eb + eq + j;
+      if (c == 0 && t < T && e < E) {
+        if (bias) r = r + bias[e];
+        logits[(int64_t)t * E + e] = r;
+      }
+    }
+}
+
+constexpr int TK_NT = 256;  // two waves per token: routing, and the token's int8 row
+constexpr int TK_PV = 4;    // probabilities per lane (E <= 256)
+
+// Per token, two waves: one writes the int8 activation row for the expert
+// GEMMs (qrow_i8, hw/hw_quant.h:9-16); the other runs softmax (nn/norm.c:10 ->
+// hw/hw_ops.h:22-26: max order-free, sum serial in expert order, per-element
+// divide) and greedy top-k (runtime/moecache.c:97-111) as ranks: the rank of
+// expert e under (p desc, index asc); ranks 0..K-1 are the greedy picks of
+// the strict '>' scan, in order.  Normalisation sum serial over k.
+__global__ __launch_bounds__(TK_NT) void k_route_topk(const float* __restrict__ x, const float* __restrict__ logits,
+                                                      int T, int D, int E, int K, int norm, int* __restrict__ idx,
+                                                      float* __restrict__ wout, int8_t* __restrict__ xq,
+                                                      float* __restrict__ sx, float* __restrict__ probs_out) {
+  extern __shared__ float prs[];  // [TK_NT/128][E]
+  __shared__ int sel[TK_NT / 128][64];
+  __shared__ float selw[TK_NT / 128][64];
+  const int lane = threadIdx.x % MOTY_WAVE, wv = (threadIdx.x / MOTY_WAVE) >> 1;
+  const int t = blockIdx.x * (TK_NT / 128) + wv;
+  if (t >= T) return;  // whole wave; no workgroup barrier in this kernel
+  float* p = prs + wv * E;
+  if ((threadIdx.x / MOTY_WAVE) & 1) {  // qrow_i8 of x[t]
+    const float* xr = x + (int64_t)t * D;
+    float amax = 0.f;
+    for (int i = lane * 4; i < D; i += MOTY_WAVE * 4) {
+      const float4 v = *(const float4*)(xr + i);
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    amax = wave_max_f32(amax);
+    float s = amax / 127.f;
+    if (s < 1e-12f) s = 1e-12f;
+    const float inv = 1.f / s;
+    if (lane == 0) sx[t] = s;
+    for (int i = lane * 4; i < D; i += MOTY_WAVE * 4) {
+      const float4 v = *(const float4*)(xr + i);
+      const uint32_t q = (uint32_t)(rne_int(v.x * inv) & 0xff) | ((uint32_t)(rne_int(v.y * inv) & 0xff) << 8) |
+                         ((uint32_t)(rne_int(v.z * inv) & 0xff) << 16) | ((uint32_t)(rne_int(v.w * inv) & 0xff) << 24);
+      *(uint32_t*)(xq + (int64_t)t * D + i) = q;
+    }
+    return;
+  }
+  float pv[TK_PV];
+#pragma unroll
+  for (int j = 0; j < TK_PV; j++) pv[j] = (lane + 64 * j < E) ? logits[(int64_t)t * E + lane + 64 * j] : -1e30f;
+  float m = -1e30f;
+#pragma unroll
+  for (int j = 0; j < TK_PV; j++) m = pv[j] > m ? pv[j] : m;
+  m = wave_max_f32(m);
+#pragma unroll
+  for (int j = 0; j < TK_PV; j++)
+    if (lane + 64 * j < E) p[lane + 64 * j] = ref_expf(pv[j] - m);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float ssum = 0.f;  // serial in expert order (every lane runs it; reads batched)
+  {
+    int e = 0;
+    for (; e + 16 <= E; e += 16) {
+      float v[16];
+#pragma unroll
+      for (int u = 0; u < 16; u++) v[u] = p[e + u];
+#pragma unroll
+      for (int u = 0; u < 16; u++) ssum += v[u];
+    }
+    for (; e < E; e++) ssum += p[e];
+  }
+#pragma unroll
+  for (int j = 0; j < TK_PV; j++) pv[j] = (lane + 64 * j < E) ? p[lane + 64 * j] / ssum : 0.f;
+  if (probs_out)
+#pragma unroll
+    for (int j = 0; j < TK_PV; j++)
+      if (lane + 64 * j < E) probs_out[(int64_t)t * E + lane + 64 * j] = pv[j];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int j = 0; j < TK_PV; j++)
+    if (lane + 64 * j < E) p[lane + 64 * j] = pv[j];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // branch-free compares: rank += (u > v) | (u == v & j < e)
+  const int npv = (E + 63) / 64;
+  int rank[TK_PV];
+#pragma unroll
+  for (int j = 0; j < TK_PV; j++) rank[j] = 0;
+  {
+    int e = 0;
+    for (; e + 16 <= E; e += 16) {
+      float v[16];
+#pragma unroll
+      for (int u = 0; u < 16; u++) v[u] = p[e + u];
+#pragma unroll
+      for (int j = 0; j < TK_PV; j++) {
+        if (j >= npv) break;  // wave-uniform
+        const int me = lane + 64 * j;
+#pragma unroll
+        for (int u = 0; u < 16; u++)
+          rank[j] += (int)(v[u] > pv[j]) | ((int)(v[u] == pv[j]) & (int)(e + u < me));
+      }
+    }
+    for (; e < E; e++) {
+      const float u = p[e];
+#pragma unroll
+      for (int j = 0; j < TK_PV; j++)
+        rank[j] += (int)(u > pv[j]) | ((int)(u == pv[j]) & (int)(e < lane + 64 * j));
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < TK_PV; j++) {
+    const int e = lane + 64 * j;
+    if (e < E && rank[j] < K) {
+      sel[wv][rank[j]] = e;
+      selw[wv][rank[j]] = pv[j];
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (lane == 0) {
+    float ws = 0.f;
+    if (norm)
+      for (int kk = 0; kk < K; kk++) ws += selw[wv][kk];
     for (int kk = 0; kk < K; kk++) {
-      idx[(int64_t)t * K + kk] = sel[kk];
-      wout[(int64_t)t * K + kk] = selw[kk];
+      float v = selw[wv][kk];
+      if (norm && ws > 0) v = v / ws;
+      idx[(int64_t)t * K + kk] = sel[wv][kk];
+      wout[(int64_t)t * K + kk] = v;
     }
   }
 }
@@ -333,17 +461,20 @@ __global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ y
   __shared__ int slot_s[64];
   __shared__ float w_s[64];
   const int t = blockIdx.x;
-  if (threadIdx.x == 0) {
-    int ord[64];
-    for (int k = 0; k < K; k++) ord[k] = k;
-    if (order == 1)
-      for (int a = 1; a < K; a++)
-        for (int b = a; b > 0 && idx[t * K + ord[b]] < idx[t * K + ord[b - 1]]; b--) {
-          const int tmp = ord[b]; ord[b] = ord[b - 1]; ord[b - 1] = tmp;
-        }
-    for (int j = 0; j < K; j++) {
-      slot_s[j] = pair_slot[t * K + ord[j]];
-      w_s[j] = w[t * K + ord[j]];
+  if (threadIdx.x < MOTY_WAVE) {
+    // lane k < K places pair k at its rank: k itself (top-k order) or the
+    // number of the token's experts with a smaller id (ascending id; the K
+    // ids of a token are distinct)
+    const int k = threadIdx.x;
+    const int e = k < K ? idx[t * K + k] : 0x7fffffff;
+    int rank = k;
+    if (order == 1) {
+      rank = 0;
+      for (int j = 0; j < K; j++) rank += (__shfl(e, j, 64) < e) ? 1 : 0;
+    }
+    if (k < K) {
+      slot_s[rank] = pair_slot[t * K + k];
+      w_s[rank] = w[t * K + k];
     }
   }
   __syncthreads();
@@ -410,12 +541,19 @@ int launch_moe(const MoeArgs& a, void* scratch, hipStream_t st) {
   const int P = T * K;
   const int maxt = P / MOE_BM + E + 1;
 
-  if ((size_t)D * 4 > 64 * 1024 || (size_t)E * 4 > 64 * 1024) return MOTY_EUNSUP;
+  if (E > 64 * TK_PV) return MOTY_EUNSUP;
   float* logits = (float*)(b + off[14]);
-  hipLaunchKernelGGL(k_router_logits, dim3(T, (E + RT_EPB - 1) / RT_EPB), dim3(RT_NT), (size_t)D * 4, st, a.x, a.Wr,
-                     a.bias, D, E, logits, xq, sx);
+  // 8-token tiles while that still leaves few workgroups per CU, 16 beyond
+  // (halves the router re-reads)
+  if ((int64_t)((T + 7) / 8) * ((E + RG_TE - 1) / RG_TE) <= 512)
+    hipLaunchKernelGGL(k_router_logits<2>, dim3((T + 7) / 8, (E + RG_TE - 1) / RG_TE), dim3(RG_NT), 0, st, a.x, a.Wr,
+                       a.bias, T, D, E, logits);
+  else
+    hipLaunchKernelGGL(k_router_logits<4>, dim3((T + 15) / 16, (E + RG_TE - 1) / RG_TE), dim3(RG_NT), 0, st, a.x,
+                       a.Wr, a.bias, T, D, E, logits);
   LAUNCH_TRY("k_router_logits");
-  hipLaunchKernelGGL(k_route_topk, dim3(T), dim3(MOTY_WAVE), (size_t)E * 4, st, logits, E, K, a.norm, idx, w,
+  hipLaunchKernelGGL(k_route_topk, dim3((T + TK_NT / 128 - 1) / (TK_NT / 128)), dim3(TK_NT),
+                     (size_t)(TK_NT / 128) * E * 4, st, a.x, logits, T, D, E, K, a.norm, idx, w, xq, sx,
                      a.probs_out);
   LAUNCH_TRY("k_route_topk");
   hipLaunchKernelGGL(k_group, dim3(1), dim3(GR_NT), (size_t)(3 * E + 1) * 4, st, idx, P, K, E, offs, slot_tok,

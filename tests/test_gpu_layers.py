@@ -104,6 +104,24 @@ def test_moe_layer(ops, E, K, I, D, S, order):
     assert same_bits(to_np(y), y2), mismatch(to_np(y), y2)
 
 
+@pytest.mark.parametrize("order", ["batch", "olmoe"])
+def test_moe_routing_ties(ops, order):
+    # duplicated router rows give exactly equal logits and probabilities:
+    # the greedy top-k must take the lower expert id first (strict '>')
+    E, K, I, D, S = 16, 5, 32, 64, 33
+    Wr = randn(7, (E // 2, D), 0.02)
+    Wr = np.repeat(Wr, 2, axis=0)
+    x = randn(8, (S, D))
+    ex = moe_weights(E, I, D, seed=30)
+    from moty_amd import ORDER_EXPERT, ORDER_TOPK
+    norm = 1 if order == "batch" else 0
+    L = layer(ops, Wr, ex, K, norm, ORDER_EXPERT if order == "batch" else ORDER_TOPK)
+    y, idx, w, cnt = L(to_dev(x), want_routing=True)
+    y2, idx2, w2 = o_moe(x, Wr, ex, K, order, norm=norm)
+    assert (to_np(idx) == idx2).all() and same_bits(to_np(w), w2)
+    assert same_bits(to_np(y), y2)
+
+
 def test_moe_skewed_bias(ops):
     # +2.0 on 8 hot experts' logits (the skewed continuous-batch variant)
     E, K, I, D, S = 32, 4, 64, 128, 40
