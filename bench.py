@@ -230,9 +230,12 @@ def bench_c3(c, steps, warmup):
 
         def step(w):
             def f():
-                ops.matmul_i4_grouped_s(x, w[0][0], w[0][1], out=gy)
-                ops.matmul_i4_grouped_s(x, w[1][0], w[1][1], out=uy)
-                ops.silu_mul(gy, uy)
+                if M == 1:  # decode: fused gate+up+SiLU GEMV, then down
+                    ops.gate_up_silu_i4g(x, w[0][0], w[0][1], w[1][0], w[1][1], out=gy)
+                else:
+                    ops.matmul_i4_grouped_s(x, w[0][0], w[0][1], out=gy)
+                    ops.matmul_i4_grouped_s(x, w[1][0], w[1][1], out=uy)
+                    ops.silu_mul(gy, uy)
                 ops.matmul_i4_grouped_s(gy, w[2][0], w[2][1], out=y)
             return f
         t, n = c.time_steps([step(w) for w in copies], max(8, steps // (8 if M == 1 else 64)), 8)

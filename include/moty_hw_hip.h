@@ -140,6 +140,10 @@ int moty_hip_dense_ffn_q8_dev(float *out, const float *x, int S, const int8_t *g
  * gate_up + silu_rows step of nn/ffn.c:28-37.  S <= 4. */
 int moty_hip_gate_up_silu_q8_dev(float *h, const float *x, int S, const int8_t *gate, const float *gs,
                                  const int8_t *up, const float *us, int D, int I, void *stream);
+/* The same fused decode step over grouped-int4 weights (gs = 32, IDOT4 int8
+ * activations): h [I] = silu(x.gate^T) * (x.up^T), one token, D % 64 == 0. */
+int moty_hip_gate_up_silu_i4g_dev(float *h, const float *x, const uint8_t *gate, const float *gs,
+                                  const uint8_t *up, const float *us, int D, int I, void *stream);
 /* the MoE layer, all pointers in m and x/out on the device */
 int moty_hip_moe_topk_dev(const MotyHipMoe *m, const float *x, int S, float *out, void *stream);
 

@@ -246,7 +246,7 @@ int moty_hip_matmul_i4_grouped_s_dev(float* y, const float* x, const uint8_t* q4
   if (S == 0 || O == 0) return MOTY_OK;
   hipStream_t st = STREAM(stream);
   if (idot4 && gs == 32 && (I % 64) == 0 && I <= 16384) {
-    if (S <= 4) return launch_gemv_i4g(x, q4, scale, y, S, I, O, st);
+    if (S <= 4) return launch_gemv_i4g(x, q4, scale, nullptr, nullptr, y, S, I, O, st);
     void* sp;
     const size_t xb = al256((size_t)S * I);
     int rc = arena_get(d->scratch, xb + al256((size_t)S * 4), &sp);
@@ -297,6 +297,16 @@ int moty_hip_gate_up_silu_q8_dev(float* h, const float* x, int S, const int8_t* 
     return MOTY_EUNSUP;
   }
   return launch_gemv_q8(x, gate, gs, up, us, h, S, D, I, STREAM(stream));
+}
+
+int moty_hip_gate_up_silu_i4g_dev(float* h, const float* x, const uint8_t* gate, const float* gs,
+                                  const uint8_t* up, const float* us, int D, int I, void* stream) {
+  CUR(d);
+  if (D <= 0 || I <= 0 || !h || !x || !gate || !gs || !up || !us)
+    return set_error("gate_up_silu_i4g: bad arguments"), MOTY_EINVAL;
+  int rc = launch_gemv_i4g(x, gate, gs, up, us, h, 1, D, I, STREAM(stream));
+  if (rc == MOTY_EUNSUP) set_error("gate_up_silu_i4g: D=%d unsupported (D %% 64 == 0, D <= 16384)", D);
+  return rc;
 }
 
 int moty_hip_dense_ffn_q8_dev(float* out, const float* x, int S, const int8_t* gate, const float* gs,

@@ -22,8 +22,9 @@ int launch_gemv_q8(const float* x, const int8_t* W, const float* scale, const in
 int launch_gemm_q8(const int8_t* xq, const float* sx, const int8_t* W, const float* scale, float* y, int M, int K,
                    int O, hipStream_t st);
 
-int launch_gemv_i4g(const float* x, const uint8_t* q4, const float* scl, float* y, int S, int I, int O,
-                    hipStream_t st);
+// q4b/sclb non-null: PAIR mode (S = 1), y = silu(x.q4^T) * (x.q4b^T)
+int launch_gemv_i4g(const float* x, const uint8_t* q4, const float* scl, const uint8_t* q4b, const float* sclb,
+                    float* y, int S, int I, int O, hipStream_t st);
 int launch_gemm_i4g(const int8_t* xq, const float* sx, const uint8_t* q4, const float* scl, float* y, int M, int I,
                     int O, hipStream_t st);
 int launch_i4g_f32(const float* x, const uint8_t* q4, const float* scl, float* y, int S, int I, int O,

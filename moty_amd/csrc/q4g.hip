@@ -105,6 +105,136 @@ __global__ __launch_bounds__(Q4V_NT) void k_gemv_i4g(const float* __restrict__ x
 }
 
 // ---------------------------------------------------------------------------
+// IDOT4 GEMV for decode (S = 1), optionally PAIR (gate + up + SiLU).
+// Workgroup = 4 waves; a wave owns RW consecutive output rows (of W, and of
+// W2 in PAIR mode):
+//   1. it issues every nibble load of its rows first -- lane l takes groups
+//      l, l+64, ... (16 B each, coalesced along the row);
+//   2. the workgroup quantizes x into LDS (qrow_i8) while those loads fly;
+//   3. each lane forms its groups' exact integer dots sum (n-8)*x and parks
+//      them, with the group scales, in the wave's LDS slice;
+//   4. one lane per row runs the reference's FMA chain over the groups in
+//      order; y = sx * acc (PAIR: h = silu(g) * u).
+template <int RW, int NGC, bool PAIR, int NT>
+__global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, const uint8_t* __restrict__ q4,
+                                                      const float* __restrict__ scl,
+                                                      const uint8_t* __restrict__ q4b,
+                                                      const float* __restrict__ sclb, float* __restrict__ y, int I,
+                                                      int O) {
+  constexpr int NM = PAIR ? 2 : 1;
+  constexpr int WAVES = NT / MOTY_WAVE;
+  constexpr int XV = (NGC * 64 * 32) / (NT * 4);  // float4 of x per thread (I <= 2048 * NGC)
+  extern __shared__ __align__(16) int8_t lds[];
+  __shared__ float red[WAVES];
+  __shared__ float sx_s;
+  const int lane = threadIdx.x % MOTY_WAVE, wv = threadIdx.x / MOTY_WAVE;
+  const int ng = I / 32, rb = I / 2, ldv = ng + 2;  // ldv even: float2 rows stay 8-byte aligned
+  int8_t* xq_s = lds;                                                          // [I]
+  float2* dv = (float2*)(lds + I) + (size_t)wv * (NM * RW * ldv);               // [NM*RW][ldv] (scale, dot)
+  const int o0 = (blockIdx.x * WAVES + wv) * RW;
+
+  // 1. x (one pass, kept in registers), then every nibble load of this wave
+  float4 xr[XV];
+#pragma unroll
+  for (int j = 0; j < XV; j++) {
+    const int i = (threadIdx.x + j * NT) * 4;
+    xr[j] = i < I ? *(const float4*)(x + i) : float4{0.f, 0.f, 0.f, 0.f};
+  }
+  int4 wb[NM][RW][NGC];
+  float wsc[NM][RW][NGC];  // group scales, loaded with the nibbles
+#pragma unroll
+  for (int m = 0; m < NM; m++)
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+      const int64_t o = o0 + r < O ? o0 + r : O - 1;
+      const uint8_t* base = (m ? q4b : q4) + o * rb;
+      const float* sbase = (m ? sclb : scl) + o * ng;
+#pragma unroll
+      for (int c = 0; c < NGC; c++) {
+        const int g = c * 64 + lane;
+        wb[m][r][c] = g < ng ? *(const int4*)(base + g * 16) : int4{0, 0, 0, 0};
+        wsc[m][r][c] = g < ng ? sbase[g] : 0.f;
+      }
+    }
+  // 2. qrow_i8 of x into LDS
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < XV; j++)
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(xr[j].x), fabsf(xr[j].y)), fmaxf(fabsf(xr[j].z), fabsf(xr[j].w))));
+  amax = wave_max_f32(amax);
+  if (lane == 0) red[wv] = amax;
+  __syncthreads();
+  {
+    float mx = red[0];
+#pragma unroll
+    for (int i = 1; i < WAVES; i++) mx = fmaxf(mx, red[i]);
+    float sc = mx / 127.f;
+    if (sc < 1e-12f) sc = 1e-12f;
+    const float inv = 1.f / sc;
+    if (threadIdx.x == 0) sx_s = sc;
+#pragma unroll
+    for (int j = 0; j < XV; j++) {
+      const int i = (threadIdx.x + j * NT) * 4;
+      const float4 v = xr[j];
+      if (i < I)
+        *(uint32_t*)(xq_s + i) = (uint32_t)(rne_int(v.x * inv) & 0xff) | ((uint32_t)(rne_int(v.y * inv) & 0xff) << 8) |
+                                 ((uint32_t)(rne_int(v.z * inv) & 0xff) << 16) |
+                                 ((uint32_t)(rne_int(v.w * inv) & 0xff) << 24);
+    }
+  }
+  __syncthreads();
+  // 3. exact group dots with their group scales into the wave's LDS slice
+#pragma unroll
+  for (int c = 0; c < NGC; c++) {
+    const int g = c * 64 + lane;
+    if (g >= ng) break;
+    const int4 x0 = *(const int4*)(xq_s + g * 32);
+    const int4 x1 = *(const int4*)(xq_s + g * 32 + 16);
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+#pragma unroll
+      for (int r = 0; r < RW; r++) {
+        const int4 w = wb[m][r][c];
+        const int4 w0 = unpack_nib16(uint2{(uint32_t)w.x, (uint32_t)w.y});
+        const int4 w1 = unpack_nib16(uint2{(uint32_t)w.z, (uint32_t)w.w});
+        const int d = dot16(w1, x1, dot16(w0, x0, 0));
+        dv[(m * RW + r) * ldv + g] = float2{wsc[m][r][c], (float)d};
+      }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // 4. ordered FMA chains: lane j < NM*RW runs row (j % RW) of matrix j / RW;
+  //    16-byte LDS reads carry two groups' (scale, dot)
+  float acc = 0.f;
+  if (lane < NM * RW) {
+    const float4* dr = (const float4*)(dv + lane * ldv);
+    int g = 0;
+    for (; g + 16 <= ng; g += 16) {
+      float4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) v[u] = dr[g / 2 + u];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        acc = __fmaf_rn(v[u].x, v[u].y, acc);
+        acc = __fmaf_rn(v[u].z, v[u].w, acc);
+      }
+    }
+    const float2* d2 = dv + lane * ldv;
+    for (; g < ng; g++) acc = __fmaf_rn(d2[g].x, d2[g].y, acc);
+  }
+  const float sxv = sx_s;
+  if (PAIR) {
+    const float u = __shfl(acc, (lane + RW) & 63, 64);  // lane r < RW: the up row's chain
+    const int o = o0 + lane;
+    if (lane < RW && o < O) y[o] = ref_silu_mul(sxv * acc, sxv * u);
+  } else {
+    const int o = o0 + lane;
+    if (lane < RW && o < O) y[o] = sxv * acc;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // IDOT4 GEMM on v_mfma_i32_32x32x32_i8: one MFMA per group (K = 32 exactly),
 // so each group's integer dot comes out separately and is folded into a
 // float accumulator per output, in group order:
@@ -202,10 +332,51 @@ __global__ __launch_bounds__(Q4F_NT) void k_i4g_f32(const float* __restrict__ x,
   y[(int64_t)s * O + o] = a;
 }
 
-int launch_gemv_i4g(const float* x, const uint8_t* q4, const float* scl, float* y, int S, int I, int O,
-                    hipStream_t st) {
+// NT = 256 or 512 threads: wider workgroups amortize the activation row
+// (read once per workgroup) over more weight rows when I is large
+template <int RW, int NGC, bool PAIR, int NT>
+static int go_gemv1_i4g(const float* x, const uint8_t* q4, const float* scl, const uint8_t* q4b, const float* sclb,
+                        float* y, int I, int O, hipStream_t st) {
+  constexpr int NM = PAIR ? 2 : 1;
+  const int ng = I / 32;
+  const size_t lds = (size_t)I + (size_t)(NT / MOTY_WAVE) * NM * RW * (ng + 2) * 8;
+  if (lds > 64 * 1024) return MOTY_EUNSUP;
+  const unsigned nb = (unsigned)((O + RW * (NT / MOTY_WAVE) - 1) / (RW * (NT / MOTY_WAVE)));
+  hipLaunchKernelGGL((k_gemv1_i4g<RW, NGC, PAIR, NT>), dim3(nb), dim3(NT), lds, st, x, q4, scl, q4b, sclb, y, I, O);
+  LAUNCH_TRY("k_gemv1_i4g");
+  return MOTY_OK;
+}
+
+int launch_gemv_i4g(const float* x, const uint8_t* q4, const float* scl, const uint8_t* q4b, const float* sclb,
+                    float* y, int S, int I, int O, hipStream_t st) {
   if (S < 1 || S > 4 || (I % 64) || I > 16384) return MOTY_EUNSUP;
   if (O <= 0) return MOTY_OK;
+  if (S == 1) {
+    // widest instance whose LDS fits, else the next narrower one
+    const int ngc = (I / 32 + 63) / 64;
+    int rc = MOTY_EUNSUP;
+    if (q4b) {
+      if (ngc <= 2) rc = go_gemv1_i4g<4, 2, true, 256>(x, q4, scl, q4b, sclb, y, I, O, st);
+      else if (ngc <= 4) {
+        rc = go_gemv1_i4g<2, 4, true, 512>(x, q4, scl, q4b, sclb, y, I, O, st);
+        if (rc == MOTY_EUNSUP) rc = go_gemv1_i4g<2, 4, true, 256>(x, q4, scl, q4b, sclb, y, I, O, st);
+      } else if (ngc <= 8) {
+        rc = go_gemv1_i4g<1, 8, true, 512>(x, q4, scl, q4b, sclb, y, I, O, st);
+        if (rc == MOTY_EUNSUP) rc = go_gemv1_i4g<1, 8, true, 256>(x, q4, scl, q4b, sclb, y, I, O, st);
+      }
+      return rc;
+    }
+    if (ngc <= 2) rc = go_gemv1_i4g<8, 2, false, 256>(x, q4, scl, nullptr, nullptr, y, I, O, st);
+    else if (ngc <= 4) {
+      rc = go_gemv1_i4g<4, 4, false, 512>(x, q4, scl, nullptr, nullptr, y, I, O, st);
+      if (rc == MOTY_EUNSUP) rc = go_gemv1_i4g<4, 4, false, 256>(x, q4, scl, nullptr, nullptr, y, I, O, st);
+    } else if (ngc <= 8) {
+      rc = go_gemv1_i4g<2, 8, false, 512>(x, q4, scl, nullptr, nullptr, y, I, O, st);
+      if (rc == MOTY_EUNSUP) rc = go_gemv1_i4g<2, 8, false, 256>(x, q4, scl, nullptr, nullptr, y, I, O, st);
+    }
+    if (rc != MOTY_EUNSUP) return rc;
+  }
+  if (q4b) return MOTY_EUNSUP;
   const unsigned nb = (unsigned)((O + Q4V_ROWS - 1) / Q4V_ROWS);
   const size_t lds = (size_t)S * I;
   switch (S) {

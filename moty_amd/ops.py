@@ -140,6 +140,17 @@ def gate_up_silu_q8(x, gate, gs, up, us, out=None):
     return h
 
 
+def gate_up_silu_i4g(x, gate, gs, up, us, out=None):
+    """Decode gate+up+SiLU over grouped-int4 weights (IDOT4), one token."""
+    _dev(x, gate, gs, up, us)
+    D = x.shape[-1]
+    I = gate.shape[0]
+    h = out if out is not None else torch.empty((1, I), dtype=torch.float32, device=x.device)
+    check(lib().moty_hip_gate_up_silu_i4g_dev(_p(h), _p(x), _p(gate), _p(gs), _p(up), _p(us), D, I, _stream()),
+          "gate_up_silu_i4g")
+    return h
+
+
 class MoeLayer:
     """Device-resident MoE layer (MotyMoeView analogue, nn/moe.h:19-33)."""
 

@@ -118,7 +118,8 @@ def test_matmul_q8_extremes(ops):
 
 
 @pytest.mark.parametrize("S,I,O", [(1, 4096, 256), (2, 1024, 64), (4, 12288, 128), (1, 64, 5),
-                                   (256, 4096, 192), (37, 1024, 100), (5, 128, 64)])
+                                   (256, 4096, 192), (37, 1024, 100), (5, 128, 64), (1, 12288, 100),
+                                   (1, 8192, 77), (1, 16384, 40), (1, 2048, 1000)])
 def test_i4g_idot4(ops, S, I, O):
     say("i4g idot4", S, I, O)
     w = randn(O + I, (O, I), 0.02)
@@ -127,6 +128,21 @@ def test_i4g_idot4(ops, S, I, O):
     y = to_np(ops.matmul_i4_grouped_s(to_dev(x), to_dev(q4), to_dev(s), 32, True))
     y2 = o_matmul_i4g(x, q4, s, True)
     assert same_bits(y, y2), mismatch(y, y2)
+
+
+@pytest.mark.parametrize("D,I", [(4096, 300), (64, 17), (8192, 64), (12288, 40), (16384, 33), (2048, 513)])
+def test_gate_up_silu_i4g(ops, D, I):
+    say("gate_up_silu_i4g", D, I)
+    G = randn(D + 1, (I, D), 0.02)
+    U = randn(D + 2, (I, D), 0.02)
+    gq, gs = o_pack_int4_grouped(G)
+    uq, us = o_pack_int4_grouped(U)
+    x = randn(D + 3, (1, D))
+    h = to_np(ops.gate_up_silu_i4g(to_dev(x), to_dev(gq), to_dev(gs), to_dev(uq), to_dev(us)))
+    g = o_matmul_i4g(x, gq, gs, True)
+    u = o_matmul_i4g(x, uq, us, True)
+    oracle().o_silu_mul(ptr(g), ptr(u), g.size)
+    assert same_bits(h, g), mismatch(h, g)
 
 
 @pytest.mark.parametrize("S,I,O", [(1, 4096, 256), (3, 96, 40), (16, 1024, 64)])
