@@ -239,55 +239,93 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
 // so each group's integer dot comes out separately and is folded into a
 // float accumulator per output, in group order:
 //     accf = fma(scl[o][g], (float)d, accf)
-// Lane l holds weight row (l % 32) -- one scale per lane per group.
-// Workgroup: 4 waves as 2 (tokens) x 2 (rows), block tile 64 x 64.
+// Workgroup: 4 waves as 2 (tokens) x 2 (rows), block tile 64 x 64.  Per
+// K block of 4 groups the workgroup stages, by whole-line loads, the int8
+// activations (64 x 128 B), the nibbles (64 x 64 B) and the group scales
+// (64 x 4) in LDS, the next block's loads in flight in registers.
+// Lane l's A fragment is 16 bytes of token row (l % 32) at offset 16*(l/32)
+// of the group; its B fragment the matching 8 nibble bytes of weight row
+// (l % 32), expanded to signed n-8 -- one scale per lane per group.
 constexpr int Q4M_NT = 256;
+constexpr int Q4M_KG = 4;             // groups per K block
+constexpr int Q4M_AS = 128 + 16;      // LDS row stride: activations
+constexpr int Q4M_BS = 64 + 16;       // nibbles
+constexpr int Q4M_SS = Q4M_KG + 1;    // scales
 
-__global__ __launch_bounds__(Q4M_NT) void k_gemm_i4g(const int8_t* __restrict__ xq, const float* __restrict__ sx,
-                                                     const uint8_t* __restrict__ q4,
-                                                     const float* __restrict__ scl, float* __restrict__ y, int M,
-                                                     int I, int O) {
-  const int lane = threadIdx.x % MOTY_WAVE, wv = threadIdx.x / MOTY_WAVE;
-  const int m0 = blockIdx.y * 64 + (wv >> 1) * 32;
-  const int n0 = blockIdx.x * 64 + (wv & 1) * 32;
+__global__ __launch_bounds__(Q4M_NT, 2) void k_gemm_i4g(const int8_t* __restrict__ xq, const float* __restrict__ sx,
+                                                        const uint8_t* __restrict__ q4,
+                                                        const float* __restrict__ scl, float* __restrict__ y,
+                                                        int M, int I, int O) {
+  __shared__ __align__(16) int8_t sA[64 * Q4M_AS];
+  __shared__ __align__(16) uint8_t sB[64 * Q4M_BS];
+  __shared__ float sS[64 * Q4M_SS];
+  const int tid = threadIdx.x, lane = tid % MOTY_WAVE, wv = tid / MOTY_WAVE;
+  const int wm = wv >> 1, wn = wv & 1;
   const int r32 = lane & 31, hk = lane >> 5;
+  const int mb = blockIdx.y * 64, nb = blockIdx.x * 64;
   const int ng = I / 32, rb = I / 2;
-  int m = m0 + r32;
-  m = m < M ? m : M - 1;
-  int n = n0 + r32;
-  n = n < O ? n : O - 1;
-  const int8_t* ap = xq + (int64_t)m * I + hk * 16;
-  const uint8_t* bp = q4 + (int64_t)n * rb + hk * 8;
-  const float* sp = scl + (int64_t)n * ng;
+  // copy assignments: A 2 x 16 B chunks (row = q/8, col16 = q%8), B 1 chunk
+  // (row = tid/4, col16 = tid%4), S 1 float (row = tid/4, group = tid%4)
+  const int8_t* srcA[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int q = tid + i * Q4M_NT;
+    int m = mb + (q >> 3);
+    m = m < M ? m : M - 1;
+    srcA[i] = xq + (int64_t)m * I + (q & 7) * 16;
+  }
+  int nrow = nb + (tid >> 2);
+  nrow = nrow < O ? nrow : O - 1;
+  const uint8_t* srcB = q4 + (int64_t)nrow * rb + (tid & 3) * 16;
+  const float* srcS = scl + (int64_t)nrow * ng + (tid & 3);
+  int4 ra[2], rbv;
+  float rs;
+  auto gload = [&](int g0) {
+    // I % 64 == 0, so a K block of 4 groups (128 elements) is whole or the
+    // last 2 groups of the row are missing (I % 128 == 64)
+    const int kb = g0 * 32;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int q = tid + i * Q4M_NT;
+      ra[i] = (kb + (q & 7) * 16 < I) ? *(const int4*)(srcA[i] + kb) : int4{0, 0, 0, 0};
+    }
+    rbv = (g0 * 16 + (tid & 3) * 16 < rb) ? *(const int4*)(srcB + g0 * 16) : int4{0, 0, 0, 0};
+    rs = (g0 + (tid & 3) < ng) ? srcS[g0] : 0.f;
+  };
   float accf[16];
 #pragma unroll
   for (int r = 0; r < 16; r++) accf[r] = 0.f;
-  int4 a = *(const int4*)ap;
-  uint2 b = *(const uint2*)bp;
-  float sc = sp[0];
-  for (int g = 0; g < ng; g++) {
-    int4 an = a;
-    uint2 bn = b;
-    float scn = sc;
-    if (g + 1 < ng) {
-      an = *(const int4*)(ap + (g + 1) * 32);
-      bn = *(const uint2*)(bp + (g + 1) * 16);
-      scn = sp[g + 1];
-    }
-    const int4 w = unpack_nib16(b);
-    v16i d = {};
-    d = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(v4i*)&a, *(const v4i*)&w, d, 0, 0, 0);
+  gload(0);
+  for (int g0 = 0; g0 < ng; g0 += Q4M_KG) {
 #pragma unroll
-    for (int r = 0; r < 16; r++) accf[r] = __fmaf_rn(sc, (float)d[r], accf[r]);
-    a = an;
-    b = bn;
-    sc = scn;
+    for (int i = 0; i < 2; i++) {
+      const int q = tid + i * Q4M_NT;
+      *(int4*)(sA + (q >> 3) * Q4M_AS + (q & 7) * 16) = ra[i];
+    }
+    *(int4*)(sB + (tid >> 2) * Q4M_BS + (tid & 3) * 16) = rbv;
+    sS[(tid >> 2) * Q4M_SS + (tid & 3)] = rs;
+    __syncthreads();
+    if (g0 + Q4M_KG < ng) gload(g0 + Q4M_KG);
+    const int ngk = (ng - g0) < Q4M_KG ? (ng - g0) : Q4M_KG;
+#pragma unroll
+    for (int gg = 0; gg < Q4M_KG; gg++) {
+      if (gg >= ngk) break;  // wave-uniform
+      const v4i a = *(const v4i*)(sA + (wm * 32 + r32) * Q4M_AS + gg * 32 + hk * 16);
+      const uint2 wb = *(const uint2*)(sB + (wn * 32 + r32) * Q4M_BS + gg * 16 + hk * 8);
+      const float sc = sS[(wn * 32 + r32) * Q4M_SS + gg];
+      const int4 w = unpack_nib16(wb);
+      v16i d = {};
+      d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, *(const v4i*)&w, d, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 16; r++) accf[r] = __fmaf_rn(sc, (float)d[r], accf[r]);
+    }
+    __syncthreads();
   }
-  const int col = n0 + r32;
+  const int col = nb + wn * 32 + r32;
   if (col >= O) return;
 #pragma unroll
   for (int r = 0; r < 16; r++) {
-    const int row = m0 + 8 * (r >> 2) + 4 * hk + (r & 3);
+    const int row = mb + wm * 32 + 8 * (r >> 2) + 4 * hk + (r & 3);
     if (row < M) y[(int64_t)row * O + col] = sx[row] * accf[r];
   }
 }
