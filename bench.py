@@ -182,17 +182,24 @@ def bench_moe(c, cfg, T, E, K, I, D, norm, order, steps, warmup, bias=None, labe
 
 
 def bench_c2(c, steps, warmup):
-    """Qwen3-0.6B layer, the seven projections as Q8 prefill GEMMs, M=512."""
+    """Qwen3-0.6B layer, the seven projections as Q8 prefill GEMMs, M=512.
+    q, k, v, gate and up share their input, so their rows are stored
+    concatenated (the fused-rows layout of moty_mat_fuse_rows,
+    nn/mat.c:32-68, and of the fused gate_up of nn/ffn.c:28-37) and run as
+    one GEMM; o and down run on their own inputs.  One activation
+    quantization per distinct input."""
     torch, ops = c.torch, c.ops
     M = 512
     shapes = [("q", 2048, 1024), ("k", 1024, 1024), ("v", 1024, 1024), ("gate", 3072, 1024), ("up", 3072, 1024),
               ("o", 1024, 2048), ("down", 1024, 3072)]
+    fused_o = sum(O for _, O, I in shapes if I == 1024)
     wbytes = sum(O * I + O * 4 for _, O, I in shapes)
     ncopy = n_copies(wbytes, target=1100 << 20)
     g = c.gen(1, 1)
-    copies = [[c.q8((O, I), g) for _, O, I in shapes] for _ in range(ncopy)]
+    copies = [[c.q8((fused_o, 1024), g), c.q8((1024, 2048), g), c.q8((1024, 3072), g)] for _ in range(ncopy)]
     xs = {I: c.randn((M, I), c.gen(1, 2 + I)) for I in (1024, 2048, 3072)}
-    ys = [torch.empty((M, O), device="cuda:0") for _, O, _ in shapes]
+    ys = {1024: torch.empty((M, fused_o), device="cuda:0"), 2048: torch.empty((M, 1024), device="cuda:0"),
+          3072: torch.empty((M, 1024), device="cuda:0")}
     xq = {I: torch.empty((M, I), dtype=torch.int8, device="cuda:0") for I in xs}
     sx = {I: torch.empty(M, device="cuda:0") for I in xs}
     lib = ops.lib()
@@ -202,14 +209,16 @@ def bench_c2(c, steps, warmup):
             for I in xs:  # one activation quantization per distinct input
                 ops.check(lib.moty_hip_qrow_i8_dev(ops._p(xs[I]), ops._p(xq[I]), ops._p(sx[I]), None, M, I,
                                                    ops._stream()), "qrow")
-            for (name, O, I), (q, s), y in zip(shapes, ws, ys):
-                ops.matmul_q8_preq(xq[I], sx[I], q, s, out=y)
+            for I, (q, s) in zip((1024, 2048, 3072), ws):
+                ops.matmul_q8_preq(xq[I], sx[I], q, s, out=ys[I])
         return f
     t, n = c.time_steps([step(w) for w in copies], max(16, steps // 8), max(4, warmup // 8))
     ops_int = 2 * M * sum(O * I for _, O, I in shapes)
-    algo = wbytes + sum(M * I * 4 for I in (1024, 1024, 1024, 1024, 1024, 2048, 3072)) + sum(M * O * 4 for _, O, _ in shapes)
-    return {"workload": "C2 Qwen3-0.6B layer, 7 Q8 projections as prefill GEMMs, M=512", "ms_per_step": t * 1e3,
-            "steps": n, "roofline": roofline("mfma", ops_int / t / 1e12, INT8_PEAK_TOPS, "TOP/s"),
+    algo = wbytes + M * (1024 + 2048 + 3072) * 4 + sum(M * O * 4 for _, O, _ in shapes)
+    return {"workload": "C2 Qwen3-0.6B layer, 7 Q8 projections as prefill GEMMs, M=512 "
+                        "(q/k/v/gate/up fused by rows: one GEMM N=10240, K=1024; o; down)",
+            "ms_per_step": t * 1e3, "steps": n,
+            "roofline": roofline("mfma", ops_int / t / 1e12, INT8_PEAK_TOPS, "TOP/s"),
             "hbm_gbs": round(algo / t / 1e9, 1)}
 
 

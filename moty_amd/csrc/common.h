@@ -64,6 +64,15 @@ __device__ __forceinline__ float ref_silu_mul(float g, float u) {
 }
 
 // lrintf under the default round-to-nearest-even mode, as an int.
+// Branch-free "ok ? v : 0" for a value loaded from a clamped (always valid)
+// address: a predicated load would split the wave's loads into branches and
+// force a wait for every load in flight at the join.
+__device__ __forceinline__ int4 sel4(bool ok, int4 v) {
+  return int4{ok ? v.x : 0, ok ? v.y : 0, ok ? v.z : 0, ok ? v.w : 0};
+}
+__device__ __forceinline__ float4 sel4(bool ok, float4 v) {
+  return float4{ok ? v.x : 0.f, ok ? v.y : 0.f, ok ? v.z : 0.f, ok ? v.w : 0.f};
+}
 __device__ __forceinline__ int rne_int(float v) { return (int)__builtin_rintf(v); }
 
 // ---------------------------------------------------------------------------

@@ -83,13 +83,16 @@ __global__ __launch_bounds__(GEMV_NT) void k_gemv_q8(const float* __restrict__ x
     int4 wq[RPW][CB], wq2[RPW][CB];
 #pragma unroll
     for (int r = 0; r < RPW; r++) {
-      const int o = o0 + r;
+      // clamped addresses, unconditional loads (no waits at branch joins):
+      // rows past O are never stored, columns past I meet zero activations
+      // in LDS, chunks past the row end are never consumed
+      const int o = o0 + r < O ? o0 + r : O - 1;
 #pragma unroll
       for (int j = 0; j < CB; j++) {
         const int k = (cb + j) * CHUNK + lane * 16;
-        const bool ok = (o < O) && (cb + j < nch) && (k < I);
-        wq[r][j] = ok ? ldnt16(W + (int64_t)o * I + k) : int4{0, 0, 0, 0};
-        if (PAIR) wq2[r][j] = ok ? ldnt16(W2 + (int64_t)o * I + k) : int4{0, 0, 0, 0};
+        const int kc = k < I ? k : 0;
+        wq[r][j] = ldnt16(W + (int64_t)o * I + kc);
+        if (PAIR) wq2[r][j] = ldnt16(W2 + (int64_t)o * I + kc);
       }
     }
     if (cb == 0) {
@@ -187,7 +190,7 @@ __global__ __launch_bounds__(GEMV_NT) void k_gemv1_q8(const float* __restrict__ 
   for (int c = 0; c < NC; c++) {
     const int k = c * CHUNK + lane * 16;
 #pragma unroll
-    for (int j = 0; j < 4; j++) xv[c][j] = (k < I) ? *(const float4*)(x + k + 4 * j) : float4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 4; j++) xv[c][j] = *(const float4*)(x + (k < I ? k : 0) + 4 * j);
   }
   int4 wq[RPW][NC], wq2[RPW][NC];
 #pragma unroll
@@ -196,10 +199,27 @@ __global__ __launch_bounds__(GEMV_NT) void k_gemv1_q8(const float* __restrict__ 
 #pragma unroll
     for (int c = 0; c < NC; c++) {
       const int k = c * CHUNK + lane * 16;
-      wq[r][c] = k < I ? ldnt16(W + (int64_t)o * I + k) : int4{0, 0, 0, 0};
-      if (PAIR) wq2[r][c] = k < I ? ldnt16(W2 + (int64_t)o * I + k) : int4{0, 0, 0, 0};
+      const int kc = k < I ? k : 0;
+      wq[r][c] = ldnt16(W + (int64_t)o * I + kc);
+      if (PAIR) wq2[r][c] = ldnt16(W2 + (int64_t)o * I + kc);
     }
   }
+  // lane r holds the scales of the wave's row r, loaded with the weights so
+  // the epilogue waits on no further memory latency
+  float sc = 0.f, sc2 = 0.f;
+  {
+    const int o = o0 + (lane < RPW ? lane : 0);
+    sc = scale[o < O ? o : O - 1];
+    if (PAIR) sc2 = scale2[o < O ? o : O - 1];
+  }
+  // keep the scheduler from sinking weight loads below the first use of x
+  __builtin_amdgcn_sched_barrier(0);
+  // past the row end x was read from a clamped address: zero it (the
+  // weights there are multiplied by these zeros)
+#pragma unroll
+  for (int c = 0; c < NC; c++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) xv[c][j] = sel4(c * CHUNK + lane * 16 < I, xv[c][j]);
   int4 xq[NC];
   const float sx = wave_qrow<NC>(xv, xq);
   int acc[RPW], acc2[RPW];
@@ -215,15 +235,18 @@ __global__ __launch_bounds__(GEMV_NT) void k_gemv1_q8(const float* __restrict__ 
     acc[r] = wave_sum_i32(acc[r]);
     if (PAIR) acc2[r] = wave_sum_i32(acc2[r]);
   }
+  // lane r finishes row o0 + r; computed on every lane (wave-wide cost is
+  // the same) so the scale loads above stay where they were issued
+  int a = acc[0], a2 = acc2[0];
 #pragma unroll
-  for (int r = 0; r < RPW; r++) {
-    const int o = o0 + r;
-    if (lane == r && o < O) {
-      float v = (scale[o] * sx) * (float)acc[r];
-      if (PAIR) v = ref_silu_mul(v, (scale2[o] * sx) * (float)acc2[r]);
-      y[o] = v;
-    }
+  for (int r = 1; r < RPW; r++) {
+    a = lane == r ? acc[r] : a;
+    a2 = lane == r ? acc2[r] : a2;
   }
+  float v = (sc * sx) * (float)a;
+  if (PAIR) v = ref_silu_mul(v, (sc2 * sx) * (float)a2);
+  const int o = o0 + lane;
+  if (lane < RPW && o < O) y[o] = v;
 }
 
 template <int NC, bool PAIR>

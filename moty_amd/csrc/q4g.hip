@@ -138,7 +138,7 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
 #pragma unroll
   for (int j = 0; j < XV; j++) {
     const int i = (threadIdx.x + j * NT) * 4;
-    xr[j] = i < I ? *(const float4*)(x + i) : float4{0.f, 0.f, 0.f, 0.f};
+    xr[j] = *(const float4*)(x + (i < I ? i : 0));  // clamped: zeroed below
   }
   int4 wb[NM][RW][NGC];
   float wsc[NM][RW][NGC];  // group scales, loaded with the nibbles
@@ -151,11 +151,16 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
       const float* sbase = (m ? sclb : scl) + o * ng;
 #pragma unroll
       for (int c = 0; c < NGC; c++) {
-        const int g = c * 64 + lane;
-        wb[m][r][c] = g < ng ? *(const int4*)(base + g * 16) : int4{0, 0, 0, 0};
-        wsc[m][r][c] = g < ng ? sbase[g] : 0.f;
+        // clamped (unused past ng): unconditional loads keep the wave's
+        // loads in one straight run, with no wait at branch joins
+        const int g = c * 64 + lane < ng ? c * 64 + lane : 0;
+        wb[m][r][c] = *(const int4*)(base + g * 16);
+        wsc[m][r][c] = sbase[g];
       }
     }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < XV; j++) xr[j] = sel4((threadIdx.x + j * NT) * 4 < I, xr[j]);
   // 2. qrow_i8 of x into LDS
   float amax = 0.f;
 #pragma unroll
