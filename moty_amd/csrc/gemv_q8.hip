@@ -177,14 +177,14 @@ __global__ __launch_bounds__(GEMV_NT) void k_gemv_q8(const float* __restrict__ x
 // The activation loads are issued before the weight loads, so waiting for
 // them does not wait for the weights.  Weights stream with non-temporal
 // loads (read once, kept out of the caches' way).
-template <int NC, int RPW, bool PAIR>
-__global__ __launch_bounds__(GEMV_NT) void k_gemv1_q8(const float* __restrict__ x, const int8_t* __restrict__ W,
+template <int NC, int RPW, bool PAIR, int NW = GEMV_WAVES>
+__global__ __launch_bounds__(NW * MOTY_WAVE) void k_gemv1_q8(const float* __restrict__ x, const int8_t* __restrict__ W,
                                                       const float* __restrict__ scale,
                                                       const int8_t* __restrict__ W2,
                                                       const float* __restrict__ scale2, float* __restrict__ y,
                                                       int I, int O) {
   const int lane = threadIdx.x % MOTY_WAVE;
-  const int o0 = (blockIdx.x * GEMV_WAVES + threadIdx.x / MOTY_WAVE) * RPW;
+  const int o0 = (blockIdx.x * NW + threadIdx.x / MOTY_WAVE) * RPW;
   float4 xv[NC][4];
 #pragma unroll
   for (int c = 0; c < NC; c++) {
@@ -252,17 +252,25 @@ __global__ __launch_bounds__(GEMV_NT) void k_gemv1_q8(const float* __restrict__ 
 template <int NC, bool PAIR>
 static int launch_1(const float* x, const int8_t* W, const float* scale, const int8_t* W2, const float* scale2,
                     float* y, int I, int O, hipStream_t st) {
-  // rows per wave: keep >= ~2 workgroups per CU on the 256-CU part
-  const int rpw = (O >= 16384) ? 4 : (O >= 8192 ? 2 : 1);
-  auto go = [&](auto kern, int r) {
-    const unsigned nb = (unsigned)((O + GEMV_WAVES * r - 1) / (GEMV_WAVES * r));
-    hipLaunchKernelGGL(kern, dim3(nb), dim3(GEMV_NT), 0, st, x, W, scale, W2, scale2, y, I, O);
-  };
-  if (rpw == 4) go(k_gemv1_q8<NC, 4, PAIR>, 4);
-  else if (rpw == 2) go(k_gemv1_q8<NC, 2, PAIR>, 2);
-  else go(k_gemv1_q8<NC, 1, PAIR>, 1);
-  LAUNCH_TRY("k_gemv1_q8");
-  return MOTY_OK;
+  // Launch shape from a sweep of rows/wave x waves/workgroup on MI355X over
+  // decode shapes (O 1024..12288, I 1024..4096, plain and PAIR): four rows
+  // per wave (fewer when that leaves < 256 waves), then enough waves per
+  // workgroup to bring the grid near one workgroup per CU.
+  int rpw = 4;
+  while (rpw > 1 && (O + rpw - 1) / rpw < 256) rpw >>= 1;
+  const int waves = (O + rpw - 1) / rpw;
+  const int nw = waves > 512 ? 4 : (waves > 256 ? 2 : 1);
+  const unsigned nb = (unsigned)((waves + nw - 1) / nw);
+#define L1(R, N)                                                                                              \
+  if (rpw == R && nw == N) {                                                                                 \
+    hipLaunchKernelGGL((k_gemv1_q8<NC, R, PAIR, N>), dim3(nb), dim3(N * MOTY_WAVE), 0, st, x, W, scale, W2,   \
+                       scale2, y, I, O);                                                                     \
+    LAUNCH_TRY("k_gemv1_q8");                                                                                \
+    return MOTY_OK;                                                                                          \
+  }
+  L1(4, 4) L1(4, 2) L1(4, 1) L1(2, 2) L1(2, 1) L1(1, 2) L1(1, 1)
+#undef L1
+  return MOTY_EUNSUP;
 }
 
 template <int S_, bool PAIR>
