@@ -287,18 +287,45 @@ __global__ __launch_bounds__(GR_NT) void k_group(const int* __restrict__ idx, in
     if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int o = 0, tl = 0;
-    for (int e = 0; e < E; e++) {
-      cur[e] = o;
-      offs[e] = o;
-      tstart[e] = tl;
-      o += cnt[e];
-      tl += (cnt[e] + MOE_BM - 1) / MOE_BM;
+  if (threadIdx.x < MOTY_WAVE) {
+    // exclusive scans of the counts and of the M-tile counts by one wave:
+    // lane l owns experts 4l..4l+3 (E <= 256)
+    const int l = threadIdx.x;
+    int c[4], t[4], so = 0, st = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int e = 4 * l + j;
+      c[j] = e < E ? cnt[e] : 0;
+      t[j] = (c[j] + MOE_BM - 1) / MOE_BM;
+      so += c[j];
+      st += t[j];
     }
-    offs[E] = o;
-    tstart[E] = tl;
-    ntiles[0] = tl;
+    int io = so, it = st;  // inclusive scans over lanes
+#pragma unroll
+    for (int d = 1; d < MOTY_WAVE; d <<= 1) {
+      const int po = __shfl_up(io, d, MOTY_WAVE), pt = __shfl_up(it, d, MOTY_WAVE);
+      if (l >= d) {
+        io += po;
+        it += pt;
+      }
+    }
+    int o = io - so, tl = it - st;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int e = 4 * l + j;
+      if (e < E) {
+        cur[e] = o;
+        offs[e] = o;
+        tstart[e] = tl;
+      }
+      o += c[j];
+      tl += t[j];
+    }
+    if (l == MOTY_WAVE - 1) {
+      offs[E] = o;
+      tstart[E] = tl;
+      ntiles[0] = tl;
+    }
   }
   __syncthreads();
   for (int e = threadIdx.x; e < E; e += GR_NT) {

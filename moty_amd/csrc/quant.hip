@@ -80,6 +80,56 @@ __global__ __launch_bounds__(NT) void k_qrow_i8(const float* __restrict__ x, int
   }
 }
 
+// One wave per row (I <= 1024*NC, I % 16 == 0, no group sums): lane l holds
+// elements [c*1024 + 16l, +16) of every chunk c, so a wave-max is the row's
+// amax and the row never waits on a workgroup barrier.  Same arithmetic as
+// k_qrow_i8.
+template <int NC>
+__global__ __launch_bounds__(256) void k_qrow_wave(const float* __restrict__ x, int8_t* __restrict__ q,
+                                                   float* __restrict__ sx, int S, int I, int64_t ldx, int64_t ldq) {
+  const int lane = threadIdx.x % MOTY_WAVE;
+  int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / MOTY_WAVE;
+  const bool live = row < S;
+  row = live ? row : S - 1;
+  const float* xr = x + row * ldx;
+  float4 v[NC][4];
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    const int k = c * 1024 + lane * 16;
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[c][j] = *(const float4*)(xr + (k < I ? k : 0) + 4 * j);
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    const bool ok = c * 1024 + lane * 16 < I;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      v[c][j] = sel4(ok, v[c][j]);
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[c][j].x), fabsf(v[c][j].y)), fmaxf(fabsf(v[c][j].z), fabsf(v[c][j].w))));
+    }
+  }
+  amax = wave_max_f32(amax);
+  float s = amax / 127.f;
+  if (s < 1e-12f) s = 1e-12f;
+  const float inv = 1.f / s;
+  if (!live) return;
+  if (lane == 0) sx[row] = s;
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    const int k = c * 1024 + lane * 16;
+    if (k >= I) continue;
+    int4 o;
+    int* op = (int*)&o;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      op[j] = (int)((uint32_t)(rne_int(v[c][j].x * inv) & 0xff) | ((uint32_t)(rne_int(v[c][j].y * inv) & 0xff) << 8) |
+                    ((uint32_t)(rne_int(v[c][j].z * inv) & 0xff) << 16) |
+                    ((uint32_t)(rne_int(v[c][j].w * inv) & 0xff) << 24));
+    *(int4*)(q + row * ldq + k) = o;
+  }
+}
+
 // Weight rows: s = amax/qmax clamped at 1e-8, v = clip(rint(w/s)).
 template <int NT>
 __global__ __launch_bounds__(NT) void k_quantize_rows(const float* __restrict__ w, int8_t* __restrict__ q,
@@ -136,6 +186,19 @@ int launch_qrow_i8(const float* x, int8_t* q, float* sx, int32_t* xg, int S, int
                    int64_t ldq, hipStream_t st) {
   if (S <= 0) return MOTY_OK;
   if (xg && (I % 32)) return MOTY_EINVAL;
+  const bool wave_ok = !xg && I <= 4096 && (I % 16) == 0 && (ldx % 4) == 0 && (ldq % 16) == 0 &&
+                       (((uintptr_t)x) & 15) == 0 && (((uintptr_t)q) & 15) == 0;
+  if (wave_ok) {
+    const unsigned nb = (unsigned)((S + 3) / 4);
+    switch ((I + 1023) / 1024) {
+      case 1: hipLaunchKernelGGL(k_qrow_wave<1>, dim3(nb), dim3(256), 0, st, x, q, sx, S, I, ldx, ldq); break;
+      case 2: hipLaunchKernelGGL(k_qrow_wave<2>, dim3(nb), dim3(256), 0, st, x, q, sx, S, I, ldx, ldq); break;
+      case 3: hipLaunchKernelGGL(k_qrow_wave<3>, dim3(nb), dim3(256), 0, st, x, q, sx, S, I, ldx, ldq); break;
+      default: hipLaunchKernelGGL(k_qrow_wave<4>, dim3(nb), dim3(256), 0, st, x, q, sx, S, I, ldx, ldq); break;
+    }
+    LAUNCH_TRY("k_qrow_wave");
+    return MOTY_OK;
+  }
   hipLaunchKernelGGL(k_qrow_i8<256>, dim3(S), dim3(256), 0, st, x, q, sx, xg, I, ldx, ldq);
   LAUNCH_TRY("k_qrow_i8");
   return MOTY_OK;

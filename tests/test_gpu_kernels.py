@@ -67,6 +67,18 @@ def test_qrow_i8(ops, S, I):
         assert (to_np(xg) == q2.reshape(S, -1, 32).astype(np.int32).sum(-1)).all()
 
 
+@pytest.mark.parametrize("S,I", [(1, 1024), (5, 4096), (3, 48), (7, 2000), (9, 3072), (4, 5008), (6, 1030)])
+def test_qrow_i8_rows(ops, S, I):
+    """Without group sums: rows of I <= 4096 (I % 16 == 0) take the
+    wave-per-row kernel, the rest the workgroup-per-row one."""
+    say("qrow rows", S, I)
+    x = randn(S * I + 7, (S, I)) * 3
+    x[0, :3] = [0.0, 1e-30, -5.5]
+    q, sx, _ = ops.qrow_i8(to_dev(x), group_sums=False)
+    q2, sx2 = o_qrow(x)
+    assert same_bits(to_np(sx), sx2) and same_bits(to_np(q), q2)
+
+
 def test_qrow_zero_row(ops):
     q, sx, _ = ops.qrow_i8(torch.zeros((2, 64), device="cuda:0"))
     assert (to_np(sx) == np.float32(1e-12)).all() and not to_np(q).any()
