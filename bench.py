@@ -133,15 +133,15 @@ def bench_c1(c, steps, warmup):
     h = torch.empty((1, I), device="cuda:0")
     t, n = c.time_steps([lambda w=w: ops.dense_ffn_q8(x, *w, out=out) for w in copies], steps, warmup)
     # dominant kernel alone: the fused gate+up GEMV (k_gemv_q8 PAIR mode)
-    tg, _ = c.time_steps([lambda w=w: ops.gate_up_silu_q8(x, w[0], w[1], w[2], w[3], out=h) for w in copies],
-                         steps, warmup)
+    gu = [lambda w=w: ops.gate_up_silu_q8(x, w[0], w[1], w[2], w[3], out=h) for w in copies]
+    tg, _ = c.time_steps(gu, steps, warmup)
     gu_algo = 2 * I * D + 2 * I * 4 + D * 4 + I * 4
     torch.cuda.synchronize()
     return {
         "workload": "C1 Qwen3-0.6B FFN decode, Q8_0 (fused gate/up GEMV + SiLU, down GEMV), S=1, D=1024, I=3072",
         "gbs": algo / t / 1e9, "ms_per_step": t * 1e3, "steps": n, "algo_bytes": algo,
         "weight_copies": ncopy, "x": x, "w0": copies[0],
-        "kernel": {"name": "k_gemv1_q8<1,1,PAIR> gate+up+SiLU", "us": tg * 1e6, "algo_bytes": gu_algo,
+        "kernel": {"name": "k_gemv1_q8<1,4,PAIR,4> gate+up+SiLU", "us": tg * 1e6, "algo_bytes": gu_algo,
                    "gbs": gu_algo / tg / 1e9},
     }
 
@@ -411,7 +411,9 @@ def main():
                 "weights rotate over %d copies" % c1["weight_copies"],
         "config": {"workload": c1["workload"]},
         "roofline": dict(roofline("hbm", k["gbs"], HBM_PEAK_GBS, "GB/s", pmc_traffic("c1_gate_up_gemv_pmc")),
-                         kernel=k["name"], kernel_us=round(k["us"], 3), algo_bytes=k["algo_bytes"]),
+                         kernel=k["name"], kernel_us=round(k["us"], 3), algo_bytes=k["algo_bytes"],
+                         timing="HIP events around graph replays of the kernel alone (weights rotating "
+                                "over the copies), elapsed / launches"),
         "whole_ffn_roofline": roofline("hbm", c1["gbs"], HBM_PEAK_GBS, "GB/s"),
         "cpu_baseline": cpu,
         "moe": moe,
