@@ -17,10 +17,6 @@ constexpr int GM_NT = 256;  // 4 waves, 2 x 2 over the block tile
 constexpr int GM_KB = 128;  // K bytes per stage
 constexpr int GM_LS = 144;  // padded LDS row stride
 
-__device__ __forceinline__ int4 ld16(const int8_t* p, bool ok) {
-  return ok ? *(const int4*)p : int4{0, 0, 0, 0};
-}
-
 // y[M][O] from xq[M][K], W[O][K]; K % 16 == 0.  Block tile BM x BN with
 // BM = 64*WM, BN = 64*WN; wave (wm, wn) owns (32*WM) x (32*WN) outputs as
 // WM x WN v_mfma_i32_32x32x32_i8 tiles.  Per 128-byte K block the tile is
@@ -57,27 +53,51 @@ __global__ __launch_bounds__(GM_NT, 2) void k_gemm_q8(const int8_t* __restrict__
     srcB[i] = W + (int64_t)n * K + col;
   }
   // two register sets: while one K block is consumed from LDS, the next two
-  // are in flight from HBM
+  // are in flight from HBM.  Every load is unconditional, from a clamped
+  // address (a chunk past the row end re-reads the row start; a K block past
+  // the end re-reads the last block, an L2 hit), and chunks past the end are
+  // zeroed when written to LDS: with no branch around a load, the compiler
+  // waits only for the register set about to be consumed.
   int4 ra0[NA], rb0[NB], ra1[NA], rb1[NB];
+  const int klast = (K - 1) / GM_KB * GM_KB;
   auto gload = [&](int k0, int4(&ra)[NA], int4(&rb)[NB]) {
-    const bool ok = (k0 + col) < K;
+    const int kc = k0 < K ? k0 : klast;
+    const int off = kc + col < K ? kc : -col;
 #pragma unroll
-    for (int i = 0; i < NA; i++) ra[i] = ld16(srcA[i] + k0, ok);
+    for (int i = 0; i < NA; i++) ra[i] = *(const int4*)(srcA[i] + off);
 #pragma unroll
-    for (int i = 0; i < NB; i++) rb[i] = ld16(srcB[i] + k0, ok);
+    for (int i = 0; i < NB; i++) rb[i] = *(const int4*)(srcB[i] + off);
+    // keep each set's loads together and in issue order
+    __builtin_amdgcn_sched_barrier(0);
   };
+  // epilogue scales, loaded before the K loop so that their latency hides
+  // behind it: the tile's activation-row scales (to LDS after the loop) and
+  // this lane's weight-row scales
+  __shared__ float s_sx[BM];
+  float sxr;
+  {
+    const int m = mb + tid % BM;
+    sxr = sx[m < M ? m : M - 1];
+  }
+  float scn[WN];
+#pragma unroll
+  for (int j = 0; j < WN; j++) {
+    const int n = nb + wn * 32 * WN + j * 32 + r32;
+    scn[j] = scale[n < O ? n : O - 1];
+  }
   v16i acc[WM][WN];
 #pragma unroll
   for (int i = 0; i < WM; i++)
 #pragma unroll
     for (int j = 0; j < WN; j++) acc[i][j] = v16i{};
   auto stage = [&](int k0, int4(&ra)[NA], int4(&rb)[NB]) {
+    const bool ok = k0 + col < K;
 #pragma unroll
-    for (int i = 0; i < NA; i++) *(int4*)(sA + ((tid + i * GM_NT) >> 3) * GM_LS + col) = ra[i];
+    for (int i = 0; i < NA; i++) *(int4*)(sA + ((tid + i * GM_NT) >> 3) * GM_LS + col) = sel4(ok, ra[i]);
 #pragma unroll
-    for (int i = 0; i < NB; i++) *(int4*)(sB + ((tid + i * GM_NT) >> 3) * GM_LS + col) = rb[i];
+    for (int i = 0; i < NB; i++) *(int4*)(sB + ((tid + i * GM_NT) >> 3) * GM_LS + col) = sel4(ok, rb[i]);
     __syncthreads();
-    if (k0 + 2 * GM_KB < K) gload(k0 + 2 * GM_KB, ra, rb);
+    gload(k0 + 2 * GM_KB, ra, rb);
 #pragma unroll
     for (int st = 0; st < 4; st++) {
       v4i fa[WM], fb[WN];
@@ -95,23 +115,29 @@ __global__ __launch_bounds__(GM_NT, 2) void k_gemm_q8(const int8_t* __restrict__
     __syncthreads();
   };
   gload(0, ra0, rb0);
-  if (GM_KB < K) gload(GM_KB, ra1, rb1);
+  gload(GM_KB, ra1, rb1);
+  // an odd number of K blocks runs one all-zero block (adds exactly 0)
   for (int k0 = 0; k0 < K; k0 += 2 * GM_KB) {
     stage(k0, ra0, rb0);
-    if (k0 + GM_KB < K) stage(k0 + GM_KB, ra1, rb1);
+    stage(k0 + GM_KB, ra1, rb1);
   }
+  // retire every load still in flight (the clamped prefetches past the end)
+  // once, here: otherwise the compiler waits for all memory operations --
+  // each previous store included -- before every conditional store below
+  __builtin_amdgcn_s_waitcnt(0);
+  if (tid < BM) s_sx[tid] = sxr;
+  __syncthreads();
   // D layout: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, column l%32
 #pragma unroll
   for (int j = 0; j < WN; j++) {
     const int n = nb + wn * 32 * WN + j * 32 + r32;
     if (n >= O) continue;
-    const float sc = scale[n];
 #pragma unroll
     for (int i = 0; i < WM; i++)
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        const int m = mb + wm * 32 * WM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (m < M) y[(int64_t)m * O + n] = (sc * sx[m]) * (float)acc[i][j][r];
+        const int ml = wm * 32 * WM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (mb + ml < M) y[(int64_t)(mb + ml) * O + n] = (scn[j] * s_sx[ml]) * (float)acc[i][j][r];
       }
   }
 }

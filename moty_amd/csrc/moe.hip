@@ -388,6 +388,21 @@ __global__ __launch_bounds__(MG_NT, 2) void k_moe_gemm(
   const int nb0 = blockIdx.x * MG_BN;
   const bool two = (nseg - mb) > 32;  // second 32-slot half has rows (uniform)
 
+  // epilogue scales, loaded before the K loop so their latency hides behind
+  // it: the activation scale of M-tile row tid % 64 (to LDS after the loop)
+  // and this lane's weight-row scales
+  __shared__ float s_act[64];
+  float srow;
+  {
+    int m = mb + (tid & 63);
+    m = m < nseg ? m : nseg - 1;
+    const int sl = seg0 + m;
+    srow = act_s[GATEUP ? slot_tok[sl] : sl];
+  }
+  const int ncol = nb0 + wv * 32 + r32;
+  const int ncl = ncol < N ? ncol : N - 1;
+  const float s1 = S1[(int64_t)e * N + ncl];
+  const float s2 = GATEUP ? S2[(int64_t)e * N + ncl] : 0.f;
   // this thread's copy assignments: chunk q -> (row q/8, 16 B column q%8)
   const int8_t* srcA[NA];
   const int8_t* srcB[NBW];
@@ -410,23 +425,32 @@ __global__ __launch_bounds__(MG_NT, 2) void k_moe_gemm(
     srcB[i] = W + ((int64_t)e * N + n) * Kd + col;
   }
   // two register sets: while one K block is consumed from LDS, the next two
-  // are in flight from HBM
+  // are in flight from HBM.  Every load is unconditional, from a clamped
+  // address (a K chunk past the row end re-reads the row start; a K block
+  // past the end re-reads the last block, an L2 hit), and chunks past the
+  // end are zeroed when written to LDS: with no branch around a load, the
+  // compiler waits only for the register set about to be consumed.
   int4 ra0[NA], rb0[NBW], ra1[NA], rb1[NBW];
+  const int klast = (Kd - 1) / MG_KB * MG_KB;
   auto gload = [&](int k0, int4(&ra)[NA], int4(&rb)[NBW]) {
-    const bool ok = (k0 + col) < Kd;  // K % 16 == 0: a chunk is all in or all out
+    const int kc = k0 < Kd ? k0 : klast;
+    const int off = kc + col < Kd ? kc : -col;  // K % 16 == 0: a chunk is all in or all out
 #pragma unroll
-    for (int i = 0; i < NA; i++) ra[i] = ok ? ldg16(srcA[i] + k0) : int4{0, 0, 0, 0};
+    for (int i = 0; i < NA; i++) ra[i] = ldg16(srcA[i] + off);
 #pragma unroll
-    for (int i = 0; i < NBW; i++) rb[i] = ok ? ldg16(srcB[i] + k0) : int4{0, 0, 0, 0};
+    for (int i = 0; i < NBW; i++) rb[i] = ldg16(srcB[i] + off);
+    // keep each set's loads together and in issue order
+    __builtin_amdgcn_sched_barrier(0);
   };
   v16i acc1[2] = {}, acc2[2] = {};
   auto stage = [&](int k0, int4(&ra)[NA], int4(&rb)[NBW]) {
+    const bool ok = k0 + col < Kd;
 #pragma unroll
-    for (int i = 0; i < NA; i++) *(int4*)(sA + ((tid + i * MG_NT) >> 3) * MG_LS + col) = ra[i];
+    for (int i = 0; i < NA; i++) *(int4*)(sA + ((tid + i * MG_NT) >> 3) * MG_LS + col) = sel4(ok, ra[i]);
 #pragma unroll
-    for (int i = 0; i < NBW; i++) *(int4*)(sB + ((tid + i * MG_NT) >> 3) * MG_LS + col) = rb[i];
+    for (int i = 0; i < NBW; i++) *(int4*)(sB + ((tid + i * MG_NT) >> 3) * MG_LS + col) = sel4(ok, rb[i]);
     __syncthreads();
-    if (k0 + 2 * MG_KB < Kd) gload(k0 + 2 * MG_KB, ra, rb);
+    gload(k0 + 2 * MG_KB, ra, rb);
     const int8_t* a0 = sA + r32 * MG_LS + h * 64;
     const int8_t* a1 = a0 + 32 * MG_LS;
     const int8_t* bg = sB + (wv * 32 + r32) * MG_LS + h * 64;
@@ -450,15 +474,19 @@ __global__ __launch_bounds__(MG_NT, 2) void k_moe_gemm(
     __syncthreads();
   };
   gload(0, ra0, rb0);
-  if (MG_KB < Kd) gload(MG_KB, ra1, rb1);
+  gload(MG_KB, ra1, rb1);
+  // an odd number of K blocks runs one all-zero block (adds exactly 0)
   for (int k0 = 0; k0 < Kd; k0 += 2 * MG_KB) {
     stage(k0, ra0, rb0);
-    if (k0 + MG_KB < Kd) stage(k0 + MG_KB, ra1, rb1);
+    stage(k0 + MG_KB, ra1, rb1);
   }
-  const int ncol = nb0 + wv * 32 + r32;
+  // retire every load still in flight (the clamped prefetches past the end)
+  // once, here: otherwise the compiler waits for all memory operations --
+  // each previous store included -- before every conditional store below
+  __builtin_amdgcn_s_waitcnt(0);
+  if (tid < 64) s_act[tid] = srow;
+  __syncthreads();
   if (ncol >= N) return;
-  const float s1 = S1[(int64_t)e * N + ncol];
-  const float s2 = GATEUP ? S2[(int64_t)e * N + ncol] : 0.f;
 #pragma unroll
   for (int i = 0; i < 2; i++) {
     if (i == 1 && !two) break;
@@ -468,12 +496,12 @@ __global__ __launch_bounds__(MG_NT, 2) void k_moe_gemm(
       if (m >= nseg) continue;
       const int sl = seg0 + m;
       if (GATEUP) {
-        const float sxv = act_s[slot_tok[sl]];
+        const float sxv = s_act[m - mb];
         const float g = (s1 * sxv) * (float)acc1[i][r];
         const float u = (s2 * sxv) * (float)acc2[i][r];
         out[(int64_t)sl * N + ncol] = ref_silu_mul(g, u);
       } else {
-        out[(int64_t)sl * N + ncol] = (s1 * act_s[sl]) * (float)acc1[i][r];
+        out[(int64_t)sl * N + ncol] = (s1 * s_act[m - mb]) * (float)acc1[i][r];
       }
     }
   }

@@ -283,34 +283,51 @@ __global__ __launch_bounds__(Q4M_NT, 2) void k_gemm_i4g(const int8_t* __restrict
   nrow = nrow < O ? nrow : O - 1;
   const uint8_t* srcB = q4 + (int64_t)nrow * rb + (tid & 3) * 16;
   const float* srcS = scl + (int64_t)nrow * ng + (tid & 3);
-  int4 ra[2], rbv;
-  float rs;
-  auto gload = [&](int g0) {
-    // I % 64 == 0, so a K block of 4 groups (128 elements) is whole or the
-    // last 2 groups of the row are missing (I % 128 == 64)
-    const int kb = g0 * 32;
+  // epilogue: the activation scale of tile row tid % 64, loaded now so its
+  // latency hides behind the K loop (to LDS after it)
+  __shared__ float s_sx[64];
+  const float sxr = sx[mb + (tid & 63) < M ? mb + (tid & 63) : M - 1];
+  // Two register sets: while one K block is consumed from LDS, the next two
+  // are in flight.  Loads are unconditional, from clamped addresses (a block
+  // past the end re-reads the last one; a chunk past the row end re-reads
+  // the row start), and are masked when written to LDS: with no branch
+  // around a load the compiler waits only for the set about to be consumed.
+  // I % 64 == 0, so a K block of 4 groups (128 elements) is whole or the
+  // last 2 groups of the row are missing (I % 128 == 64).
+  struct Set {
+    int4 a[2];
+    int4 b;
+    float s;
+  };
+  Set st0, st1;
+  const int glast = (ng - 1) / Q4M_KG * Q4M_KG;
+  auto gload = [&](int g0, Set& st) {
+    const int gc = g0 < ng ? g0 : glast;
+    const int kb = gc * 32;
 #pragma unroll
     for (int i = 0; i < 2; i++) {
       const int q = tid + i * Q4M_NT;
-      ra[i] = (kb + (q & 7) * 16 < I) ? *(const int4*)(srcA[i] + kb) : int4{0, 0, 0, 0};
+      st.a[i] = *(const int4*)(srcA[i] + (kb + (q & 7) * 16 < I ? kb : -(q & 7) * 16));
     }
-    rbv = (g0 * 16 + (tid & 3) * 16 < rb) ? *(const int4*)(srcB + g0 * 16) : int4{0, 0, 0, 0};
-    rs = (g0 + (tid & 3) < ng) ? srcS[g0] : 0.f;
+    st.b = *(const int4*)(srcB + (gc * 16 + (tid & 3) * 16 < rb ? gc * 16 : -(tid & 3) * 16));
+    st.s = srcS[gc + (tid & 3) < ng ? gc : -(tid & 3)];
+    __builtin_amdgcn_sched_barrier(0);
   };
   float accf[16];
 #pragma unroll
   for (int r = 0; r < 16; r++) accf[r] = 0.f;
-  gload(0);
-  for (int g0 = 0; g0 < ng; g0 += Q4M_KG) {
+  auto stage = [&](int g0, Set& st) {
+    const int kb = g0 * 32;
 #pragma unroll
     for (int i = 0; i < 2; i++) {
       const int q = tid + i * Q4M_NT;
-      *(int4*)(sA + (q >> 3) * Q4M_AS + (q & 7) * 16) = ra[i];
+      *(int4*)(sA + (q >> 3) * Q4M_AS + (q & 7) * 16) = sel4(kb + (q & 7) * 16 < I, st.a[i]);
     }
-    *(int4*)(sB + (tid >> 2) * Q4M_BS + (tid & 3) * 16) = rbv;
-    sS[(tid >> 2) * Q4M_SS + (tid & 3)] = rs;
+    *(int4*)(sB + (tid >> 2) * Q4M_BS + (tid & 3) * 16) = sel4(g0 * 16 + (tid & 3) * 16 < rb, st.b);
+    sS[(tid >> 2) * Q4M_SS + (tid & 3)] = g0 + (tid & 3) < ng ? st.s : 0.f;
     __syncthreads();
-    if (g0 + Q4M_KG < ng) gload(g0 + Q4M_KG);
+    gload(g0 + 2 * Q4M_KG, st);
+    // blocks past the end (an odd block count) compute nothing
     const int ngk = (ng - g0) < Q4M_KG ? (ng - g0) : Q4M_KG;
 #pragma unroll
     for (int gg = 0; gg < Q4M_KG; gg++) {
@@ -325,13 +342,24 @@ __global__ __launch_bounds__(Q4M_NT, 2) void k_gemm_i4g(const int8_t* __restrict
       for (int r = 0; r < 16; r++) accf[r] = __fmaf_rn(sc, (float)d[r], accf[r]);
     }
     __syncthreads();
+  };
+  gload(0, st0);
+  gload(Q4M_KG, st1);
+  for (int g0 = 0; g0 < ng; g0 += 2 * Q4M_KG) {
+    stage(g0, st0);
+    stage(g0 + Q4M_KG, st1);
   }
+  // retire the clamped prefetch still in flight once, here: otherwise the
+  // compiler waits for every memory operation before each conditional store
+  __builtin_amdgcn_s_waitcnt(0);
+  if (tid < 64) s_sx[tid] = sxr;
+  __syncthreads();
   const int col = nb + wn * 32 + r32;
   if (col >= O) return;
 #pragma unroll
   for (int r = 0; r < 16; r++) {
-    const int row = mb + wm * 32 + 8 * (r >> 2) + 4 * hk + (r & 3);
-    if (row < M) y[(int64_t)row * O + col] = sx[row] * accf[r];
+    const int rl = wm * 32 + 8 * (r >> 2) + 4 * hk + (r & 3);
+    if (mb + rl < M) y[(int64_t)(mb + rl) * O + col] = s_sx[rl] * accf[r];
   }
 }
 
