@@ -69,39 +69,50 @@ __global__ __launch_bounds__(RG_NT) void k_router_logits(const float* __restrict
 #pragma unroll
     for (int j = 0; j < RG_PE; j++) acc[i][j] = 0.f;
   const int nsteps = D / 32;  // D % 32 == 0
-  float4 rx[NX], rw[NW];
-  auto gload = [&](int st0) {
-    const int k0 = st0 * 32, kn = ((nsteps - st0) < RG_KS ? (nsteps - st0) : RG_KS) * 32;
-#pragma unroll
-    for (int i = 0; i < NX; i++) {
-      const int q = threadIdx.x + i * RG_NT, r = q / (RG_KC / 4), k = (q % (RG_KC / 4)) * 4;
-      rx[i] = (k < kn && tb + r < T) ? *(const float4*)(x + (int64_t)(tb + r) * D + k0 + k)
-                                     : float4{0.f, 0.f, 0.f, 0.f};
-    }
-#pragma unroll
-    for (int i = 0; i < NW; i++) {
-      const int q = threadIdx.x + i * RG_NT, r = q / (RG_KC / 4), k = (q % (RG_KC / 4)) * 4;
-      rw[i] = (k < kn && eb + r < E) ? *(const float4*)(Wr + (int64_t)(eb + r) * D + k0 + k)
-                                     : float4{0.f, 0.f, 0.f, 0.f};
-    }
+  // Two register sets of K-chunk loads, one chunk consumed from LDS while
+  // the next two are in flight.  Loads are unconditional, from clamped
+  // addresses, and zeroed when written to LDS: a branch around a load would
+  // make the compiler wait for every load in flight.  Past the row end the
+  // zeros extend every FMA chain by fma(0, 0, acc) = acc (acc is never -0:
+  // it starts at +0 and an exact zero sum rounds to +0), so full chunks are
+  // always run.
+  struct Set {
+    float4 x[NX], w[NW];
   };
-  gload(0);
-  for (int st0 = 0; st0 < nsteps; st0 += RG_KS) {
-    const int ns = (nsteps - st0) < RG_KS ? (nsteps - st0) : RG_KS;
-    __syncthreads();
+  Set s0, s1;
+  auto gload = [&](int st0, Set& sv) {
+    const int k0 = st0 * 32;
 #pragma unroll
     for (int i = 0; i < NX; i++) {
-      const int q = threadIdx.x + i * RG_NT;
-      *(float4*)(xs + (q / (RG_KC / 4)) * RG_LS + (q % (RG_KC / 4)) * 4) = rx[i];
+      const int q = threadIdx.x + i * RG_NT, r = q / (RG_KC / 4), k = (q % (RG_KC / 4)) * 4;
+      const int t = tb + r < T ? tb + r : T - 1;
+      sv.x[i] = *(const float4*)(x + (int64_t)t * D + (k0 + k < D ? k0 + k : 0));
     }
 #pragma unroll
     for (int i = 0; i < NW; i++) {
-      const int q = threadIdx.x + i * RG_NT;
-      *(float4*)(ws + (q / (RG_KC / 4)) * RG_LS + (q % (RG_KC / 4)) * 4) = rw[i];
+      const int q = threadIdx.x + i * RG_NT, r = q / (RG_KC / 4), k = (q % (RG_KC / 4)) * 4;
+      const int e = eb + r < E ? eb + r : E - 1;
+      sv.w[i] = *(const float4*)(Wr + (int64_t)e * D + (k0 + k < D ? k0 + k : 0));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto chunk = [&](int st0, Set& sv) {
+    const int k0 = st0 * 32;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NX; i++) {
+      const int q = threadIdx.x + i * RG_NT, r = q / (RG_KC / 4), k = (q % (RG_KC / 4)) * 4;
+      *(float4*)(xs + r * RG_LS + k) = sel4(k0 + k < D && tb + r < T, sv.x[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < NW; i++) {
+      const int q = threadIdx.x + i * RG_NT, r = q / (RG_KC / 4), k = (q % (RG_KC / 4)) * 4;
+      *(float4*)(ws + r * RG_LS + k) = sel4(k0 + k < D && eb + r < E, sv.w[i]);
     }
     __syncthreads();
-    if (st0 + RG_KS < nsteps) gload(st0 + RG_KS);
-    auto step = [&](int u) {
+    gload(st0 + 2 * RG_KS, sv);
+#pragma unroll
+    for (int u = 0; u < RG_KS; u++) {
       float xv[PT], wv[RG_PE];
 #pragma unroll
       for (int i = 0; i < PT; i++) xv[i] = xs[(tq + i) * RG_LS + u * 32 + c];
@@ -111,13 +122,23 @@ __global__ __launch_bounds__(RG_NT) void k_router_logits(const float* __restrict
       for (int i = 0; i < PT; i++)
 #pragma unroll
         for (int j = 0; j < RG_PE; j++) acc[i][j] = __fmaf_rn(xv[i], wv[j], acc[i][j]);
-    };
-    if (ns == RG_KS) {
-#pragma unroll
-      for (int u = 0; u < RG_KS; u++) step(u);
-    } else {
-      for (int u = 0; u < ns; u++) step(u);
     }
+  };
+  gload(0, s0);
+  gload(RG_KS, s1);
+  for (int st0 = 0; st0 < nsteps; st0 += 2 * RG_KS) {
+    chunk(st0, s0);
+    chunk(st0 + RG_KS, s1);
+  }
+  // retire the clamped prefetches still in flight before the branchy
+  // epilogue, then load this thread's biases in one batch
+  __builtin_amdgcn_s_waitcnt(0);
+  float bv[RG_PE];
+#pragma unroll
+  for (int j = 0; j < RG_PE; j++) bv[j] = 0.f;
+  if (bias) {
+#pragma unroll
+    for (int j = 0; j < RG_PE; j++) bv[j] = bias[eb + eq + j < E ? eb + eq + j : E - 1];
   }
   // s0[c] + s1[c], then the 16-lane reduce_add tree, per pair
   const int base = (threadIdx.x % MOTY_WAVE) & 32;
@@ -129,7 +150,7 @@ __global__ __launch_bounds__(RG_NT) void k_router_logits(const float* __restrict
       float r = hsum16_half(t2, base);
       const int t = tb + tq + i, e = eb + eq + j;
       if (c == 0 && t < T && e < E) {
-        if (bias) r = r + bias[e];
+        if (bias) r = r + bv[j];
         logits[(int64_t)t * E + e] = r;
       }
     }
@@ -157,6 +178,46 @@ __global__ __launch_bounds__(TK_NT) void k_route_topk(const float* __restrict__ 
   float* p = prs + wv * E;
   if ((threadIdx.x / MOTY_WAVE) & 1) {  // qrow_i8 of x[t]
     const float* xr = x + (int64_t)t * D;
+    if (D <= 4096) {
+      // the row held in registers: lane l owns [c*1024 + 16l, +16) of each
+      // 1 KiB chunk c (clamped loads past the end, zeroed)
+      float4 v[4][4];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const int k = c * 1024 + lane * 16;
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[c][j] = *(const float4*)(xr + (k < D ? k : 0) + 4 * j);
+      }
+      float amax = 0.f;
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const bool ok = c * 1024 + lane * 16 < D;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          v[c][j] = sel4(ok, v[c][j]);
+          amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[c][j].x), fabsf(v[c][j].y)), fmaxf(fabsf(v[c][j].z), fabsf(v[c][j].w))));
+        }
+      }
+      amax = wave_max_f32(amax);
+      float s = amax / 127.f;
+      if (s < 1e-12f) s = 1e-12f;
+      const float inv = 1.f / s;
+      if (lane == 0) sx[t] = s;
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const int k = c * 1024 + lane * 16;
+        if (k >= D) continue;
+        int4 o;
+        int* op = (int*)&o;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          op[j] = (int)((uint32_t)(rne_int(v[c][j].x * inv) & 0xff) | ((uint32_t)(rne_int(v[c][j].y * inv) & 0xff) << 8) |
+                        ((uint32_t)(rne_int(v[c][j].z * inv) & 0xff) << 16) |
+                        ((uint32_t)(rne_int(v[c][j].w * inv) & 0xff) << 24));
+        *(int4*)(xq + (int64_t)t * D + k) = o;
+      }
+      return;
+    }
     float amax = 0.f;
     for (int i = lane * 4; i < D; i += MOTY_WAVE * 4) {
       const float4 v = *(const float4*)(xr + i);
@@ -540,8 +601,10 @@ __global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ y
     float4 v[8];
 #pragma unroll
     for (int u = 0; u < 8; u++) {
+      // unconditional loads (clamped slot; skipped pairs are not used): a
+      // branch around each load would serialize their latencies
       const int sl = (j0 + u < K) ? slot_s[j0 + u] : -1;
-      v[u] = sl >= 0 ? *(const float4*)(y + (int64_t)sl * D + d) : float4{0.f, 0.f, 0.f, 0.f};
+      v[u] = *(const float4*)(y + (int64_t)(sl >= 0 ? sl : 0) * D + d);
     }
 #pragma unroll
     for (int u = 0; u < 8; u++) {
@@ -598,14 +661,17 @@ int launch_moe(const MoeArgs& a, void* scratch, hipStream_t st) {
 
   if (E > 64 * TK_PV) return MOTY_EUNSUP;
   float* logits = (float*)(b + off[14]);
-  // 8-token tiles while that still leaves few workgroups per CU, 16 beyond
-  // (halves the router re-reads)
-  if ((int64_t)((T + 7) / 8) * ((E + RG_TE - 1) / RG_TE) <= 512)
-    hipLaunchKernelGGL(k_router_logits<2>, dim3((T + 7) / 8, (E + RG_TE - 1) / RG_TE), dim3(RG_NT), 0, st, a.x, a.Wr,
-                       a.bias, T, D, E, logits);
+  // 4-token tiles while that leaves at most ~2 workgroups per CU (the
+  // router is latency-bound at small T), 16-token tiles beyond (fewer router
+  // re-reads); measured on MI355X: T=256, E=64: 8.0 us vs 10.5 (8-token);
+  // T=1072, E=128: 28.7 us vs 34.7 (4-token)
+  const int eblk = (E + RG_TE - 1) / RG_TE;
+  if ((int64_t)((T + 3) / 4) * eblk <= 512)
+    hipLaunchKernelGGL(k_router_logits<1>, dim3((T + 3) / 4, eblk), dim3(RG_NT), 0, st, a.x, a.Wr, a.bias, T, D,
+                       E, logits);
   else
-    hipLaunchKernelGGL(k_router_logits<4>, dim3((T + 15) / 16, (E + RG_TE - 1) / RG_TE), dim3(RG_NT), 0, st, a.x,
-                       a.Wr, a.bias, T, D, E, logits);
+    hipLaunchKernelGGL(k_router_logits<4>, dim3((T + 15) / 16, eblk), dim3(RG_NT), 0, st, a.x, a.Wr, a.bias, T, D,
+                       E, logits);
   LAUNCH_TRY("k_router_logits");
   hipLaunchKernelGGL(k_route_topk, dim3((T + TK_NT / 128 - 1) / (TK_NT / 128)), dim3(TK_NT),
                      (size_t)(TK_NT / 128) * E * 4, st, a.x, logits, T, D, E, K, a.norm, idx, w, xq, sx,
