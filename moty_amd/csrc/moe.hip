@@ -332,8 +332,8 @@ constexpr int GR_NT = 1024;
 
 // Single workgroup.  offs[E+1]: expert segment starts; slot_tok[P]: token of
 // each slot; pair_slot[P]: slot of pair (t,k); tiles[]: (expert, m0) M-tiles
-// of MOE_BM slots; ntiles[0]: their count.
-__global__ __launch_bounds__(GR_NT) void k_group(const int* __restrict__ idx, int P, int K, int E,
+// of bm slots; ntiles[0]: their count.
+__global__ __launch_bounds__(GR_NT) void k_group(const int* __restrict__ idx, int P, int K, int E, int bm,
                                                  int* __restrict__ offs, int* __restrict__ slot_tok,
                                                  int* __restrict__ pair_slot, int2* __restrict__ tiles,
                                                  int* __restrict__ ntiles, int* __restrict__ counts_out) {
@@ -357,7 +357,7 @@ __global__ __launch_bounds__(GR_NT) void k_group(const int* __restrict__ idx, in
     for (int j = 0; j < 4; j++) {
       const int e = 4 * l + j;
       c[j] = e < E ? cnt[e] : 0;
-      t[j] = (c[j] + MOE_BM - 1) / MOE_BM;
+      t[j] = (c[j] + bm - 1) / bm;
       so += c[j];
       st += t[j];
     }
@@ -392,7 +392,7 @@ __global__ __launch_bounds__(GR_NT) void k_group(const int* __restrict__ idx, in
   for (int e = threadIdx.x; e < E; e += GR_NT) {
     if (counts_out) counts_out[e] = cnt[e];
     const int nt = tstart[e + 1] - tstart[e];
-    for (int j = 0; j < nt; j++) tiles[tstart[e] + j] = int2{e, j * MOE_BM};
+    for (int j = 0; j < nt; j++) tiles[tstart[e] + j] = int2{e, j * bm};
   }
   for (int p = threadIdx.x; p < P; p += GR_NT) {
     const int e = idx[p];
@@ -404,15 +404,17 @@ __global__ __launch_bounds__(GR_NT) void k_group(const int* __restrict__ idx, in
 }
 
 // ---------------------------------------------------------------------------
-// Grouped GEMMs.  Workgroup = 4 waves over one (expert, 64-slot M-tile,
-// 128-row N-tile).  Per 128-byte K block the workgroup stages the tile in
-// LDS: every global load instruction reads whole 128 B lines (8 lanes per
-// row, 16 B each) -- activation rows gathered through slot -> token for the
-// gate/up GEMM -- into rows padded to 144 B.  Each wave then owns 32 weight
-// rows (of gate and up, or of down) for both 32-slot halves of the M-tile
-// and runs v_mfma_i32_32x32x32_i8 on fragments read back from LDS.  Two
-// register sets keep the next two K blocks' global loads in flight during
-// the MFMAs.
+// Grouped GEMMs.  Workgroup = MT groups of 4 waves over one (expert,
+// 64*MT-slot M-tile, 128-row N-tile); MT = 2 when experts average more than
+// 48 slots, so that an expert's weight tile is read once for up to 128 slots
+// instead of once per 64.  Per 128-byte K block the workgroup stages the
+// tile in LDS: every global load instruction reads whole 128 B lines (8
+// lanes per row, 16 B each) -- activation rows gathered through slot ->
+// token for the gate/up GEMM -- into rows padded to 144 B.  Each wave then
+// owns 32 weight rows (of gate and up, or of down) for both 32-slot halves
+// of its group's 64-slot sub-tile and runs v_mfma_i32_32x32x32_i8 on
+// fragments read back from LDS.  Two register sets keep the next two K
+// blocks' global loads in flight during the MFMAs.
 //
 // Fragment k-order: MFMA step j of a K block takes, in lane l, bytes
 // [64*(l/32) + 16j, +16) of row (l % 32).  An integer dot is order-free, so
@@ -425,8 +427,8 @@ constexpr int MG_LS = 144;   // padded LDS row stride
 
 __device__ __forceinline__ int4 ldg16(const int8_t* p) { return *(const int4*)p; }
 
-template <bool GATEUP>
-__global__ __launch_bounds__(MG_NT, 2) void k_moe_gemm(
+template <bool GATEUP, int MT>
+__global__ __launch_bounds__(MG_NT * MT, 2 / MT) void k_moe_gemm(
     const int2* __restrict__ tiles, const int* __restrict__ ntiles, const int* __restrict__ offs,
     const int* __restrict__ slot_tok,
     const int8_t* __restrict__ act, const float* __restrict__ act_s,  // GATEUP: xq[T][K], sx[T]; else hq[P][K], sh[P]
@@ -434,33 +436,38 @@ __global__ __launch_bounds__(MG_NT, 2) void k_moe_gemm(
     const int8_t* __restrict__ W2, const float* __restrict__ S2,      // up (GATEUP only)
     float* __restrict__ out,                                          // [P][N]
     int N, int Kd) {
+  constexpr int NTH = MG_NT * MT;                    // MT groups of 4 waves, one per 64-slot sub-tile
+  constexpr int BM = 64 * MT;                        // slots per M-tile
   constexpr int BROWS = GATEUP ? 2 * MG_BN : MG_BN;  // staged weight rows
-  constexpr int NA = 64 * 8 / MG_NT;                 // 16 B chunks per thread: A
-  constexpr int NBW = BROWS * 8 / MG_NT;             // and B
-  __shared__ __align__(16) int8_t sA[64 * MG_LS];
+  constexpr int NA = BM * 8 / NTH;                   // 16 B chunks per thread: A
+  constexpr int NBW = BROWS * 8 / NTH;               // and B
+  __shared__ __align__(16) int8_t sA[BM * MG_LS];
   __shared__ __align__(16) int8_t sB[BROWS * MG_LS];
+  __shared__ float s_act[BM];
   const int tile = blockIdx.y;
   if (tile >= ntiles[0]) return;
   const int2 tm = tiles[tile];
   const int e = tm.x, mb = tm.y;
   const int seg0 = offs[e], nseg = offs[e + 1] - seg0;
   const int tid = threadIdx.x, lane = tid % MOTY_WAVE, wv = tid / MOTY_WAVE;
+  const int sub = wv / 4, wn = wv % 4;  // this wave: sub-tile, 32-row N slice
   const int r32 = lane & 31, h = lane >> 5;
   const int nb0 = blockIdx.x * MG_BN;
-  const bool two = (nseg - mb) > 32;  // second 32-slot half has rows (uniform)
+  const int msub = mb + 64 * sub;
+  const bool one = (nseg - msub) > 0;   // the sub-tile's halves have rows (wave-uniform)
+  const bool two = (nseg - msub) > 32;
 
   // epilogue scales, loaded before the K loop so their latency hides behind
-  // it: the activation scale of M-tile row tid % 64 (to LDS after the loop)
+  // it: the activation scale of M-tile row tid % BM (to LDS after the loop)
   // and this lane's weight-row scales
-  __shared__ float s_act[64];
   float srow;
   {
-    int m = mb + (tid & 63);
+    int m = mb + (tid % BM);
     m = m < nseg ? m : nseg - 1;
     const int sl = seg0 + m;
     srow = act_s[GATEUP ? slot_tok[sl] : sl];
   }
-  const int ncol = nb0 + wv * 32 + r32;
+  const int ncol = nb0 + wn * 32 + r32;
   const int ncl = ncol < N ? ncol : N - 1;
   const float s1 = S1[(int64_t)e * N + ncl];
   const float s2 = GATEUP ? S2[(int64_t)e * N + ncl] : 0.f;
@@ -470,7 +477,7 @@ __global__ __launch_bounds__(MG_NT, 2) void k_moe_gemm(
   const int col = (tid & 7) * 16;
 #pragma unroll
   for (int i = 0; i < NA; i++) {
-    const int row = (tid + i * MG_NT) >> 3;
+    const int row = (tid + i * NTH) >> 3;
     int m = mb + row;
     m = m < nseg ? m : nseg - 1;
     const int slot = seg0 + m;
@@ -479,13 +486,13 @@ __global__ __launch_bounds__(MG_NT, 2) void k_moe_gemm(
   }
 #pragma unroll
   for (int i = 0; i < NBW; i++) {
-    const int row = (tid + i * MG_NT) >> 3;
+    const int row = (tid + i * NTH) >> 3;
     const int8_t* W = (GATEUP && row >= MG_BN) ? W2 : W1;
     int n = nb0 + (row & (MG_BN - 1));
     n = n < N ? n : N - 1;
     srcB[i] = W + ((int64_t)e * N + n) * Kd + col;
   }
-  // two register sets: while one K block is consumed from LDS, the next two
+  // Two register sets: while one K block is consumed from LDS, the next two
   // are in flight from HBM.  Every load is unconditional, from a clamped
   // address (a K chunk past the row end re-reads the row start; a K block
   // past the end re-reads the last block, an L2 hit), and chunks past the
@@ -507,29 +514,31 @@ __global__ __launch_bounds__(MG_NT, 2) void k_moe_gemm(
   auto stage = [&](int k0, int4(&ra)[NA], int4(&rb)[NBW]) {
     const bool ok = k0 + col < Kd;
 #pragma unroll
-    for (int i = 0; i < NA; i++) *(int4*)(sA + ((tid + i * MG_NT) >> 3) * MG_LS + col) = sel4(ok, ra[i]);
+    for (int i = 0; i < NA; i++) *(int4*)(sA + ((tid + i * NTH) >> 3) * MG_LS + col) = sel4(ok, ra[i]);
 #pragma unroll
-    for (int i = 0; i < NBW; i++) *(int4*)(sB + ((tid + i * MG_NT) >> 3) * MG_LS + col) = sel4(ok, rb[i]);
+    for (int i = 0; i < NBW; i++) *(int4*)(sB + ((tid + i * NTH) >> 3) * MG_LS + col) = sel4(ok, rb[i]);
     __syncthreads();
     gload(k0 + 2 * MG_KB, ra, rb);
-    const int8_t* a0 = sA + r32 * MG_LS + h * 64;
+    const int8_t* a0 = sA + (64 * sub + r32) * MG_LS + h * 64;
     const int8_t* a1 = a0 + 32 * MG_LS;
-    const int8_t* bg = sB + (wv * 32 + r32) * MG_LS + h * 64;
+    const int8_t* bg = sB + (wn * 32 + r32) * MG_LS + h * 64;
     const int8_t* bu = bg + MG_BN * MG_LS;
+    if (one) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const v4i fa0 = *(const v4i*)(a0 + 16 * j);
-      const v4i fg = *(const v4i*)(bg + 16 * j);
-      acc1[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0, fg, acc1[0], 0, 0, 0);
-      v4i fu = {};
-      if (GATEUP) {
-        fu = *(const v4i*)(bu + 16 * j);
-        acc2[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0, fu, acc2[0], 0, 0, 0);
-      }
-      if (two) {
-        const v4i fa1 = *(const v4i*)(a1 + 16 * j);
-        acc1[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1, fg, acc1[1], 0, 0, 0);
-        if (GATEUP) acc2[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1, fu, acc2[1], 0, 0, 0);
+      for (int j = 0; j < 4; j++) {
+        const v4i fa0 = *(const v4i*)(a0 + 16 * j);
+        const v4i fg = *(const v4i*)(bg + 16 * j);
+        acc1[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0, fg, acc1[0], 0, 0, 0);
+        v4i fu = {};
+        if (GATEUP) {
+          fu = *(const v4i*)(bu + 16 * j);
+          acc2[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0, fu, acc2[0], 0, 0, 0);
+        }
+        if (two) {
+          const v4i fa1 = *(const v4i*)(a1 + 16 * j);
+          acc1[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1, fg, acc1[1], 0, 0, 0);
+          if (GATEUP) acc2[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1, fu, acc2[1], 0, 0, 0);
+        }
       }
     }
     __syncthreads();
@@ -545,24 +554,24 @@ __global__ __launch_bounds__(MG_NT, 2) void k_moe_gemm(
   // once, here: otherwise the compiler waits for all memory operations --
   // each previous store included -- before every conditional store below
   __builtin_amdgcn_s_waitcnt(0);
-  if (tid < 64) s_act[tid] = srow;
+  if (tid < BM) s_act[tid] = srow;
   __syncthreads();
-  if (ncol >= N) return;
+  if (ncol >= N || !one) return;
 #pragma unroll
   for (int i = 0; i < 2; i++) {
     if (i == 1 && !two) break;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      const int m = mb + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-      if (m >= nseg) continue;
-      const int sl = seg0 + m;
+      const int ml = 64 * sub + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);  // row within the M-tile
+      if (mb + ml >= nseg) continue;
+      const int sl = seg0 + mb + ml;
       if (GATEUP) {
-        const float sxv = s_act[m - mb];
+        const float sxv = s_act[ml];
         const float g = (s1 * sxv) * (float)acc1[i][r];
         const float u = (s2 * sxv) * (float)acc2[i][r];
         out[(int64_t)sl * N + ncol] = ref_silu_mul(g, u);
       } else {
-        out[(int64_t)sl * N + ncol] = (s1 * s_act[m - mb]) * (float)acc1[i][r];
+        out[(int64_t)sl * N + ncol] = (s1 * s_act[ml]) * (float)acc1[i][r];
       }
     }
   }
@@ -657,7 +666,6 @@ int launch_moe(const MoeArgs& a, void* scratch, hipStream_t st) {
   float* y = (float*)(b + off[12]);
   int* counts = (int*)(b + off[13]);
   const int P = T * K;
-  const int maxt = P / MOE_BM + E + 1;
 
   if (E > 64 * TK_PV) return MOTY_EUNSUP;
   float* logits = (float*)(b + off[14]);
@@ -677,16 +685,28 @@ int launch_moe(const MoeArgs& a, void* scratch, hipStream_t st) {
                      (size_t)(TK_NT / 128) * E * 4, st, a.x, logits, T, D, E, K, a.norm, idx, w, xq, sx,
                      a.probs_out);
   LAUNCH_TRY("k_route_topk");
-  hipLaunchKernelGGL(k_group, dim3(1), dim3(GR_NT), (size_t)(3 * E + 1) * 4, st, idx, P, K, E, offs, slot_tok,
-                     pair_slot, tiles, ntiles, counts);
+  // 128-slot M-tiles when experts average more than 48 slots (one pass over
+  // an expert's weights for up to 128 slots), 64-slot tiles otherwise
+  const int mt = (P > 48 * E) ? 2 : 1;
+  hipLaunchKernelGGL(k_group, dim3(1), dim3(GR_NT), (size_t)(3 * E + 1) * 4, st, idx, P, K, E, 64 * mt, offs,
+                     slot_tok, pair_slot, tiles, ntiles, counts);
   LAUNCH_TRY("k_group");
-  hipLaunchKernelGGL(k_moe_gemm<true>, dim3((I + MG_BN - 1) / MG_BN, maxt), dim3(MG_NT), 0, st, tiles, ntiles,
-                     offs, slot_tok, xq, sx, a.G, a.GS, a.U, a.US, h, I, D);
+  const int maxt = P / (64 * mt) + E + 1;
+  if (mt == 2)
+    hipLaunchKernelGGL((k_moe_gemm<true, 2>), dim3((I + MG_BN - 1) / MG_BN, maxt), dim3(MG_NT * 2), 0, st, tiles,
+                       ntiles, offs, slot_tok, xq, sx, a.G, a.GS, a.U, a.US, h, I, D);
+  else
+    hipLaunchKernelGGL((k_moe_gemm<true, 1>), dim3((I + MG_BN - 1) / MG_BN, maxt), dim3(MG_NT), 0, st, tiles,
+                       ntiles, offs, slot_tok, xq, sx, a.G, a.GS, a.U, a.US, h, I, D);
   LAUNCH_TRY("k_moe_gemm<gateup>");
   int rc = launch_qrow_i8(h, hq, sh, nullptr, P, I, I, I, st);
   if (rc) return rc;
-  hipLaunchKernelGGL(k_moe_gemm<false>, dim3((D + MG_BN - 1) / MG_BN, maxt), dim3(MG_NT), 0, st, tiles, ntiles,
-                     offs, slot_tok, hq, sh, a.Dn, a.DS, nullptr, nullptr, y, D, I);
+  if (mt == 2)
+    hipLaunchKernelGGL((k_moe_gemm<false, 2>), dim3((D + MG_BN - 1) / MG_BN, maxt), dim3(MG_NT * 2), 0, st, tiles,
+                       ntiles, offs, slot_tok, hq, sh, a.Dn, a.DS, nullptr, nullptr, y, D, I);
+  else
+    hipLaunchKernelGGL((k_moe_gemm<false, 1>), dim3((D + MG_BN - 1) / MG_BN, maxt), dim3(MG_NT), 0, st, tiles,
+                       ntiles, offs, slot_tok, hq, sh, a.Dn, a.DS, nullptr, nullptr, y, D, I);
   LAUNCH_TRY("k_moe_gemm<down>");
   hipLaunchKernelGGL(k_moe_combine, dim3(T, (D / 4 + 255) / 256), dim3(256), 0, st, y, idx, w, pair_slot, a.out, D,
                      K, a.order);

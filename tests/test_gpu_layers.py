@@ -86,7 +86,7 @@ def layer(ops, Wr, ex, K, norm, order, bias=None):
 
 @pytest.mark.parametrize("E,K,I,D,S", [(16, 4, 128, 256, 24), (8, 2, 64, 64, 1), (64, 8, 1024, 2048, 32),
                                        (128, 8, 768, 2048, 20), (5, 5, 32, 32, 7), (8, 2, 64, 128, 300),
-                                       (6, 2, 96, 160, 50)])
+                                       (6, 2, 96, 160, 50), (16, 4, 96, 128, 400), (32, 8, 64, 96, 257)])
 @pytest.mark.parametrize("order", ["batch", "olmoe"])
 def test_moe_layer(ops, E, K, I, D, S, order):
     say("moe", E, K, I, D, S, order)
@@ -122,9 +122,11 @@ def test_moe_routing_ties(ops, order):
     assert same_bits(to_np(y), y2)
 
 
-def test_moe_skewed_bias(ops):
-    # +2.0 on 8 hot experts' logits (the skewed continuous-batch variant)
-    E, K, I, D, S = 32, 4, 64, 128, 40
+@pytest.mark.parametrize("S", [40, 400])
+def test_moe_skewed_bias(ops, S):
+    # +2.0 on 8 hot experts' logits (the skewed continuous-batch variant);
+    # S = 400 takes 128-slot M-tiles, hot experts spanning several
+    E, K, I, D = 32, 4, 64, 128
     Wr = randn(5, (E, D), 0.02)
     x = randn(6, (S, D))
     ex = moe_weights(E, I, D, seed=20)
