@@ -39,7 +39,10 @@ namespace moty {
 // Thread (pair group g, chain c) accumulates chain c of PT x RG_PE
 // (token, expert) pairs; x and router K-chunks are staged in LDS, so each
 // router row is read once per workgroup's tokens and each x row once per
-// RG_TE experts.
+// RG_TE experts.  The grid is 1-D and XCD-aware: workgroups are dispatched to
+// the 8 XCDs round-robin by linear id, so ids are decoded such that all the
+// expert tiles of one token tile run on the same XCD and its x rows come
+// from that XCD's L2 after the first read, rather than once per XCD.
 constexpr int RG_NT = 256;                       // 8 pair groups x 32 chains
 constexpr int RG_TE = 16;                        // experts per workgroup
 constexpr int RG_PE = 8;                         // experts per thread
@@ -59,7 +62,14 @@ __global__ __launch_bounds__(RG_NT) void k_router_logits(const float* __restrict
   constexpr int NW = RG_TE * (RG_KC / 4) / RG_NT;   // and router
   __shared__ __align__(16) float xs[TT * RG_LS];
   __shared__ __align__(16) float ws[RG_TE * RG_LS];
-  const int tb = blockIdx.x * TT, eb = blockIdx.y * RG_TE;
+  int tb, eb;
+  {
+    const int nxcd = 8, eblk = (E + RG_TE - 1) / RG_TE;
+    const int xcd = blockIdx.x % nxcd, j = blockIdx.x / nxcd;
+    tb = ((j / eblk) * nxcd + xcd) * TT;
+    eb = (j % eblk) * RG_TE;
+    if (tb >= T) return;  // padding of the token-tile count to a multiple of 8
+  }
   const int c = threadIdx.x % 32, g = threadIdx.x / 32;
   const int tq = (g % 4) * PT;        // this thread's tokens tb+tq..
   const int eq = (g / 4) * RG_PE;     // and experts eb+eq..
@@ -420,15 +430,13 @@ __global__ __launch_bounds__(GR_NT) void k_group(const int* __restrict__ idx, in
 // [64*(l/32) + 16j, +16) of row (l % 32).  An integer dot is order-free, so
 // this k-permutation, shared by A and B, gives the exact sum.
 // D layout: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, column l%32.
-constexpr int MG_NT = 256;
-constexpr int MG_BN = 128;
 constexpr int MG_KB = 128;   // K bytes per stage
 constexpr int MG_LS = 144;   // padded LDS row stride
 
 __device__ __forceinline__ int4 ldg16(const int8_t* p) { return *(const int4*)p; }
 
-template <bool GATEUP, int MT>
-__global__ __launch_bounds__(MG_NT * MT, 2 / MT) void k_moe_gemm(
+template <bool GATEUP, int MT, int NW>
+__global__ __launch_bounds__(MOTY_WAVE * MT * NW) void k_moe_gemm(
     const int2* __restrict__ tiles, const int* __restrict__ ntiles, const int* __restrict__ offs,
     const int* __restrict__ slot_tok,
     const int8_t* __restrict__ act, const float* __restrict__ act_s,  // GATEUP: xq[T][K], sx[T]; else hq[P][K], sh[P]
@@ -436,9 +444,10 @@ __global__ __launch_bounds__(MG_NT * MT, 2 / MT) void k_moe_gemm(
     const int8_t* __restrict__ W2, const float* __restrict__ S2,      // up (GATEUP only)
     float* __restrict__ out,                                          // [P][N]
     int N, int Kd) {
-  constexpr int NTH = MG_NT * MT;                    // MT groups of 4 waves, one per 64-slot sub-tile
-  constexpr int BM = 64 * MT;                        // slots per M-tile
-  constexpr int BROWS = GATEUP ? 2 * MG_BN : MG_BN;  // staged weight rows
+  constexpr int NTH = MOTY_WAVE * MT * NW;  // MT groups of NW waves, one group per 64-slot sub-tile
+  constexpr int BM = 64 * MT;               // slots per M-tile
+  constexpr int BN = 32 * NW;               // weight rows per N-tile (32 per wave)
+  constexpr int BROWS = GATEUP ? 2 * BN : BN;  // staged weight rows
   constexpr int NA = BM * 8 / NTH;                   // 16 B chunks per thread: A
   constexpr int NBW = BROWS * 8 / NTH;               // and B
   __shared__ __align__(16) int8_t sA[BM * MG_LS];
@@ -450,9 +459,9 @@ __global__ __launch_bounds__(MG_NT * MT, 2 / MT) void k_moe_gemm(
   const int e = tm.x, mb = tm.y;
   const int seg0 = offs[e], nseg = offs[e + 1] - seg0;
   const int tid = threadIdx.x, lane = tid % MOTY_WAVE, wv = tid / MOTY_WAVE;
-  const int sub = wv / 4, wn = wv % 4;  // this wave: sub-tile, 32-row N slice
+  const int sub = wv / NW, wn = wv % NW;  // this wave: sub-tile, 32-row N slice
   const int r32 = lane & 31, h = lane >> 5;
-  const int nb0 = blockIdx.x * MG_BN;
+  const int nb0 = blockIdx.x * BN;
   const int msub = mb + 64 * sub;
   const bool one = (nseg - msub) > 0;   // the sub-tile's halves have rows (wave-uniform)
   const bool two = (nseg - msub) > 32;
@@ -487,8 +496,8 @@ __global__ __launch_bounds__(MG_NT * MT, 2 / MT) void k_moe_gemm(
 #pragma unroll
   for (int i = 0; i < NBW; i++) {
     const int row = (tid + i * NTH) >> 3;
-    const int8_t* W = (GATEUP && row >= MG_BN) ? W2 : W1;
-    int n = nb0 + (row & (MG_BN - 1));
+    const int8_t* W = (GATEUP && row >= BN) ? W2 : W1;
+    int n = nb0 + (GATEUP && row >= BN ? row - BN : row);
     n = n < N ? n : N - 1;
     srcB[i] = W + ((int64_t)e * N + n) * Kd + col;
   }
@@ -522,7 +531,7 @@ __global__ __launch_bounds__(MG_NT * MT, 2 / MT) void k_moe_gemm(
     const int8_t* a0 = sA + (64 * sub + r32) * MG_LS + h * 64;
     const int8_t* a1 = a0 + 32 * MG_LS;
     const int8_t* bg = sB + (wn * 32 + r32) * MG_LS + h * 64;
-    const int8_t* bu = bg + MG_BN * MG_LS;
+    const int8_t* bu = bg + BN * MG_LS;
     if (one) {
 #pragma unroll
       for (int j = 0; j < 4; j++) {
@@ -674,12 +683,11 @@ int launch_moe(const MoeArgs& a, void* scratch, hipStream_t st) {
   // re-reads); measured on MI355X: T=256, E=64: 8.0 us vs 10.5 (8-token);
   // T=1072, E=128: 28.7 us vs 34.7 (4-token)
   const int eblk = (E + RG_TE - 1) / RG_TE;
+  auto rgrid = [&](int tt) { return dim3((unsigned)(((T + tt - 1) / tt + 7) / 8 * 8 * eblk)); };
   if ((int64_t)((T + 3) / 4) * eblk <= 512)
-    hipLaunchKernelGGL(k_router_logits<1>, dim3((T + 3) / 4, eblk), dim3(RG_NT), 0, st, a.x, a.Wr, a.bias, T, D,
-                       E, logits);
+    hipLaunchKernelGGL(k_router_logits<1>, rgrid(4), dim3(RG_NT), 0, st, a.x, a.Wr, a.bias, T, D, E, logits);
   else
-    hipLaunchKernelGGL(k_router_logits<4>, dim3((T + 15) / 16, eblk), dim3(RG_NT), 0, st, a.x, a.Wr, a.bias, T, D,
-                       E, logits);
+    hipLaunchKernelGGL(k_router_logits<4>, rgrid(16), dim3(RG_NT), 0, st, a.x, a.Wr, a.bias, T, D, E, logits);
   LAUNCH_TRY("k_router_logits");
   hipLaunchKernelGGL(k_route_topk, dim3((T + TK_NT / 128 - 1) / (TK_NT / 128)), dim3(TK_NT),
                      (size_t)(TK_NT / 128) * E * 4, st, a.x, logits, T, D, E, K, a.norm, idx, w, xq, sx,
@@ -693,20 +701,20 @@ int launch_moe(const MoeArgs& a, void* scratch, hipStream_t st) {
   LAUNCH_TRY("k_group");
   const int maxt = P / (64 * mt) + E + 1;
   if (mt == 2)
-    hipLaunchKernelGGL((k_moe_gemm<true, 2>), dim3((I + MG_BN - 1) / MG_BN, maxt), dim3(MG_NT * 2), 0, st, tiles,
-                       ntiles, offs, slot_tok, xq, sx, a.G, a.GS, a.U, a.US, h, I, D);
+    hipLaunchKernelGGL((k_moe_gemm<true, 2, 4>), dim3((I + 127) / 128, maxt), dim3(512), 0, st, tiles, ntiles, offs,
+                       slot_tok, xq, sx, a.G, a.GS, a.U, a.US, h, I, D);
   else
-    hipLaunchKernelGGL((k_moe_gemm<true, 1>), dim3((I + MG_BN - 1) / MG_BN, maxt), dim3(MG_NT), 0, st, tiles,
-                       ntiles, offs, slot_tok, xq, sx, a.G, a.GS, a.U, a.US, h, I, D);
+    hipLaunchKernelGGL((k_moe_gemm<true, 1, 4>), dim3((I + 127) / 128, maxt), dim3(256), 0, st, tiles, ntiles, offs,
+                       slot_tok, xq, sx, a.G, a.GS, a.U, a.US, h, I, D);
   LAUNCH_TRY("k_moe_gemm<gateup>");
   int rc = launch_qrow_i8(h, hq, sh, nullptr, P, I, I, I, st);
   if (rc) return rc;
   if (mt == 2)
-    hipLaunchKernelGGL((k_moe_gemm<false, 2>), dim3((D + MG_BN - 1) / MG_BN, maxt), dim3(MG_NT * 2), 0, st, tiles,
-                       ntiles, offs, slot_tok, hq, sh, a.Dn, a.DS, nullptr, nullptr, y, D, I);
+    hipLaunchKernelGGL((k_moe_gemm<false, 2, 4>), dim3((D + 127) / 128, maxt), dim3(512), 0, st, tiles, ntiles, offs,
+                       slot_tok, hq, sh, a.Dn, a.DS, nullptr, nullptr, y, D, I);
   else
-    hipLaunchKernelGGL((k_moe_gemm<false, 1>), dim3((D + MG_BN - 1) / MG_BN, maxt), dim3(MG_NT), 0, st, tiles,
-                       ntiles, offs, slot_tok, hq, sh, a.Dn, a.DS, nullptr, nullptr, y, D, I);
+    hipLaunchKernelGGL((k_moe_gemm<false, 1, 4>), dim3((D + 127) / 128, maxt), dim3(256), 0, st, tiles, ntiles, offs,
+                       slot_tok, hq, sh, a.Dn, a.DS, nullptr, nullptr, y, D, I);
   LAUNCH_TRY("k_moe_gemm<down>");
   hipLaunchKernelGGL(k_moe_combine, dim3(T, (D / 4 + 255) / 256), dim3(256), 0, st, y, idx, w, pair_slot, a.out, D,
                      K, a.order);
