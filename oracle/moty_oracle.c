@@ -22,6 +22,12 @@
  *   o_softmax, o_silu_mul, o_topk -> _ref, naive greedy top-k
  *   o_moe_batch / o_moe_olmoe -> _ref (moty_nn_moe_topk_batch and the
  *       olmoe call sequence), plus the permutation property of the grouping
+ *   o_f16_to_f32 / o_f32_to_f16 -> every half round-trips, numpy's IEEE
+ *       binary16 conversions, _ref
+ *   o_quant_g32, o_pack_q4r4, o_pack_q8r4, o_matmul_q4r4, o_matmul_q8r4 ->
+ *       _ref bit-exact (moty_hw_quant_g32, moty_pack_q{4,8}r4_block,
+ *       moty_matmul_q{4,8}r4_s), the no-clip packing bounds and the double
+ *       dequantized reference of c/tests/q4r4_tests.c
  */
 #include <math.h>
 #include <stdint.h>
@@ -462,4 +468,191 @@ O_EXPORT void o_dense_ffn_q8(float *out, const float *x, int S, const int8_t *G,
     o_silu_mul(g, u, (int64_t)S * I);
     o_matmul_q_s(out, g, Dn, DS, S, I, D);
     free(g); free(u);
+}
+
+/* ------------------------------------------------------------------ */
+/* Q4R4 / Q8R4: 4-row blocks, groups of 32, f16 group scales.          */
+/* hw/hw_q4r4.h, nn/quant.c:110-179, nn/matmul.c:365-466               */
+
+/* IEEE half -> float, exact (hw/hw_q4r4.h:22-33) */
+O_EXPORT float o_f16_to_f32(uint16_t h) {
+    uint32_t s = (uint32_t)(h & 0x8000) << 16, e = (h >> 10) & 0x1f, m = h & 0x3ff, u;
+    if (e == 0) {
+        if (m == 0) u = s;
+        else {
+            int ee = 1;
+            while (!(m & 0x400)) { m <<= 1; ee--; }
+            m &= 0x3ff;
+            u = s | ((uint32_t)(ee + 112) << 23) | (m << 13);
+        }
+    } else if (e == 31) u = s | 0x7f800000u | (m << 13);
+    else u = s | ((e + 112) << 23) | (m << 13);
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* float -> IEEE half, round to nearest even (nn/quant.c:111-128) */
+O_EXPORT uint16_t o_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000, e = (x >> 23) & 0xff, m = x & 0x7fffff;
+    if (e == 0xff) return (uint16_t)(sign | 0x7c00 | (m ? 0x200 : 0));
+    int ne = (int)e - 127 + 15;
+    if (ne >= 31) return (uint16_t)(sign | 0x7c00);
+    if (ne <= 0) {
+        if (ne < -10) return (uint16_t)sign;
+        m |= 0x800000;
+        int sh = 14 - ne;
+        uint32_t h = m >> sh, rem = m & ((1u << sh) - 1), half = 1u << (sh - 1);
+        if (rem > half || (rem == half && (h & 1))) h++;
+        return (uint16_t)(sign | h);
+    }
+    uint32_t h = ((uint32_t)ne << 10) | (m >> 13), rem = m & 0x1fff;
+    if (rem > 0x1000 || (rem == 0x1000 && (h & 1))) h++;
+    return (uint16_t)(sign | h);
+}
+
+/* group-32 activation quantization (hw/hw_q4r4.h:36-46): per group
+ * s = amax/127 clamped at 1e-30, inv = 1/s, q = rint(x*inv), xsum = sum q */
+O_EXPORT void o_quant_g32(const float *x, int I, int8_t *xq, float *xs, int32_t *xsum) {
+    for (int g = 0; g < I / 32; g++) {
+        const float *xg = x + g * 32;
+        float amax = 0.f;
+        for (int j = 0; j < 32; j++) { float a = fabsf(xg[j]); if (a > amax) amax = a; }
+        float s = amax / 127.f;
+        if (s < 1e-30f) s = 1e-30f;
+        float inv = 1.f / s;
+        int32_t sm = 0;
+        for (int j = 0; j < 32; j++) { int q = (int)rintf(xg[j] * inv); xq[g * 32 + j] = (int8_t)q; sm += q; }
+        xs[g] = s;
+        xsum[g] = sm;
+    }
+}
+
+/* the "no-clip Q4_0" group scale shared by both packers (nn/quant.c:130-177):
+ * mx = the group's largest-magnitude weight (first one wins ties), opp = the
+ * largest |w| of the other sign, d = -sign(mx) * max(|mx|/lo, opp/hi) as f16 */
+static uint16_t r4_scale(const float *wg, float lo, float hi, float *inv) {
+    float mx = 0.f;
+    for (int j = 0; j < 32; j++) if (fabsf(wg[j]) > fabsf(mx)) mx = wg[j];
+    float opp = 0.f;
+    for (int j = 0; j < 32; j++) if ((wg[j] > 0) != (mx > 0) && fabsf(wg[j]) > opp) opp = fabsf(wg[j]);
+    float dm = fmaxf(fabsf(mx) / lo, opp / hi);
+    uint16_t h = o_f32_to_f16(mx > 0 ? -dm : dm);
+    float dd = o_f16_to_f32(h);
+    *inv = dd != 0.f ? 1.f / dd : 0.f;
+    return h;
+}
+
+/* w [O][I] f32 (I % 32 == 0) -> q [ceil(O/4)][I/32][4][16] (row r byte j =
+ * c[j] | c[j+16] << 4, c = v + 8), d [ceil(O/4)][I/32][4] f16; missing rows
+ * of the last block: codes 0x88, scale 0 (nn/quant.c:157-177) */
+O_EXPORT void o_pack_q4r4(const float *w, int O, int I, uint8_t *q, uint16_t *d) {
+    int nb = I / 32, O4 = (O + 3) / 4;
+    for (int b = 0; b < O4; b++)
+        for (int g = 0; g < nb; g++)
+            for (int r = 0; r < 4; r++) {
+                uint8_t *dst = q + ((size_t)b * nb + g) * 64 + r * 16;
+                uint16_t *dp = d + ((size_t)b * nb + g) * 4 + r;
+                int row = b * 4 + r;
+                if (row >= O) { memset(dst, 0x88, 16); *dp = 0; continue; }
+                const float *wg = w + (size_t)row * I + g * 32;
+                float inv;
+                *dp = r4_scale(wg, 8.f, 7.f, &inv);
+                uint8_t c[32];
+                for (int j = 0; j < 32; j++) {
+                    int v = (int)rintf(wg[j] * inv);
+                    if (v < -8) v = -8;
+                    if (v > 7) v = 7;
+                    c[j] = (uint8_t)(v + 8);
+                }
+                for (int j = 0; j < 16; j++) dst[j] = (uint8_t)(c[j] | (c[j + 16] << 4));
+            }
+}
+
+/* the int8 sibling: [ceil(O/4)][I/32][4][32] signed codes (nn/quant.c:135-155) */
+O_EXPORT void o_pack_q8r4(const float *w, int O, int I, int8_t *q, uint16_t *d) {
+    int nb = I / 32, O4 = (O + 3) / 4;
+    for (int b = 0; b < O4; b++)
+        for (int g = 0; g < nb; g++)
+            for (int r = 0; r < 4; r++) {
+                int8_t *dst = q + ((size_t)b * nb + g) * 128 + r * 32;
+                uint16_t *dp = d + ((size_t)b * nb + g) * 4 + r;
+                int row = b * 4 + r;
+                if (row >= O) { memset(dst, 0, 32); *dp = 0; continue; }
+                const float *wg = w + (size_t)row * I + g * 32;
+                float inv;
+                *dp = r4_scale(wg, 128.f, 127.f, &inv);
+                for (int j = 0; j < 32; j++) {
+                    int v = (int)rintf(wg[j] * inv);
+                    if (v < -128) v = -128;
+                    if (v > 127) v = 127;
+                    dst[j] = (int8_t)v;
+                }
+            }
+}
+
+/* Q4R4 matmul, the x86 build's evaluation (portable kernels = the scalar
+ * references, nn/matmul.c:395-431).  Tokens t < 4*floor(S/4) go through the
+ * 4-token tile kernel (hw/hw_q4r4.h:70-87): raw sum s = sum c*x over the
+ * group, then acc = fma(s, dd*xs, acc) and acc = fma(-dd, xct, acc) with
+ * xct = (8*xsum)*xs rounded once (:89-96).  The remaining tokens go through
+ * the per-token kernel (:48-64): s -= 8*xsum in integers, acc = fma(s,
+ * dd*xs, acc).  Groups in order; y [S][O]. */
+O_EXPORT void o_matmul_q4r4(float *y, const float *x, const uint8_t *q, const uint16_t *d, int S, int I, int O) {
+    int nb = I / 32, S4 = S / 4 * 4;
+    int8_t *xq = malloc((size_t)I);
+    float *xs = malloc(sizeof(float) * nb);
+    int32_t *xm = malloc(sizeof(int32_t) * nb);
+    for (int t = 0; t < S; t++) {
+        o_quant_g32(x + (size_t)t * I, I, xq, xs, xm);
+        for (int o = 0; o < O; o++) {
+            int b = o / 4, r = o % 4;
+            float acc = 0.f;
+            for (int g = 0; g < nb; g++) {
+                const uint8_t *wb = q + ((size_t)b * nb + g) * 64 + r * 16;
+                const int8_t *xg = xq + g * 32;
+                int32_t s = 0;
+                for (int j = 0; j < 16; j++) s += (int32_t)(wb[j] & 0xF) * xg[j] + (int32_t)(wb[j] >> 4) * xg[j + 16];
+                float dd = o_f16_to_f32(d[((size_t)b * nb + g) * 4 + r]);
+                if (t < S4) {
+                    float xct = 8.f * (float)xm[g] * xs[g];
+                    acc = fmaf((float)s, dd * xs[g], acc);
+                    acc = fmaf(-dd, xct, acc);
+                } else {
+                    s -= 8 * xm[g];
+                    acc = fmaf((float)s, dd * xs[g], acc);
+                }
+            }
+            y[(size_t)t * O + o] = acc;
+        }
+    }
+    free(xq); free(xs); free(xm);
+}
+
+/* Q8R4 matmul (nn/matmul.c:435-466): one formula for both kernels,
+ * acc = fma(sum c*x, dd*xs, acc) over the groups in order */
+O_EXPORT void o_matmul_q8r4(float *y, const float *x, const int8_t *q, const uint16_t *d, int S, int I, int O) {
+    int nb = I / 32;
+    int8_t *xq = malloc((size_t)I);
+    float *xs = malloc(sizeof(float) * nb);
+    int32_t *xm = malloc(sizeof(int32_t) * nb);
+    for (int t = 0; t < S; t++) {
+        o_quant_g32(x + (size_t)t * I, I, xq, xs, xm);
+        for (int o = 0; o < O; o++) {
+            int b = o / 4, r = o % 4;
+            float acc = 0.f;
+            for (int g = 0; g < nb; g++) {
+                const int8_t *wr = q + ((size_t)b * nb + g) * 128 + r * 32;
+                const int8_t *xg = xq + g * 32;
+                int32_t s = 0;
+                for (int j = 0; j < 32; j++) s += (int32_t)wr[j] * xg[j];
+                float dd = o_f16_to_f32(d[((size_t)b * nb + g) * 4 + r]);
+                acc = fmaf((float)s, dd * xs[g], acc);
+            }
+            y[(size_t)t * O + o] = acc;
+        }
+    }
+    free(xq); free(xs); free(xm);
 }

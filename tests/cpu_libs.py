@@ -44,6 +44,21 @@ _SIGS = {
     "o_moe_olmoe": (None, [P, P, I32, P, P, P, P, P, P, P, P, I32, I32, I32, I32, I32, P, P]),
     "o_moe_batch": (None, [P, P, I32, P, P, P, P, P, P, P, P, I32, I32, I32, I32, P, P]),
     "o_dense_ffn_q8": (None, [P, P, I32, P, P, P, P, P, P, I32, I32]),
+    "o_f16_to_f32": (F32, [C.c_uint16]),
+    "o_f32_to_f16": (C.c_uint16, [F32]),
+    "o_quant_g32": (None, [P, I32, P, P, P]),
+    "o_pack_q4r4": (None, [P, I32, I32, P, P]),
+    "o_pack_q8r4": (None, [P, I32, I32, P, P]),
+    "o_matmul_q4r4": (None, [P, P, P, P, I32, I32, I32]),
+    "o_matmul_q8r4": (None, [P, P, P, P, I32, I32, I32]),
+    # the reference's own R4 symbols (nn/quant.c, hw/hw_q4r4.h, nn/matmul.c)
+    "moty_hw_f16_to_f32": (F32, [C.c_uint16]),
+    "moty_f32_to_f16": (C.c_uint16, [F32]),
+    "moty_hw_quant_g32": (None, [P, I32, P, P, P]),
+    "moty_pack_q4r4_block": (None, [P, I32, I32, P, P]),
+    "moty_pack_q8r4_block": (None, [P, I32, I32, P, P]),
+    "moty_matmul_q4r4_s": (None, [P, P, P, P, I32, I32, I32]),
+    "moty_matmul_q8r4_s": (None, [P, P, P, P, I32, I32, I32]),
     "ref_init": (None, [I32]),
     "ref_tier": (C.c_char_p, []),
     "ref_qrow_i8": (F32, [P, P, I32]),
@@ -223,3 +238,63 @@ def rng(seed):
 
 def randn(seed, shape, std=1.0):
     return (rng(seed).standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
+
+
+# ---- R4 formats (Q4R4 / Q8R4) ----
+def r4_sizes(O, I, q8):
+    O4, nb = (O + 3) // 4, I // 32
+    return O4 * nb * (128 if q8 else 64), O4 * nb * 4
+
+
+def o_quant_g32(x):
+    x = f32(x)
+    S, I = x.shape
+    xq = np.empty((S, I), np.int8)
+    xs = np.empty((S, I // 32), np.float32)
+    xm = np.empty((S, I // 32), np.int32)
+    for t in range(S):
+        oracle().o_quant_g32(C.c_void_p(x.ctypes.data + t * I * 4), I, C.c_void_p(xq.ctypes.data + t * I),
+                             C.c_void_p(xs.ctypes.data + t * (I // 32) * 4), C.c_void_p(xm.ctypes.data + t * (I // 32) * 4))
+    return xq, xs, xm
+
+
+def o_pack_r4(w, q8=False):
+    """(codes uint8/int8 flat, f16 scales uint16 flat) in the R4 layout."""
+    w = f32(w)
+    O, I = w.shape
+    nq, nd = r4_sizes(O, I, q8)
+    q = np.empty(nq, np.int8 if q8 else np.uint8)
+    d = np.empty(nd, np.uint16)
+    (oracle().o_pack_q8r4 if q8 else oracle().o_pack_q4r4)(ptr(w), O, I, ptr(q), ptr(d))
+    return q, d
+
+
+def o_matmul_r4(x, q, d, O, q8=False):
+    x = f32(x)
+    S, I = x.shape
+    y = np.empty((S, O), np.float32)
+    (oracle().o_matmul_q8r4 if q8 else oracle().o_matmul_q4r4)(ptr(y), ptr(x), ptr(q), ptr(d), S, I, O)
+    return y
+
+
+def ref_pack_r4(r, w, q8=False):
+    """The reference's block packer over every 4-row block."""
+    w = f32(w)
+    O, I = w.shape
+    nq, nd = r4_sizes(O, I, q8)
+    q = np.empty(nq, np.int8 if q8 else np.uint8)
+    d = np.empty(nd, np.uint16)
+    nb, gb = I // 32, (128 if q8 else 64)
+    fn = r.moty_pack_q8r4_block if q8 else r.moty_pack_q4r4_block
+    for b in range((O + 3) // 4):
+        fn(C.c_void_p(w.ctypes.data + b * 4 * I * 4), min(4, O - 4 * b), I,
+           C.c_void_p(q.ctypes.data + b * nb * gb), C.c_void_p(d.ctypes.data + b * nb * 4 * 2))
+    return q, d
+
+
+def ref_matmul_r4(r, x, q, d, O, q8=False):
+    x = f32(x)
+    S, I = x.shape
+    y = np.empty((S, O), np.float32)
+    (r.moty_matmul_q8r4_s if q8 else r.moty_matmul_q4r4_s)(ptr(y), ptr(x), ptr(q), ptr(d), S, I, O)
+    return y
