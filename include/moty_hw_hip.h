@@ -65,6 +65,15 @@ int moty_hip_matmul_q_s(float *y, const float *x, const int8_t *q, const float *
  * anything else the exact f32 path (served for gs == 32, I % 32 == 0). */
 int moty_hip_matmul_i4_grouped_s(float *y, const float *x, const uint8_t *q4, const float *scale, int S, int I,
                                  int O, int gs);
+/* moty_matmul_q4r4_s (nn/nn_matmul.h:72, nn/matmul.c:395-431): Q4R4 weights
+ * (nn/quant.c:157-177) -- 4-row blocks, per (block, group of 32) 64 bytes of
+ * packed codes q4 [ceil(O/4)][I/32][4][16] and f16 scales s16
+ * [ceil(O/4)][I/32][4]; activations quantized per group of 32
+ * (moty_hw_quant_g32).  I % 32 == 0. */
+int moty_hip_matmul_q4r4_s(float *y, const float *x, const uint8_t *q4, const uint16_t *s16, int S, int I, int O);
+/* moty_matmul_q8r4_s (nn/nn_matmul.h:70, nn/matmul.c:435-466): the int8
+ * sibling, q8 [ceil(O/4)][I/32][4][32] signed codes, same scale stream. */
+int moty_hip_matmul_q8r4_s(float *y, const float *x, const int8_t *q8, const uint16_t *s16, int S, int I, int O);
 /* moty_matmul (nn/nn_matmul.h:63, nn/matmul.c:15-27): f32 W [O][I], dot_f32
  * in the AVX512 order (hw/hw_avx512.h:231-243).  The f32 MoE router. */
 int moty_hip_matmul(float *y, const float *x, const float *W, int S, int I, int O);
@@ -144,6 +153,21 @@ int moty_hip_gate_up_silu_q8_dev(float *h, const float *x, int S, const int8_t *
  * activations): h [I] = silu(x.gate^T) * (x.up^T), one token, D % 64 == 0. */
 int moty_hip_gate_up_silu_i4g_dev(float *h, const float *x, const uint8_t *gate, const float *gs,
                                   const uint8_t *up, const float *us, int D, int I, void *stream);
+/* moty_matmul_q4r4_s / moty_matmul_q8r4_s on device pointers: S <= 4 runs
+ * the decode GEMV with fused activation quantization, larger S quantizes
+ * then runs the MFMA GEMM (tokens below 4*floor(S/4) in the reference's
+ * 4-token tile form, the rest in its per-token form). */
+int moty_hip_matmul_q4r4_s_dev(float *y, const float *x, const uint8_t *q4, const uint16_t *s16, int S, int I, int O,
+                               void *stream);
+int moty_hip_matmul_q8r4_s_dev(float *y, const float *x, const int8_t *q8, const uint16_t *s16, int S, int I, int O,
+                               void *stream);
+/* moty_hw_quant_g32 (hw/hw_q4r4.h:36-46) over S rows: xq [S][I], xs and
+ * xsum [S][I/32] */
+int moty_hip_quant_g32_dev(const float *x, int8_t *xq, float *xs, int32_t *xsum, int S, int I, void *stream);
+/* Weight packers: moty_pack_q4r4_block / moty_pack_q8r4_block
+ * (nn/quant.c:135-177) over every 4-row block of w [O][I] f32. */
+int moty_hip_pack_q4r4_dev(const float *w, uint8_t *q4, uint16_t *s16, int O, int I, void *stream);
+int moty_hip_pack_q8r4_dev(const float *w, int8_t *q8, uint16_t *s16, int O, int I, void *stream);
 /* the MoE layer, all pointers in m and x/out on the device */
 int moty_hip_moe_topk_dev(const MotyHipMoe *m, const float *x, int S, float *out, void *stream);
 

@@ -36,6 +36,13 @@ SIGNATURES = {
     "moty_hip_kernel_tier": (C.c_char_p, []),
     "moty_hip_matmul_q_s": (I32, [P, P, P, P, I32, I32, I32]),
     "moty_hip_matmul_i4_grouped_s": (I32, [P, P, P, P, I32, I32, I32, I32]),
+    "moty_hip_matmul_q4r4_s": (I32, [P, P, P, P, I32, I32, I32]),
+    "moty_hip_matmul_q8r4_s": (I32, [P, P, P, P, I32, I32, I32]),
+    "moty_hip_matmul_q4r4_s_dev": (I32, [P, P, P, P, I32, I32, I32, P]),
+    "moty_hip_matmul_q8r4_s_dev": (I32, [P, P, P, P, I32, I32, I32, P]),
+    "moty_hip_quant_g32_dev": (I32, [P, P, P, P, I32, I32, P]),
+    "moty_hip_pack_q4r4_dev": (I32, [P, P, P, I32, I32, P]),
+    "moty_hip_pack_q8r4_dev": (I32, [P, P, P, I32, I32, P]),
     "moty_hip_matmul": (I32, [P, P, P, I32, I32, I32]),
     "moty_hip_moe_topk": (I32, [C.POINTER(MotyHipMoe), P, I32, P]),
     "moty_hip_weight_forget": (I32, [P]),

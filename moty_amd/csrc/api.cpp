@@ -427,6 +427,92 @@ int moty_hip_matmul_q_s(float* y, const float* x, const int8_t* q, const float* 
   return finish_io(d, y, dy, (size_t)S * O * 4);
 }
 
+// ---- Q4R4 / Q8R4 (nn/matmul.c:365-466) ----
+static int r4_check(const char* what, int S, int I, int O, const void* y, const void* x, const void* q,
+                    const void* s16) {
+  if (S < 0 || I <= 0 || O < 0 || !y || !x || !q || !s16) return set_error("%s: bad arguments", what), MOTY_EINVAL;
+  if (I % 32) return set_error("%s: I=%d must be a multiple of 32", what, I), MOTY_EINVAL;
+  return MOTY_OK;
+}
+
+static int r4_dev(bool q8, const char* what, float* y, const float* x, const uint8_t* q, const uint16_t* s16, int S,
+                  int I, int O, void* stream) {
+  CUR(d);
+  int rc = r4_check(what, S, I, O, y, x, q, s16);
+  if (rc || S == 0 || O == 0) return rc;
+  void* sp = nullptr;
+  int8_t* xq = nullptr;
+  float* xs = nullptr;
+  int32_t* xm = nullptr;
+  {  // activation scratch for the GEMM path (also taken by S <= 4 when the
+     // decode GEMV does not serve the shape)
+    const size_t bq = al256((size_t)S * I), bs = al256((size_t)S * (I / 32) * 4);
+    if ((rc = arena_get(d->scratch, bq + 2 * bs, &sp))) return rc;
+    xq = (int8_t*)sp;
+    xs = (float*)((char*)sp + bq);
+    xm = (int32_t*)((char*)sp + bq + bs);
+  }
+  rc = launch_r4_matmul(q8, x, q, s16, y, S, I, O, xq, xs, xm, STREAM(stream));
+  if (rc == MOTY_EUNSUP) set_error("%s: shape S=%d I=%d O=%d unsupported", what, S, I, O);
+  return rc;
+}
+
+int moty_hip_matmul_q4r4_s_dev(float* y, const float* x, const uint8_t* q4, const uint16_t* s16, int S, int I, int O,
+                               void* stream) {
+  return r4_dev(false, "matmul_q4r4_s", y, x, q4, s16, S, I, O, stream);
+}
+
+int moty_hip_matmul_q8r4_s_dev(float* y, const float* x, const int8_t* q8, const uint16_t* s16, int S, int I, int O,
+                               void* stream) {
+  return r4_dev(true, "matmul_q8r4_s", y, x, (const uint8_t*)q8, s16, S, I, O, stream);
+}
+
+static int r4_host(bool q8, const char* what, float* y, const float* x, const void* q, const uint16_t* s16, int S,
+                   int I, int O) {
+  CUR(d);
+  int rc = r4_check(what, S, I, O, y, x, q, s16);
+  if (rc || S == 0 || O == 0) return rc;
+  const size_t blocks = (size_t)((O + 3) / 4) * (I / 32);
+  const void *dq, *ds;
+  if ((rc = weight(d, q, blocks * (q8 ? 128 : 64), &dq))) return rc;
+  if ((rc = weight(d, s16, blocks * 8, &ds))) return rc;
+  void *dx, *dy;
+  if ((rc = stage_io(d, x, (size_t)S * I * 4, (size_t)S * O * 4, &dx, &dy))) return rc;
+  if ((rc = r4_dev(q8, what, (float*)dy, (const float*)dx, (const uint8_t*)dq, (const uint16_t*)ds, S, I, O,
+                   d->stream)))
+    return rc;
+  return finish_io(d, y, dy, (size_t)S * O * 4);
+}
+
+int moty_hip_matmul_q4r4_s(float* y, const float* x, const uint8_t* q4, const uint16_t* s16, int S, int I, int O) {
+  return r4_host(false, "matmul_q4r4_s", y, x, q4, s16, S, I, O);
+}
+
+int moty_hip_matmul_q8r4_s(float* y, const float* x, const int8_t* q8, const uint16_t* s16, int S, int I, int O) {
+  return r4_host(true, "matmul_q8r4_s", y, x, q8, s16, S, I, O);
+}
+
+int moty_hip_quant_g32_dev(const float* x, int8_t* xq, float* xs, int32_t* xsum, int S, int I, void* stream) {
+  CUR(d);
+  if (S < 0 || I <= 0 || !x || !xq || !xs || !xsum) return set_error("quant_g32: bad arguments"), MOTY_EINVAL;
+  if (I % 32) return set_error("quant_g32: I=%d must be a multiple of 32", I), MOTY_EINVAL;
+  return launch_quant_g32(x, xq, xs, xsum, S, I, STREAM(stream));
+}
+
+int moty_hip_pack_q4r4_dev(const float* w, uint8_t* q4, uint16_t* s16, int O, int I, void* stream) {
+  CUR(d);
+  if (O < 0 || I <= 0 || !w || !q4 || !s16) return set_error("pack_q4r4: bad arguments"), MOTY_EINVAL;
+  if (I % 32) return set_error("pack_q4r4: I=%d must be a multiple of 32", I), MOTY_EINVAL;
+  return launch_pack_r4(false, w, q4, s16, O, I, STREAM(stream));
+}
+
+int moty_hip_pack_q8r4_dev(const float* w, int8_t* q8, uint16_t* s16, int O, int I, void* stream) {
+  CUR(d);
+  if (O < 0 || I <= 0 || !w || !q8 || !s16) return set_error("pack_q8r4: bad arguments"), MOTY_EINVAL;
+  if (I % 32) return set_error("pack_q8r4: I=%d must be a multiple of 32", I), MOTY_EINVAL;
+  return launch_pack_r4(true, w, (uint8_t*)q8, s16, O, I, STREAM(stream));
+}
+
 void moty_hip_hw_matmul_i8(float* y, const float* x, const int8_t* q, const float* scale, int S, int I, int O) {
   (void)moty_hip_matmul_q_s(y, x, q, scale, S, I, O);
 }

@@ -63,7 +63,6 @@ __device__ __forceinline__ float ref_silu_mul(float g, float u) {
   return (g / (1.f + ref_expf(-g))) * u;
 }
 
-// lrintf under the default round-to-nearest-even mode, as an int.
 // Branch-free "ok ? v : 0" for a value loaded from a clamped (always valid)
 // address: a predicated load would split the wave's loads into branches and
 // force a wait for every load in flight at the join.
@@ -73,7 +72,19 @@ __device__ __forceinline__ int4 sel4(bool ok, int4 v) {
 __device__ __forceinline__ float4 sel4(bool ok, float4 v) {
   return float4{ok ? v.x : 0.f, ok ? v.y : 0.f, ok ? v.z : 0.f, ok ? v.w : 0.f};
 }
+// lrintf under the default round-to-nearest-even mode, as an int.
 __device__ __forceinline__ int rne_int(float v) { return (int)__builtin_rintf(v); }
+
+// IEEE half (bits) -> float, exact for every half (hw/hw_q4r4.h:22-33):
+// normals and inf/nan by re-biasing, subnormals as m * 2^-24 (exact: m has
+// 10 bits and the product is a normal float).
+__device__ __forceinline__ float f16_to_f32(uint32_t h) {
+  const uint32_t s = (h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  const uint32_t un = s | ((e + 112u) << 23) | (m << 13);
+  const uint32_t ui = s | 0x7f800000u | (m << 13);
+  const uint32_t us = s | __float_as_uint((float)m * 5.9604644775390625e-8f);
+  return __uint_as_float(e == 0u ? us : (e == 31u ? ui : un));
+}
 
 // ---------------------------------------------------------------------------
 // wave64 reductions

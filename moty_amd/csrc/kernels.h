@@ -30,6 +30,14 @@ int launch_gemm_i4g(const int8_t* xq, const float* sx, const uint8_t* q4, const 
 int launch_i4g_f32(const float* x, const uint8_t* q4, const float* scl, float* y, int S, int I, int O,
                    hipStream_t st);
 
+// Q4R4 / Q8R4 (f16 group scales, 4-row blocks): group-32 activation
+// quantization, the matmul (xq/xs/xm: activation scratch of S*I bytes and
+// S*(I/32) floats and ints, used when S > 4) and the packers
+int launch_quant_g32(const float* x, int8_t* xq, float* xs, int32_t* xm, int S, int I, hipStream_t st);
+int launch_r4_matmul(bool q8, const float* x, const uint8_t* W, const uint16_t* d16, float* y, int S, int I, int O,
+                     int8_t* xq, float* xs, int32_t* xm, hipStream_t st);
+int launch_pack_r4(bool q8, const float* w, uint8_t* q, uint16_t* d16, int O, int I, hipStream_t st);
+
 int launch_matmul_f32(const float* x, const float* W, float* y, int S, int I, int O, hipStream_t st);
 int launch_silu_mul(float* g, const float* u, int64_t n, hipStream_t st);
 int launch_expf(const float* x, float* y, int64_t n, hipStream_t st);

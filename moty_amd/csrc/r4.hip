@@ -1,0 +1,566 @@
+// r4.hip -- Q4R4 / Q8R4 matmuls: 4-row blocks, groups of 32, f16 group
+// scales, group-32 int8 activations.
+//
+// Reference: hw/hw_q4r4.h (format, kernels), nn/quant.c:110-179 (packers),
+// nn/matmul.c:365-466 (moty_matmul_q4r4_s / moty_matmul_q8r4_s).
+//
+// Layout (unchanged from the reference): weight rows in blocks of 4; per
+// (block, group) Q4R4 stores 64 bytes = 4 rows x 16 bytes, row byte j =
+// c[j] | c[j+16] << 4 with codes c = v + 8 in 0..15; Q8R4 stores 128 bytes =
+// 4 rows x 32 signed codes.  Scales: f16 [block][group][4].
+//
+// Activations: per group of 32, s = amax/127 (clamped at 1e-30), q =
+// rint(x/s) and the code sum xsum (hw/hw_q4r4.h:36-46).
+//
+// Arithmetic, as the reference's x86 build evaluates it (its portable
+// kernels are the scalar references): per output, groups in order,
+//   tokens t < 4*floor(S/4) (the 4-token tile kernel):
+//       s = sum c*x;  acc = fma(s, dd*xs, acc);  acc = fma(-dd, (8*xsum)*xs, acc)
+//   the remaining tokens (the per-token kernel):
+//       s = sum c*x - 8*xsum;  acc = fma(s, dd*xs, acc)
+//   Q8R4 (no offset): acc = fma(sum c*x, dd*xs, acc).
+// The integer group sums are exact, so only the float chain's order is
+// fixed; the kernels below keep it.
+#include "common.h"
+#include "kernels.h"
+
+namespace moty {
+
+// ---------------------------------------------------------------------------
+// Group-32 activation quantization: 8 lanes per group, 4 elements per lane.
+__global__ __launch_bounds__(256) void k_quant_g32(const float* __restrict__ x, int8_t* __restrict__ xq,
+                                                   float* __restrict__ xs, int32_t* __restrict__ xm, int I) {
+  const int64_t row = blockIdx.y;
+  const int e = (blockIdx.x * 256 + threadIdx.x) * 4;
+  const bool ok = e < I;
+  const float4 v = sel4(ok, *(const float4*)(x + row * I + (ok ? e : 0)));
+  float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+  float s = amax / 127.f;
+  if (s < 1e-30f) s = 1e-30f;
+  const float inv = 1.f / s;
+  const int a = rne_int(v.x * inv), b = rne_int(v.y * inv), c = rne_int(v.z * inv), d = rne_int(v.w * inv);
+  int sum = a + b + c + d;
+  sum += __shfl_xor(sum, 1, 64);
+  sum += __shfl_xor(sum, 2, 64);
+  sum += __shfl_xor(sum, 4, 64);
+  if (!ok) return;
+  *(uint32_t*)(xq + row * I + e) = (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) |
+                                   ((uint32_t)(c & 0xff) << 16) | ((uint32_t)(d & 0xff) << 24);
+  if ((threadIdx.x & 7) == 0) {
+    const int nb = I / 32;
+    xs[row * nb + e / 32] = s;
+    xm[row * nb + e / 32] = sum;
+  }
+}
+
+int launch_quant_g32(const float* x, int8_t* xq, float* xs, int32_t* xm, int S, int I, hipStream_t st) {
+  if (S <= 0) return MOTY_OK;
+  if (I % 32) return MOTY_EUNSUP;
+  hipLaunchKernelGGL(k_quant_g32, dim3((I + 1023) / 1024, S), dim3(256), 0, st, x, xq, xs, xm, I);
+  LAUNCH_TRY("k_quant_g32");
+  return MOTY_OK;
+}
+
+// low / high nibbles of 16 packed Q4R4 bytes as 16 + 16 unsigned int8 codes
+__device__ __forceinline__ int4 r4_lo(int4 w) {
+  return int4{w.x & 0x0f0f0f0f, w.y & 0x0f0f0f0f, w.z & 0x0f0f0f0f, w.w & 0x0f0f0f0f};
+}
+__device__ __forceinline__ int4 r4_hi(int4 w) {
+  return int4{(w.x >> 4) & 0x0f0f0f0f, (w.y >> 4) & 0x0f0f0f0f, (w.z >> 4) & 0x0f0f0f0f, (w.w >> 4) & 0x0f0f0f0f};
+}
+
+// ---------------------------------------------------------------------------
+// Decode GEMV, S_ <= 4 tokens, I <= 1024*IC.  Workgroup = 4 waves; a wave
+// owns one 4-row block.  Order of the loads: the activation rows first (4
+// floats per thread per 1 KiB), then every 16-byte chunk of the wave's block
+// (lane l takes chunks l, l+64, ...: each load instruction reads 1 KiB of
+// the contiguous block) and its f16 scales -- all issued before any is
+// consumed.  The workgroup quantizes the activation rows into LDS from
+// registers (every workgroup derives the same codes); each lane forms the
+// exact integer group sums of its chunks (Q8R4: half a row per chunk, the
+// halves joined across the lane pair) and parks them in the wave's LDS
+// slice; one lane per (row, token) runs the reference's float chain over the
+// groups in order.
+constexpr int R4V_NT = 256;
+
+template <bool Q8, int S_, int IC>
+__global__ __launch_bounds__(R4V_NT) void k_r4_gemv(const float* __restrict__ x, const uint8_t* __restrict__ W,
+                                                    const uint16_t* __restrict__ d16, float* __restrict__ y, int S,
+                                                    int I, int O) {
+  constexpr int GB = Q8 ? 128 : 64;        // bytes per (block, group)
+  constexpr int NCH = IC * (Q8 ? 4 : 2);   // weight chunks per lane
+  constexpr int DCH = (IC + 1) / 2;        // scale chunks (groups) per lane
+  constexpr int WAVES = R4V_NT / MOTY_WAVE;
+  extern __shared__ __align__(16) int8_t lds[];
+  const int nb = I / 32, O4 = (O + 3) / 4;
+  const int lane = threadIdx.x % MOTY_WAVE, wv = threadIdx.x / MOTY_WAVE;
+  // LDS: xq [S_][I] | xs [S_][nb] | xm [S_][nb] | per wave: sums [nb][4][S_], dd [nb][4]
+  int8_t* xq_s = lds;
+  float* xs_s = (float*)(lds + S_ * I);
+  int* xm_s = (int*)(xs_s + S_ * nb);
+  int* sum_s = (int*)(xm_s + S_ * nb) + (size_t)wv * (nb * 4 * S_ + nb * 4);
+  float* dd_s = (float*)(sum_s + nb * 4 * S_);
+  int blk = blockIdx.x * WAVES + wv;
+  const bool live = blk < O4;
+  blk = live ? blk : O4 - 1;
+
+  // 1. activation rows, then every weight and scale chunk of the block
+  float4 xr[S_][IC];
+#pragma unroll
+  for (int t = 0; t < S_; t++)
+#pragma unroll
+    for (int c = 0; c < IC; c++) {
+      const int e = c * 1024 + threadIdx.x * 4;
+      xr[t][c] = *(const float4*)(x + (size_t)(t < S ? t : 0) * I + (e < I ? e : 0));
+    }
+  const uint8_t* wb = W + (size_t)blk * nb * GB;
+  const int nchunk = nb * GB / 16;
+  int4 wc[NCH];
+#pragma unroll
+  for (int k = 0; k < NCH; k++) {
+    const int ci = lane + 64 * k;
+    wc[k] = *(const int4*)(wb + (size_t)(ci < nchunk ? ci : 0) * 16);
+  }
+  // the block's f16 scales: one 8-byte (4-row) chunk per group
+  const uint16_t* db = d16 + (size_t)blk * nb * 4;
+  uint2 dc[DCH];
+#pragma unroll
+  for (int k = 0; k < DCH; k++) {
+    const int g = lane + 64 * k;
+    dc[k] = *(const uint2*)(db + (size_t)(g < nb ? g : 0) * 4);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. group-32 quantization of the activation rows into LDS (k_quant_g32's
+  // arithmetic), and the block's decoded scales into the wave's slice
+#pragma unroll
+  for (int t = 0; t < S_; t++)
+#pragma unroll
+    for (int c = 0; c < IC; c++) {
+      const int e = c * 1024 + threadIdx.x * 4;
+      const bool ok = e < I;
+      const float4 v = sel4(ok, xr[t][c]);
+      float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+      amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+      amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+      amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+      float s = amax / 127.f;
+      if (s < 1e-30f) s = 1e-30f;
+      const float inv = 1.f / s;
+      const int a = rne_int(v.x * inv), b = rne_int(v.y * inv), cc = rne_int(v.z * inv), d = rne_int(v.w * inv);
+      int sum = a + b + cc + d;
+      sum += __shfl_xor(sum, 1, 64);
+      sum += __shfl_xor(sum, 2, 64);
+      sum += __shfl_xor(sum, 4, 64);
+      if (ok) {
+        *(uint32_t*)(xq_s + t * I + e) = (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) |
+                                         ((uint32_t)(cc & 0xff) << 16) | ((uint32_t)(d & 0xff) << 24);
+        if ((threadIdx.x & 7) == 0) {
+          xs_s[t * nb + e / 32] = s;
+          xm_s[t * nb + e / 32] = sum;
+        }
+      }
+    }
+#pragma unroll
+  for (int k = 0; k < DCH; k++) {
+    const int g = lane + 64 * k;
+    if (g < nb) {
+      dd_s[g * 4 + 0] = f16_to_f32(dc[k].x & 0xffffu);
+      dd_s[g * 4 + 1] = f16_to_f32(dc[k].x >> 16);
+      dd_s[g * 4 + 2] = f16_to_f32(dc[k].y & 0xffffu);
+      dd_s[g * 4 + 3] = f16_to_f32(dc[k].y >> 16);
+    }
+  }
+  __syncthreads();
+
+  // 3. exact integer group sums of this lane's chunks
+#pragma unroll
+  for (int k = 0; k < NCH; k++) {
+    const int ci = lane + 64 * k;
+    const int g = Q8 ? (ci >> 3) : (ci >> 2), r = Q8 ? ((ci >> 1) & 3) : (ci & 3), h = Q8 ? (ci & 1) : 0;
+    const bool ok = ci < nchunk;
+    const int gc = ok ? g : 0;
+#pragma unroll
+    for (int t = 0; t < S_; t++) {
+      const int8_t* xg = xq_s + t * I + gc * 32;
+      int sacc;
+      if (Q8) {
+        sacc = dot16(wc[k], *(const int4*)(xg + 16 * h), 0);
+        sacc += __shfl_xor(sacc, 1, 64);  // the row's other half: lanes 2i, 2i+1 hold (g, r, h = 0/1)
+      } else {
+        sacc = dot16(r4_lo(wc[k]), *(const int4*)xg, dot16(r4_hi(wc[k]), *(const int4*)(xg + 16), 0));
+      }
+      if (ok && h == 0) sum_s[(g * 4 + r) * S_ + t] = sacc;
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // 4. lane (t*4 + r) runs row r's chain for token t over the groups in order
+  const int S4 = S / 4 * 4;
+  if (lane < 4 * S_) {
+    const int r = lane & 3, t = lane >> 2;
+    const bool tile = t < S4;  // the 4-token tile kernel's form
+    float acc = 0.f;
+    auto step = [&](int sv, float dv, float xv, int mv) {
+      if (Q8) {
+        acc = __fmaf_rn((float)sv, dv * xv, acc);
+      } else if (tile) {
+        acc = __fmaf_rn((float)sv, dv * xv, acc);
+        acc = __fmaf_rn(-dv, (8.f * (float)mv) * xv, acc);
+      } else {
+        acc = __fmaf_rn((float)(sv - 8 * mv), dv * xv, acc);
+      }
+    };
+    int g = 0;
+    for (; g + 8 <= nb; g += 8) {
+      int sv[8], mv[8];
+      float dv[8], xv[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        sv[u] = sum_s[((g + u) * 4 + r) * S_ + t];
+        dv[u] = dd_s[(g + u) * 4 + r];
+        xv[u] = xs_s[t * nb + g + u];
+        mv[u] = xm_s[t * nb + g + u];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; u++) step(sv[u], dv[u], xv[u], mv[u]);
+    }
+    for (; g < nb; g++) step(sum_s[(g * 4 + r) * S_ + t], dd_s[g * 4 + r], xs_s[t * nb + g], xm_s[t * nb + g]);
+    const int o = blk * 4 + r;
+    if (live && t < S && o < O) y[(size_t)t * O + o] = acc;
+  }
+}
+
+template <bool Q8, int S_, int IC>
+static int go_r4_gemv(const float* x, const uint8_t* W, const uint16_t* d16, float* y, int S, int I, int O,
+                      hipStream_t st) {
+  const int nb = I / 32, O4 = (O + 3) / 4;
+  const size_t lds =
+      (size_t)S_ * I + (size_t)S_ * nb * 8 + (size_t)(R4V_NT / MOTY_WAVE) * (nb * 4 * S_ + nb * 4) * 4;
+  if (lds > 64 * 1024) return MOTY_EUNSUP;
+  hipLaunchKernelGGL((k_r4_gemv<Q8, S_, IC>), dim3((unsigned)((O4 + 3) / 4)), dim3(R4V_NT), lds, st, x, W, d16, y,
+                     S, I, O);
+  LAUNCH_TRY("k_r4_gemv");
+  return MOTY_OK;
+}
+
+// instances: activation rows x 1 KiB chunks <= 16 floats4 per thread, weight
+// chunks per lane <= 16
+template <bool Q8, int S_>
+static int go_r4_gemv_ic(const float* x, const uint8_t* W, const uint16_t* d16, float* y, int S, int I, int O,
+                         hipStream_t st) {
+  const int ic = (I + 1023) / 1024;
+  if (ic <= 1) return go_r4_gemv<Q8, S_, 1>(x, W, d16, y, S, I, O, st);
+  if (ic <= 2) return go_r4_gemv<Q8, S_, 2>(x, W, d16, y, S, I, O, st);
+  if (ic <= 4) return go_r4_gemv<Q8, S_, 4>(x, W, d16, y, S, I, O, st);
+  if constexpr (!Q8 && S_ <= 2) {
+    if (ic <= 8) return go_r4_gemv<Q8, S_, 8>(x, W, d16, y, S, I, O, st);
+  }
+  return MOTY_EUNSUP;
+}
+
+template <bool Q8>
+static int launch_r4_gemv(const float* x, const uint8_t* W, const uint16_t* d16, float* y, int S, int I, int O,
+                          hipStream_t st) {
+  switch (S) {
+    case 1: return go_r4_gemv_ic<Q8, 1>(x, W, d16, y, S, I, O, st);
+    case 2: return go_r4_gemv_ic<Q8, 2>(x, W, d16, y, S, I, O, st);
+    case 3: return go_r4_gemv_ic<Q8, 3>(x, W, d16, y, S, I, O, st);
+    case 4: return go_r4_gemv_ic<Q8, 4>(x, W, d16, y, S, I, O, st);
+  }
+  return MOTY_EUNSUP;
+}
+
+// ---------------------------------------------------------------------------
+// Prefill GEMM on v_mfma_i32_32x32x32_i8: one MFMA per group (K = 32 = the
+// group), so each group's integer sum comes out separately and is folded
+// into the float chain per output in group order.  Block tile 64 tokens x 64
+// weight rows, 4 waves as 2 x 2 (32 x 32 each).  Per K block of 4 groups the
+// workgroup stages in LDS, by whole-line loads: the tokens' int8 codes, the
+// weight codes (Q4R4: 16 packed bytes per row and group, unpacked to low /
+// high nibbles for the two MFMA halves; Q8R4: 32 codes), the decoded f16
+// scales per (row, group), and per (group, token) the activation scale xs,
+// the integer offset m8 = -8*xsum for per-token-kernel tokens (else 0) and
+// the tile kernel's offset term xct = (8*xsum)*xs (0 for per-token tokens):
+//   acc = fma(float(s + m8), dd*xs, acc);  acc = fma(-dd, xct, acc)
+// reproduces both reference forms (the second FMA adds -dd*0 to a nonzero-
+// signed or +0 accumulator: exactly nothing).  Q8R4 runs the first FMA only.
+constexpr int R4M_NT = 256;
+constexpr int R4M_KG = 4;                 // groups per K block
+constexpr int R4M_AS = R4M_KG * 32 + 16;  // A row stride (bytes)
+
+template <bool Q8>
+__global__ __launch_bounds__(R4M_NT, 2) void k_r4_gemm(const int8_t* __restrict__ xq, const float* __restrict__ xs,
+                                                       const int32_t* __restrict__ xm,
+                                                       const uint8_t* __restrict__ W,
+                                                       const uint16_t* __restrict__ d16, float* __restrict__ y,
+                                                       int S, int I, int O) {
+  constexpr int GB = Q8 ? 128 : 64;
+  constexpr int RB = Q8 ? 32 : 16;          // bytes per (row, group)
+  constexpr int BS = R4M_KG * RB + 16;      // B row stride (bytes)
+  constexpr int NBC = Q8 ? 2 : 1;           // B chunks per thread
+  __shared__ __align__(16) int8_t sA[64 * R4M_AS];
+  __shared__ __align__(16) uint8_t sB[64 * BS];
+  __shared__ float sD[64 * R4M_KG];         // [row][group]
+  __shared__ __align__(16) float sX[R4M_KG * 64], sC[R4M_KG * 64];  // [group][token]
+  __shared__ __align__(16) int sM[R4M_KG * 64];
+  const int tid = threadIdx.x, lane = tid % MOTY_WAVE, wv = tid / MOTY_WAVE;
+  const int wm = wv >> 1, wn = wv & 1;
+  const int r32 = lane & 31, hk = lane >> 5;
+  const int mb = blockIdx.y * 64, nb0 = blockIdx.x * 64;
+  const int nb = I / 32, S4 = S / 4 * 4;
+  const int O4 = (O + 3) / 4;
+
+  // copy assignments
+  const int8_t* srcA[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int q = tid + i * R4M_NT;
+    int m = mb + (q >> 3);
+    m = m < S ? m : S - 1;
+    srcA[i] = xq + (int64_t)m * I + (q & 7) * 16;
+  }
+  // B: thread -> (row tid/4, group tid%4), Q8R4 two 16-byte halves
+  int orow = nb0 + (tid >> 2);
+  int ob = orow / 4;
+  ob = ob < O4 ? ob : O4 - 1;
+  const uint8_t* srcB = W + (size_t)ob * nb * GB + (size_t)(orow & 3) * RB;
+  const uint16_t* srcD = d16 + (size_t)ob * nb * 4 + (orow & 3);
+  // token scales: thread -> (group tid/64, token tid%64)
+  const int st_t = mb + (tid & 63), st_g = tid >> 6;
+  const int st_tc = st_t < S ? st_t : S - 1;
+  const bool st_tile = st_t < S4;
+
+  struct Set {
+    int4 a[2];
+    int4 b[NBC];
+    uint32_t d;
+    float x;
+    int m;
+  };
+  Set s0, s1;
+  const int glast = (nb - 1) / R4M_KG * R4M_KG;
+  auto gload = [&](int g0, Set& sv) {
+    const int gc = g0 < nb ? g0 : glast;
+    const int kb = gc * 32;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int q = tid + i * R4M_NT;
+      sv.a[i] = *(const int4*)(srcA[i] + (kb + (q & 7) * 16 < I ? kb : -(q & 7) * 16));
+    }
+    const int g = gc + (tid & 3) < nb ? gc + (tid & 3) : 0;
+#pragma unroll
+    for (int i = 0; i < NBC; i++) sv.b[i] = *(const int4*)(srcB + (size_t)g * GB + 16 * i);
+    sv.d = srcD[(size_t)g * 4];
+    const int gt = gc + st_g < nb ? gc + st_g : 0;
+    sv.x = xs[(size_t)st_tc * nb + gt];
+    sv.m = xm[(size_t)st_tc * nb + gt];
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  float accf[16];
+#pragma unroll
+  for (int r = 0; r < 16; r++) accf[r] = 0.f;
+  auto stage = [&](int g0, Set& sv) {
+    const int kb = g0 * 32;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int q = tid + i * R4M_NT;
+      *(int4*)(sA + (q >> 3) * R4M_AS + (q & 7) * 16) = sel4(kb + (q & 7) * 16 < I, sv.a[i]);
+    }
+    const bool gok = g0 + (tid & 3) < nb;
+#pragma unroll
+    for (int i = 0; i < NBC; i++) *(int4*)(sB + (tid >> 2) * BS + (tid & 3) * RB + 16 * i) = sel4(gok, sv.b[i]);
+    sD[(tid >> 2) * R4M_KG + (tid & 3)] = gok ? f16_to_f32(sv.d) : 0.f;
+    {
+      const bool ok = g0 + st_g < nb;
+      const float xv = ok ? sv.x : 0.f;
+      sX[st_g * 64 + (tid & 63)] = xv;
+      sM[st_g * 64 + (tid & 63)] = (ok && !st_tile) ? -8 * sv.m : 0;
+      sC[st_g * 64 + (tid & 63)] = (ok && st_tile) ? (8.f * (float)sv.m) * xv : 0.f;
+    }
+    __syncthreads();
+    gload(g0 + 2 * R4M_KG, sv);
+    const int ngk = (nb - g0) < R4M_KG ? (nb - g0) : R4M_KG;
+#pragma unroll
+    for (int gg = 0; gg < R4M_KG; gg++) {
+      if (gg >= ngk) break;  // wave-uniform
+      const v4i a = *(const v4i*)(sA + (wm * 32 + r32) * R4M_AS + gg * 32 + hk * 16);
+      v4i b;
+      if (Q8) {
+        b = *(const v4i*)(sB + (wn * 32 + r32) * BS + gg * RB + hk * 16);
+      } else {
+        const int4 w = *(const int4*)(sB + (wn * 32 + r32) * BS + gg * RB);
+        const int4 u = hk ? r4_hi(w) : r4_lo(w);
+        b = v4i{u.x, u.y, u.z, u.w};
+      }
+      v16i dsum = {};
+      dsum = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, dsum, 0, 0, 0);
+      const float dd = sD[(wn * 32 + r32) * R4M_KG + gg];
+      // D layout: lane l, register r -> token 8*(r/4) + 4*(l/32) + r%4, row l%32
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int tb = wm * 32 + 8 * q + 4 * hk;
+        const float4 xv = *(const float4*)(sX + gg * 64 + tb);
+        if (Q8) {
+          accf[4 * q + 0] = __fmaf_rn((float)dsum[4 * q + 0], dd * xv.x, accf[4 * q + 0]);
+          accf[4 * q + 1] = __fmaf_rn((float)dsum[4 * q + 1], dd * xv.y, accf[4 * q + 1]);
+          accf[4 * q + 2] = __fmaf_rn((float)dsum[4 * q + 2], dd * xv.z, accf[4 * q + 2]);
+          accf[4 * q + 3] = __fmaf_rn((float)dsum[4 * q + 3], dd * xv.w, accf[4 * q + 3]);
+        } else {
+          const int4 mv = *(const int4*)(sM + gg * 64 + tb);
+          const float4 cv = *(const float4*)(sC + gg * 64 + tb);
+          accf[4 * q + 0] = __fmaf_rn(-dd, cv.x, __fmaf_rn((float)(dsum[4 * q + 0] + mv.x), dd * xv.x, accf[4 * q + 0]));
+          accf[4 * q + 1] = __fmaf_rn(-dd, cv.y, __fmaf_rn((float)(dsum[4 * q + 1] + mv.y), dd * xv.y, accf[4 * q + 1]));
+          accf[4 * q + 2] = __fmaf_rn(-dd, cv.z, __fmaf_rn((float)(dsum[4 * q + 2] + mv.z), dd * xv.z, accf[4 * q + 2]));
+          accf[4 * q + 3] = __fmaf_rn(-dd, cv.w, __fmaf_rn((float)(dsum[4 * q + 3] + mv.w), dd * xv.w, accf[4 * q + 3]));
+        }
+      }
+    }
+    __syncthreads();
+  };
+  gload(0, s0);
+  gload(R4M_KG, s1);
+  for (int g0 = 0; g0 < nb; g0 += 2 * R4M_KG) {
+    stage(g0, s0);
+    stage(g0 + R4M_KG, s1);
+  }
+  // retire the clamped prefetches once before the conditional stores
+  __builtin_amdgcn_s_waitcnt(0);
+  const int col = nb0 + wn * 32 + r32;
+  if (col >= O) return;
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    const int t = mb + wm * 32 + 8 * (r >> 2) + 4 * hk + (r & 3);
+    if (t < S) y[(int64_t)t * O + col] = accf[r];
+  }
+}
+
+// y [S][O] = R4 matmul of x [S][I]; xq/xs/xm: scratch for the activation
+// codes (S*I bytes, S*(I/32) floats and ints)
+int launch_r4_matmul(bool q8, const float* x, const uint8_t* W, const uint16_t* d16, float* y, int S, int I, int O,
+                     int8_t* xq, float* xs, int32_t* xm, hipStream_t st) {
+  if (I % 32 || I <= 0) return MOTY_EUNSUP;
+  if (S <= 0 || O <= 0) return MOTY_OK;
+  if (S <= 4) {
+    const int rc = q8 ? launch_r4_gemv<true>(x, W, d16, y, S, I, O, st) : launch_r4_gemv<false>(x, W, d16, y, S, I, O, st);
+    if (rc != MOTY_EUNSUP) return rc;
+  }
+  if (!xq || !xs || !xm) return MOTY_EINVAL;  // the GEMM path needs the activation scratch
+  int rc = launch_quant_g32(x, xq, xs, xm, S, I, st);
+  if (rc) return rc;
+  dim3 grid((O + 63) / 64, (S + 63) / 64);
+  if (q8)
+    hipLaunchKernelGGL(k_r4_gemm<true>, grid, dim3(R4M_NT), 0, st, xq, xs, xm, W, d16, y, S, I, O);
+  else
+    hipLaunchKernelGGL(k_r4_gemm<false>, grid, dim3(R4M_NT), 0, st, xq, xs, xm, W, d16, y, S, I, O);
+  LAUNCH_TRY("k_r4_gemm");
+  return MOTY_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Packers (nn/quant.c:130-177): thread per (block, group, row).  The group
+// scale is the "no-clip Q4_0" rule: mx = the largest-magnitude weight (the
+// first one on ties), opp = the largest |w| of the other sign, d =
+// -sign(mx) * max(|mx|/lo, opp/hi) rounded to f16 (nearest even), codes
+// rint(w / d) via the reciprocal of the rounded scale, clipped.
+
+// float -> IEEE half, round to nearest even (nn/quant.c:111-128)
+__device__ __forceinline__ uint32_t f32_to_f16(float f) {
+  const uint32_t x = __float_as_uint(f);
+  const uint32_t sign = (x >> 16) & 0x8000u, e = (x >> 23) & 0xffu;
+  uint32_t m = x & 0x7fffffu;
+  if (e == 0xffu) return sign | 0x7c00u | (m ? 0x200u : 0u);
+  const int ne = (int)e - 127 + 15;
+  if (ne >= 31) return sign | 0x7c00u;
+  if (ne <= 0) {
+    if (ne < -10) return sign;
+    m |= 0x800000u;
+    const int sh = 14 - ne;
+    uint32_t h = m >> sh;
+    const uint32_t rem = m & ((1u << sh) - 1), half = 1u << (sh - 1);
+    if (rem > half || (rem == half && (h & 1))) h++;
+    return sign | h;
+  }
+  uint32_t h = ((uint32_t)ne << 10) | (m >> 13);
+  const uint32_t rem = m & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1))) h++;
+  return sign | h;
+}
+
+template <bool Q8>
+__global__ __launch_bounds__(256) void k_pack_r4(const float* __restrict__ w, uint8_t* __restrict__ q,
+                                                 uint16_t* __restrict__ d16, int O, int I) {
+  const int nb = I / 32, O4 = (O + 3) / 4;
+  const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (block, group, row)
+  if (id >= (int64_t)O4 * nb * 4) return;
+  const int r = (int)(id & 3);
+  const int64_t bg = id >> 2;
+  const int g = (int)(bg % nb), b = (int)(bg / nb);
+  const int row = b * 4 + r;
+  constexpr int GB = Q8 ? 128 : 64;
+  uint8_t* dst = q + (size_t)bg * GB + r * (Q8 ? 32 : 16);
+  if (row >= O) {
+#pragma unroll
+    for (int j = 0; j < (Q8 ? 32 : 16); j += 4) *(uint32_t*)(dst + j) = Q8 ? 0u : 0x88888888u;
+    d16[(size_t)bg * 4 + r] = 0;
+    return;
+  }
+  const float* wg = w + (size_t)row * I + g * 32;
+  float v[32];
+#pragma unroll
+  for (int j = 0; j < 32; j += 4) *(float4*)(v + j) = *(const float4*)(wg + j);
+  float mx = 0.f;
+#pragma unroll
+  for (int j = 0; j < 32; j++) mx = fabsf(v[j]) > fabsf(mx) ? v[j] : mx;
+  float opp = 0.f;
+#pragma unroll
+  for (int j = 0; j < 32; j++) opp = ((v[j] > 0) != (mx > 0) && fabsf(v[j]) > opp) ? fabsf(v[j]) : opp;
+  const float lo = Q8 ? 128.f : 8.f, hi = Q8 ? 127.f : 7.f;
+  const float dm = fmaxf(fabsf(mx) / lo, opp / hi);
+  const uint32_t h = f32_to_f16(mx > 0 ? -dm : dm);
+  const float dd = f16_to_f32(h), inv = dd != 0.f ? 1.f / dd : 0.f;
+  d16[(size_t)bg * 4 + r] = (uint16_t)h;
+  int c[32];
+#pragma unroll
+  for (int j = 0; j < 32; j++) {
+    int t = rne_int(v[j] * inv);
+    t = t < (Q8 ? -128 : -8) ? (Q8 ? -128 : -8) : t;
+    t = t > (Q8 ? 127 : 7) ? (Q8 ? 127 : 7) : t;
+    c[j] = t;
+  }
+  if (Q8) {
+#pragma unroll
+    for (int j = 0; j < 32; j += 4)
+      *(uint32_t*)(dst + j) = (uint32_t)(c[j] & 0xff) | ((uint32_t)(c[j + 1] & 0xff) << 8) |
+                              ((uint32_t)(c[j + 2] & 0xff) << 16) | ((uint32_t)(c[j + 3] & 0xff) << 24);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; j += 4) {
+      uint32_t p = 0;
+#pragma unroll
+      for (int u = 0; u < 4; u++)
+        p |= ((uint32_t)(c[j + u] + 8) | ((uint32_t)(c[j + u + 16] + 8) << 4)) << (8 * u);
+      *(uint32_t*)(dst + j) = p;
+    }
+  }
+}
+
+int launch_pack_r4(bool q8, const float* w, uint8_t* q, uint16_t* d16, int O, int I, hipStream_t st) {
+  if (I % 32 || I <= 0) return MOTY_EUNSUP;
+  if (O <= 0) return MOTY_OK;
+  const int64_t n = (int64_t)((O + 3) / 4) * (I / 32) * 4;
+  const unsigned nbk = (unsigned)((n + 255) / 256);
+  if (q8)
+    hipLaunchKernelGGL(k_pack_r4<true>, dim3(nbk), dim3(256), 0, st, w, q, d16, O, I);
+  else
+    hipLaunchKernelGGL(k_pack_r4<false>, dim3(nbk), dim3(256), 0, st, w, q, d16, O, I);
+  LAUNCH_TRY("k_pack_r4");
+  return MOTY_OK;
+}
+
+}  // namespace moty

@@ -86,6 +86,46 @@ def matmul_i4_grouped_s(x, q4, scale, gs=32, idot4=True, out=None):
     return y
 
 
+def r4_sizes(O, I, q8=False):
+    """Bytes of codes and number of f16 scales of an O x I R4 matrix."""
+    blocks = (O + 3) // 4 * (I // 32)
+    return blocks * (128 if q8 else 64), blocks * 4
+
+
+def pack_r4(w, q8=False):
+    """nn/quant.c:135-177 over every 4-row block of w [O, I] (f32): returns
+    (codes uint8 (Q4R4) / int8 (Q8R4) flat, f16 scales as int16 flat)."""
+    _dev(w)
+    O, I = w.shape
+    nq, nd = r4_sizes(O, I, q8)
+    q = torch.empty(nq, dtype=torch.int8 if q8 else torch.uint8, device=w.device)
+    d = torch.empty(nd, dtype=torch.int16, device=w.device)
+    fn = lib().moty_hip_pack_q8r4_dev if q8 else lib().moty_hip_pack_q4r4_dev
+    check(fn(_p(w), _p(q), _p(d), O, I, _stream()), "pack_r4")
+    return q, d
+
+
+def quant_g32(x):
+    """hw/hw_q4r4.h:36-46 over every row: (xq int8 [S, I], xs [S, I/32], xsum int32 [S, I/32])."""
+    _dev(x)
+    S, I = x.shape
+    xq = torch.empty((S, I), dtype=torch.int8, device=x.device)
+    xs = torch.empty((S, I // 32), dtype=torch.float32, device=x.device)
+    xm = torch.empty((S, I // 32), dtype=torch.int32, device=x.device)
+    check(lib().moty_hip_quant_g32_dev(_p(x), _p(xq), _p(xs), _p(xm), S, I, _stream()), "quant_g32")
+    return xq, xs, xm
+
+
+def matmul_r4(x, q, d, O, q8=False, out=None):
+    """moty_matmul_q4r4_s / moty_matmul_q8r4_s (nn/matmul.c:395-466): y [S, O]."""
+    _dev(x, q, d)
+    S, I = x.shape
+    y = out if out is not None else torch.empty((S, O), dtype=torch.float32, device=x.device)
+    fn = lib().moty_hip_matmul_q8r4_s_dev if q8 else lib().moty_hip_matmul_q4r4_s_dev
+    check(fn(_p(y), _p(x), _p(q), _p(d), S, I, O, _stream()), "matmul_r4")
+    return y
+
+
 def matmul(x, W, out=None):
     """nn/matmul.c:15-27 (f32, dot_f32 AVX512 order)."""
     _dev(x, W)
