@@ -256,6 +256,40 @@ def bench_c3(c, steps, warmup):
     return {"workload": "C3 8B-dense FFN, grouped int4 g32 (IDOT4=1), D=4096, I=12288, M=1 and M=256", **res}
 
 
+def bench_c3_r4(c, steps, warmup):
+    """The C3 8B-dense FFN shapes in the Q4R4 format (nn/matmul.c:395-431:
+    f16 group scales, 4-row blocks, group-32 int8 activations): M=1 decode
+    and M=256 prefill, three matmuls + SiLU per step."""
+    torch, ops = c.torch, c.ops
+    D, I = 4096, 12288
+    wbytes = 3 * (I * D // 2 + I * D // 32 * 2)
+    ncopy = n_copies(wbytes)
+    g = c.gen(2, 5)
+    copies = [tuple(ops.pack_r4(c.randn(sh, g, 0.02)) for sh in ((I, D), (I, D), (D, I))) for _ in range(ncopy)]
+    res = {}
+    for M in (1, 256):
+        x = c.randn((M, D), c.gen(2, 6))
+        gy = torch.empty((M, I), device="cuda:0")
+        uy = torch.empty((M, I), device="cuda:0")
+        y = torch.empty((M, D), device="cuda:0")
+
+        def step(w):
+            def f():
+                ops.matmul_r4(x, w[0][0], w[0][1], I, out=gy)
+                ops.matmul_r4(x, w[1][0], w[1][1], I, out=uy)
+                ops.silu_mul(gy, uy)
+                ops.matmul_r4(gy, w[2][0], w[2][1], D, out=y)
+            return f
+        t, n = c.time_steps([step(w) for w in copies], max(8, steps // (8 if M == 1 else 64)), 8)
+        ops_int = 2 * M * 3 * I * D
+        algo = wbytes + M * (D + 2 * I + I + D) * 4
+        res["M%d" % M] = {"ms_per_step": t * 1e3, "steps": n,
+                          "hbm": roofline("hbm", algo / t / 1e9, HBM_PEAK_GBS, "GB/s"),
+                          "mfma": roofline("mfma", ops_int / t / 1e12, INT8_PEAK_TOPS, "TOP/s")}
+    return {"workload": "C3 shapes in Q4R4 (f16 group-32 scales, 4-row blocks), D=4096, I=12288, M=1 and M=256",
+            **res}
+
+
 def pmc_probe(c):
     """For the rocprofv3 --pmc runs behind roofline.traffic: the C1 gate+up
     GEMV on 8 distinct weight copies (3 rounds), then a plain 64 MiB
@@ -378,6 +412,8 @@ def main():
         extra.append(bench_c2(c, args.steps, args.warmup))
         log("C3")
         extra.append(bench_c3(c, args.steps, args.warmup))
+        log("C3 in Q4R4")
+        extra.append(bench_c3_r4(c, args.steps, args.warmup))
         log("C5")
         E5 = 128
         bias = torch.zeros(E5, device="cuda:0")

@@ -153,10 +153,10 @@ int moty_hip_gate_up_silu_q8_dev(float *h, const float *x, int S, const int8_t *
  * activations): h [I] = silu(x.gate^T) * (x.up^T), one token, D % 64 == 0. */
 int moty_hip_gate_up_silu_i4g_dev(float *h, const float *x, const uint8_t *gate, const float *gs,
                                   const uint8_t *up, const float *us, int D, int I, void *stream);
-/* moty_matmul_q4r4_s / moty_matmul_q8r4_s on device pointers: S <= 4 runs
- * the decode GEMV with fused activation quantization, larger S quantizes
- * then runs the MFMA GEMM (tokens below 4*floor(S/4) in the reference's
- * 4-token tile form, the rest in its per-token form). */
+/* moty_matmul_q4r4_s / moty_matmul_q8r4_s on device pointers: S <= 3 runs
+ * the decode GEMV with fused activation quantization (the reference's
+ * per-token form), larger S quantizes then runs the MFMA GEMM (tokens below
+ * 4*floor(S/4) in the reference's 4-token tile form, the rest per token). */
 int moty_hip_matmul_q4r4_s_dev(float *y, const float *x, const uint8_t *q4, const uint16_t *s16, int S, int I, int O,
                                void *stream);
 int moty_hip_matmul_q8r4_s_dev(float *y, const float *x, const int8_t *q8, const uint16_t *s16, int S, int I, int O,

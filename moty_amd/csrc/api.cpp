@@ -444,7 +444,7 @@ static int r4_dev(bool q8, const char* what, float* y, const float* x, const uin
   int8_t* xq = nullptr;
   float* xs = nullptr;
   int32_t* xm = nullptr;
-  {  // activation scratch for the GEMM path (also taken by S <= 4 when the
+  {  // activation scratch for the GEMM path (also taken by S <= 3 when the
      // decode GEMV does not serve the shape)
     const size_t bq = al256((size_t)S * I), bs = al256((size_t)S * (I / 32) * 4);
     if ((rc = arena_get(d->scratch, bq + 2 * bs, &sp))) return rc;

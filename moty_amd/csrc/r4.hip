@@ -73,47 +73,47 @@ __device__ __forceinline__ int4 r4_hi(int4 w) {
 }
 
 // ---------------------------------------------------------------------------
-// Decode GEMV, S_ <= 4 tokens, I <= 1024*IC.  Workgroup = 4 waves; a wave
-// owns one 4-row block.  Order of the loads: the activation rows first (4
-// floats per thread per 1 KiB), then every 16-byte chunk of the wave's block
-// (lane l takes chunks l, l+64, ...: each load instruction reads 1 KiB of
-// the contiguous block) and its f16 scales -- all issued before any is
-// consumed.  The workgroup quantizes the activation rows into LDS from
-// registers (every workgroup derives the same codes); each lane forms the
-// exact integer group sums of its chunks (Q8R4: half a row per chunk, the
-// halves joined across the lane pair) and parks them in the wave's LDS
-// slice; one lane per (row, token) runs the reference's float chain over the
-// groups in order.
-constexpr int R4V_NT = 256;
-
-template <bool Q8, int S_, int IC>
-__global__ __launch_bounds__(R4V_NT) void k_r4_gemv(const float* __restrict__ x, const uint8_t* __restrict__ W,
-                                                    const uint16_t* __restrict__ d16, float* __restrict__ y, int S,
-                                                    int I, int O) {
+// Decode GEMV, S_ <= 3 tokens (all in the per-token kernel's form), I <=
+// 1024*IC.  Workgroup = NT/64 waves; a wave owns one 4-row block.  Order of
+// the loads: the activation rows first, then every 16-byte chunk of the
+// wave's block (lane l takes chunks l, l+64, ...: each load instruction
+// reads 1 KiB of the contiguous block) and one 8-byte scale chunk (the 4
+// rows' f16 scales) per group -- all issued before any is consumed.  The
+// workgroup quantizes the activation rows into LDS from registers (every
+// workgroup derives the same codes).  Each lane forms the exact integer
+// group sums of its chunks (Q8R4: half a row per chunk, the halves joined
+// across the lane pair), fetches its group's scale from the lane that loaded
+// it, and parks the two operands of the chain step, (s - 8*xsum, dd*xs), in
+// the wave's LDS slice ([row][token][group]); one lane per (row, token) then
+// runs acc = fma(a, b, acc) over the groups in order.
+template <bool Q8, int S_, int IC, int NT>
+__global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, const uint8_t* __restrict__ W,
+                                                const uint16_t* __restrict__ d16, float* __restrict__ y, int S,
+                                                int I, int O) {
   constexpr int GB = Q8 ? 128 : 64;        // bytes per (block, group)
   constexpr int NCH = IC * (Q8 ? 4 : 2);   // weight chunks per lane
   constexpr int DCH = (IC + 1) / 2;        // scale chunks (groups) per lane
-  constexpr int WAVES = R4V_NT / MOTY_WAVE;
+  constexpr int WAVES = NT / MOTY_WAVE;
+  constexpr int XC = IC * 1024 / (NT * 4);  // activation float4 per thread per row
   extern __shared__ __align__(16) int8_t lds[];
   const int nb = I / 32, O4 = (O + 3) / 4;
   const int lane = threadIdx.x % MOTY_WAVE, wv = threadIdx.x / MOTY_WAVE;
-  // LDS: xq [S_][I] | xs [S_][nb] | xm [S_][nb] | per wave: sums [nb][4][S_], dd [nb][4]
+  // LDS: xq [S_][I] | xs [S_][nb] | xm [S_][nb] | per wave: operands [4][S_][nb] float2
   int8_t* xq_s = lds;
   float* xs_s = (float*)(lds + S_ * I);
   int* xm_s = (int*)(xs_s + S_ * nb);
-  int* sum_s = (int*)(xm_s + S_ * nb) + (size_t)wv * (nb * 4 * S_ + nb * 4);
-  float* dd_s = (float*)(sum_s + nb * 4 * S_);
+  float2* op_s = (float2*)(xm_s + S_ * nb) + (size_t)wv * (4 * S_ * nb);
   int blk = blockIdx.x * WAVES + wv;
   const bool live = blk < O4;
   blk = live ? blk : O4 - 1;
 
   // 1. activation rows, then every weight and scale chunk of the block
-  float4 xr[S_][IC];
+  float4 xr[S_][XC];
 #pragma unroll
   for (int t = 0; t < S_; t++)
 #pragma unroll
-    for (int c = 0; c < IC; c++) {
-      const int e = c * 1024 + threadIdx.x * 4;
+    for (int c = 0; c < XC; c++) {
+      const int e = (c * NT + threadIdx.x) * 4;
       xr[t][c] = *(const float4*)(x + (size_t)(t < S ? t : 0) * I + (e < I ? e : 0));
     }
   const uint8_t* wb = W + (size_t)blk * nb * GB;
@@ -124,7 +124,7 @@ __global__ __launch_bounds__(R4V_NT) void k_r4_gemv(const float* __restrict__ x,
     const int ci = lane + 64 * k;
     wc[k] = *(const int4*)(wb + (size_t)(ci < nchunk ? ci : 0) * 16);
   }
-  // the block's f16 scales: one 8-byte (4-row) chunk per group
+  // lane l, chunk k: the 4 rows' f16 scales of group l + 64k
   const uint16_t* db = d16 + (size_t)blk * nb * 4;
   uint2 dc[DCH];
 #pragma unroll
@@ -134,13 +134,12 @@ __global__ __launch_bounds__(R4V_NT) void k_r4_gemv(const float* __restrict__ x,
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  // 2. group-32 quantization of the activation rows into LDS (k_quant_g32's
-  // arithmetic), and the block's decoded scales into the wave's slice
+  // 2. group-32 quantization of the activation rows into LDS (k_quant_g32's arithmetic)
 #pragma unroll
   for (int t = 0; t < S_; t++)
 #pragma unroll
-    for (int c = 0; c < IC; c++) {
-      const int e = c * 1024 + threadIdx.x * 4;
+    for (int c = 0; c < XC; c++) {
+      const int e = (c * NT + threadIdx.x) * 4;
       const bool ok = e < I;
       const float4 v = sel4(ok, xr[t][c]);
       float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
@@ -164,25 +163,20 @@ __global__ __launch_bounds__(R4V_NT) void k_r4_gemv(const float* __restrict__ x,
         }
       }
     }
-#pragma unroll
-  for (int k = 0; k < DCH; k++) {
-    const int g = lane + 64 * k;
-    if (g < nb) {
-      dd_s[g * 4 + 0] = f16_to_f32(dc[k].x & 0xffffu);
-      dd_s[g * 4 + 1] = f16_to_f32(dc[k].x >> 16);
-      dd_s[g * 4 + 2] = f16_to_f32(dc[k].y & 0xffffu);
-      dd_s[g * 4 + 3] = f16_to_f32(dc[k].y >> 16);
-    }
-  }
   __syncthreads();
 
-  // 3. exact integer group sums of this lane's chunks
+  // 3. per chunk: the exact integer group sum, the group's scale (from the
+  // lane that loaded it: group g = lane/4 + 16k sits in lane g % 64, chunk
+  // k/4 -- Q8R4: lane/8 + 8k, chunk k/8), the chain step's operands
 #pragma unroll
   for (int k = 0; k < NCH; k++) {
     const int ci = lane + 64 * k;
     const int g = Q8 ? (ci >> 3) : (ci >> 2), r = Q8 ? ((ci >> 1) & 3) : (ci & 3), h = Q8 ? (ci & 1) : 0;
     const bool ok = ci < nchunk;
     const int gc = ok ? g : 0;
+    const uint2 dsrc = dc[Q8 ? k / 8 : k / 4];
+    const uint32_t dx = __shfl(dsrc.x, g & 63, 64), dy = __shfl(dsrc.y, g & 63, 64);
+    const float dd = f16_to_f32(((r < 2 ? dx : dy) >> (16 * (r & 1))) & 0xffffu);
 #pragma unroll
     for (int t = 0; t < S_; t++) {
       const int8_t* xg = xq_s + t * I + gc * 32;
@@ -192,8 +186,9 @@ __global__ __launch_bounds__(R4V_NT) void k_r4_gemv(const float* __restrict__ x,
         sacc += __shfl_xor(sacc, 1, 64);  // the row's other half: lanes 2i, 2i+1 hold (g, r, h = 0/1)
       } else {
         sacc = dot16(r4_lo(wc[k]), *(const int4*)xg, dot16(r4_hi(wc[k]), *(const int4*)(xg + 16), 0));
+        sacc -= 8 * xm_s[t * nb + gc];
       }
-      if (ok && h == 0) sum_s[(g * 4 + r) * S_ + t] = sacc;
+      if (ok && h == 0) op_s[(r * S_ + t) * nb + g] = float2{(float)sacc, dd * xs_s[t * nb + gc]};
     }
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -201,65 +196,65 @@ __global__ __launch_bounds__(R4V_NT) void k_r4_gemv(const float* __restrict__ x,
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
   // 4. lane (t*4 + r) runs row r's chain for token t over the groups in order
-  const int S4 = S / 4 * 4;
   if (lane < 4 * S_) {
     const int r = lane & 3, t = lane >> 2;
-    const bool tile = t < S4;  // the 4-token tile kernel's form
+    const float2* op = op_s + (r * S_ + t) * nb;
     float acc = 0.f;
-    auto step = [&](int sv, float dv, float xv, int mv) {
-      if (Q8) {
-        acc = __fmaf_rn((float)sv, dv * xv, acc);
-      } else if (tile) {
-        acc = __fmaf_rn((float)sv, dv * xv, acc);
-        acc = __fmaf_rn(-dv, (8.f * (float)mv) * xv, acc);
-      } else {
-        acc = __fmaf_rn((float)(sv - 8 * mv), dv * xv, acc);
-      }
-    };
     int g = 0;
     for (; g + 8 <= nb; g += 8) {
-      int sv[8], mv[8];
-      float dv[8], xv[8];
+      float2 v[8];
 #pragma unroll
-      for (int u = 0; u < 8; u++) {
-        sv[u] = sum_s[((g + u) * 4 + r) * S_ + t];
-        dv[u] = dd_s[(g + u) * 4 + r];
-        xv[u] = xs_s[t * nb + g + u];
-        mv[u] = xm_s[t * nb + g + u];
-      }
+      for (int u = 0; u < 8; u++) v[u] = op[g + u];
 #pragma unroll
-      for (int u = 0; u < 8; u++) step(sv[u], dv[u], xv[u], mv[u]);
+      for (int u = 0; u < 8; u++) acc = __fmaf_rn(v[u].x, v[u].y, acc);
     }
-    for (; g < nb; g++) step(sum_s[(g * 4 + r) * S_ + t], dd_s[g * 4 + r], xs_s[t * nb + g], xm_s[t * nb + g]);
+    for (; g < nb; g++) acc = __fmaf_rn(op[g].x, op[g].y, acc);
     const int o = blk * 4 + r;
     if (live && t < S && o < O) y[(size_t)t * O + o] = acc;
   }
 }
 
-template <bool Q8, int S_, int IC>
+template <bool Q8, int S_, int IC, int NT>
+static size_t r4_gemv_lds(int I) {
+  const int nb = I / 32;
+  return (size_t)S_ * I + (size_t)S_ * nb * 8 + (size_t)(NT / MOTY_WAVE) * 4 * S_ * nb * 8;
+}
+
+template <bool Q8, int S_, int IC, int NT>
 static int go_r4_gemv(const float* x, const uint8_t* W, const uint16_t* d16, float* y, int S, int I, int O,
                       hipStream_t st) {
-  const int nb = I / 32, O4 = (O + 3) / 4;
-  const size_t lds =
-      (size_t)S_ * I + (size_t)S_ * nb * 8 + (size_t)(R4V_NT / MOTY_WAVE) * (nb * 4 * S_ + nb * 4) * 4;
-  if (lds > 64 * 1024) return MOTY_EUNSUP;
-  hipLaunchKernelGGL((k_r4_gemv<Q8, S_, IC>), dim3((unsigned)((O4 + 3) / 4)), dim3(R4V_NT), lds, st, x, W, d16, y,
-                     S, I, O);
+  const int O4 = (O + 3) / 4, waves = NT / MOTY_WAVE;
+  const size_t lds = r4_gemv_lds<Q8, S_, IC, NT>(I);
+  hipLaunchKernelGGL((k_r4_gemv<Q8, S_, IC, NT>), dim3((unsigned)((O4 + waves - 1) / waves)), dim3(NT), lds, st, x,
+                     W, d16, y, S, I, O);
   LAUNCH_TRY("k_r4_gemv");
   return MOTY_OK;
 }
 
-// instances: activation rows x 1 KiB chunks <= 16 floats4 per thread, weight
-// chunks per lane <= 16
+// 4-wave workgroups when the LDS fits, else 2-wave ones
+template <bool Q8, int S_, int IC>
+static int go_r4_gemv_nt(const float* x, const uint8_t* W, const uint16_t* d16, float* y, int S, int I, int O,
+                         hipStream_t st) {
+  if (r4_gemv_lds<Q8, S_, IC, 256>(I) <= 64 * 1024) return go_r4_gemv<Q8, S_, IC, 256>(x, W, d16, y, S, I, O, st);
+  if (r4_gemv_lds<Q8, S_, IC, 128>(I) <= 64 * 1024) return go_r4_gemv<Q8, S_, IC, 128>(x, W, d16, y, S, I, O, st);
+  return MOTY_EUNSUP;
+}
+
+// instances: activation float4 per thread and weight chunks per lane stay
+// within a register budget (S_ * IC <= 16, Q8R4 IC <= 8)
 template <bool Q8, int S_>
 static int go_r4_gemv_ic(const float* x, const uint8_t* W, const uint16_t* d16, float* y, int S, int I, int O,
                          hipStream_t st) {
   const int ic = (I + 1023) / 1024;
-  if (ic <= 1) return go_r4_gemv<Q8, S_, 1>(x, W, d16, y, S, I, O, st);
-  if (ic <= 2) return go_r4_gemv<Q8, S_, 2>(x, W, d16, y, S, I, O, st);
-  if (ic <= 4) return go_r4_gemv<Q8, S_, 4>(x, W, d16, y, S, I, O, st);
-  if constexpr (!Q8 && S_ <= 2) {
-    if (ic <= 8) return go_r4_gemv<Q8, S_, 8>(x, W, d16, y, S, I, O, st);
+  if (ic <= 1) return go_r4_gemv_nt<Q8, S_, 1>(x, W, d16, y, S, I, O, st);
+  if (ic <= 2) return go_r4_gemv_nt<Q8, S_, 2>(x, W, d16, y, S, I, O, st);
+  if (ic <= 4) return go_r4_gemv_nt<Q8, S_, 4>(x, W, d16, y, S, I, O, st);
+  if constexpr (S_ <= 2) {
+    if (ic <= 8) return go_r4_gemv_nt<Q8, S_, 8>(x, W, d16, y, S, I, O, st);
+  }
+  if constexpr (!Q8 && S_ == 1) {
+    if (ic <= 12) return go_r4_gemv_nt<Q8, S_, 12>(x, W, d16, y, S, I, O, st);
+    if (ic <= 16) return go_r4_gemv_nt<Q8, S_, 16>(x, W, d16, y, S, I, O, st);
   }
   return MOTY_EUNSUP;
 }
@@ -271,9 +266,8 @@ static int launch_r4_gemv(const float* x, const uint8_t* W, const uint16_t* d16,
     case 1: return go_r4_gemv_ic<Q8, 1>(x, W, d16, y, S, I, O, st);
     case 2: return go_r4_gemv_ic<Q8, 2>(x, W, d16, y, S, I, O, st);
     case 3: return go_r4_gemv_ic<Q8, 3>(x, W, d16, y, S, I, O, st);
-    case 4: return go_r4_gemv_ic<Q8, 4>(x, W, d16, y, S, I, O, st);
   }
-  return MOTY_EUNSUP;
+  return MOTY_EUNSUP;  // S = 4 is the reference's 4-token tile: the GEMM path
 }
 
 // ---------------------------------------------------------------------------
@@ -446,7 +440,7 @@ int launch_r4_matmul(bool q8, const float* x, const uint8_t* W, const uint16_t* 
                      int8_t* xq, float* xs, int32_t* xm, hipStream_t st) {
   if (I % 32 || I <= 0) return MOTY_EUNSUP;
   if (S <= 0 || O <= 0) return MOTY_OK;
-  if (S <= 4) {
+  if (S <= 3) {
     const int rc = q8 ? launch_r4_gemv<true>(x, W, d16, y, S, I, O, st) : launch_r4_gemv<false>(x, W, d16, y, S, I, O, st);
     if (rc != MOTY_EUNSUP) return rc;
   }
