@@ -258,36 +258,29 @@ def bench_c3(c, steps, warmup):
 
 def bench_c3_r4(c, steps, warmup):
     """The C3 8B-dense FFN shapes in the Q4R4 format (nn/matmul.c:395-431:
-    f16 group scales, 4-row blocks, group-32 int8 activations): M=1 decode
-    and M=256 prefill, three matmuls + SiLU per step."""
+    f16 group scales, 4-row blocks, group-32 int8 activations), gate and up
+    row-fused as moty_mat_fuse_rows stores them (nn/ffn.c:26-41): M=1
+    decode (fused gate/up + SiLU GEMV, down GEMV) and M=256 prefill."""
     torch, ops = c.torch, c.ops
     D, I = 4096, 12288
     wbytes = 3 * (I * D // 2 + I * D // 32 * 2)
     ncopy = n_copies(wbytes)
     g = c.gen(2, 5)
-    copies = [tuple(ops.pack_r4(c.randn(sh, g, 0.02)) for sh in ((I, D), (I, D), (D, I))) for _ in range(ncopy)]
+    copies = [ops.pack_r4(c.randn((2 * I, D), g, 0.02)) + ops.pack_r4(c.randn((D, I), g, 0.02))
+              for _ in range(ncopy)]
     res = {}
     for M in (1, 256):
         x = c.randn((M, D), c.gen(2, 6))
-        gy = torch.empty((M, I), device="cuda:0")
-        uy = torch.empty((M, I), device="cuda:0")
         y = torch.empty((M, D), device="cuda:0")
-
-        def step(w):
-            def f():
-                ops.matmul_r4(x, w[0][0], w[0][1], I, out=gy)
-                ops.matmul_r4(x, w[1][0], w[1][1], I, out=uy)
-                ops.silu_mul(gy, uy)
-                ops.matmul_r4(gy, w[2][0], w[2][1], D, out=y)
-            return f
-        t, n = c.time_steps([step(w) for w in copies], max(8, steps // (8 if M == 1 else 64)), 8)
+        t, n = c.time_steps([lambda w=w: ops.dense_ffn_r4(x, w[0], w[1], w[2], w[3], I, out=y) for w in copies],
+                            max(8, steps // (8 if M == 1 else 64)), 8)
         ops_int = 2 * M * 3 * I * D
-        algo = wbytes + M * (D + 2 * I + I + D) * 4
+        algo = wbytes + M * (D + D) * 4
         res["M%d" % M] = {"ms_per_step": t * 1e3, "steps": n,
                           "hbm": roofline("hbm", algo / t / 1e9, HBM_PEAK_GBS, "GB/s"),
                           "mfma": roofline("mfma", ops_int / t / 1e12, INT8_PEAK_TOPS, "TOP/s")}
-    return {"workload": "C3 shapes in Q4R4 (f16 group-32 scales, 4-row blocks), D=4096, I=12288, M=1 and M=256",
-            **res}
+    return {"workload": "C3 shapes in Q4R4 (f16 group-32 scales, 4-row blocks, gate/up row-fused), D=4096, "
+                        "I=12288, M=1 and M=256", **res}
 
 
 def pmc_probe(c):

@@ -161,6 +161,20 @@ int moty_hip_matmul_q4r4_s_dev(float *y, const float *x, const uint8_t *q4, cons
                                void *stream);
 int moty_hip_matmul_q8r4_s_dev(float *y, const float *x, const int8_t *q8, const uint16_t *s16, int S, int I, int O,
                                void *stream);
+/* Decode gate/up + SiLU over a row-fused R4 gate_up matrix (moty_mat_fuse_rows,
+ * nn/mat.c:32-68: the I gate rows then the I up rows, I % 4 == 0), the
+ * gate_up + silu_rows step of nn/ffn.c:28-37 for one token:
+ * h [I] = silu(x.gate^T) * (x.up^T). */
+int moty_hip_gate_up_silu_q4r4_dev(float *h, const float *x, const uint8_t *gate_up, const uint16_t *s16, int D,
+                                   int I, void *stream);
+int moty_hip_gate_up_silu_q8r4_dev(float *h, const float *x, const int8_t *gate_up, const uint16_t *s16, int D,
+                                   int I, void *stream);
+/* moty_nn_dense_ffn (nn/ffn.c:26-41) with a row-fused R4 gate_up [2I][D]
+ * and down [D][I]: x [S][D] -> out [S][D].  D, I multiples of 32. */
+int moty_hip_dense_ffn_q4r4_dev(float *out, const float *x, int S, const uint8_t *gate_up, const uint16_t *gus16,
+                                const uint8_t *down, const uint16_t *ds16, int D, int I, void *stream);
+int moty_hip_dense_ffn_q8r4_dev(float *out, const float *x, int S, const int8_t *gate_up, const uint16_t *gus16,
+                                const int8_t *down, const uint16_t *ds16, int D, int I, void *stream);
 /* moty_hw_quant_g32 (hw/hw_q4r4.h:36-46) over S rows: xq [S][I], xs and
  * xsum [S][I/32] */
 int moty_hip_quant_g32_dev(const float *x, int8_t *xq, float *xs, int32_t *xsum, int S, int I, void *stream);

@@ -41,6 +41,10 @@ SIGNATURES = {
     "moty_hip_matmul_q4r4_s_dev": (I32, [P, P, P, P, I32, I32, I32, P]),
     "moty_hip_matmul_q8r4_s_dev": (I32, [P, P, P, P, I32, I32, I32, P]),
     "moty_hip_quant_g32_dev": (I32, [P, P, P, P, I32, I32, P]),
+    "moty_hip_gate_up_silu_q4r4_dev": (I32, [P, P, P, P, I32, I32, P]),
+    "moty_hip_gate_up_silu_q8r4_dev": (I32, [P, P, P, P, I32, I32, P]),
+    "moty_hip_dense_ffn_q4r4_dev": (I32, [P, P, I32, P, P, P, P, I32, I32, P]),
+    "moty_hip_dense_ffn_q8r4_dev": (I32, [P, P, I32, P, P, P, P, I32, I32, P]),
     "moty_hip_pack_q4r4_dev": (I32, [P, P, P, I32, I32, P]),
     "moty_hip_pack_q8r4_dev": (I32, [P, P, P, I32, I32, P]),
     "moty_hip_matmul": (I32, [P, P, P, I32, I32, I32]),

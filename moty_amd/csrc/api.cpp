@@ -492,6 +492,69 @@ int moty_hip_matmul_q8r4_s(float* y, const float* x, const int8_t* q8, const uin
   return r4_host(true, "matmul_q8r4_s", y, x, q8, s16, S, I, O);
 }
 
+static int r4_gate_up(bool q8, const char* what, float* h, const float* x, const uint8_t* gu, const uint16_t* s16,
+                      int D, int I, void* stream) {
+  CUR(d);
+  if (D <= 0 || I <= 0 || !h || !x || !gu || !s16) return set_error("%s: bad arguments", what), MOTY_EINVAL;
+  if (D % 32 || I % 4) return set_error("%s: D=%d (multiple of 32), I=%d (multiple of 4)", what, D, I), MOTY_EINVAL;
+  const int rc = launch_r4_gate_up_silu(q8, x, gu, s16, h, D, I, STREAM(stream));
+  if (rc == MOTY_EUNSUP) set_error("%s: D=%d unsupported", what, D);
+  return rc;
+}
+
+int moty_hip_gate_up_silu_q4r4_dev(float* h, const float* x, const uint8_t* gate_up, const uint16_t* s16, int D,
+                                   int I, void* stream) {
+  return r4_gate_up(false, "gate_up_silu_q4r4", h, x, gate_up, s16, D, I, stream);
+}
+
+int moty_hip_gate_up_silu_q8r4_dev(float* h, const float* x, const int8_t* gate_up, const uint16_t* s16, int D,
+                                   int I, void* stream) {
+  return r4_gate_up(true, "gate_up_silu_q8r4", h, x, (const uint8_t*)gate_up, s16, D, I, stream);
+}
+
+// moty_nn_dense_ffn with a row-fused R4 gate_up (nn/ffn.c:26-41)
+static int r4_ffn(bool q8, const char* what, float* out, const float* x, int S, const uint8_t* gu,
+                  const uint16_t* gs16, const uint8_t* dn, const uint16_t* ds16, int D, int I, void* stream) {
+  CUR(d);
+  if (S < 0 || D <= 0 || I <= 0 || !out || !x || !gu || !gs16 || !dn || !ds16)
+    return set_error("%s: bad arguments", what), MOTY_EINVAL;
+  if (D % 32 || I % 32) return set_error("%s: D=%d, I=%d must be multiples of 32", what, D, I), MOTY_EINVAL;
+  if (S == 0) return MOTY_OK;
+  hipStream_t st = STREAM(stream);
+  // scratch: h [S][I] | gu [S][2I] | activation codes for the GEMMs
+  const int W = D > I ? D : I;
+  const size_t bh = al256((size_t)S * I * 4), bgu = al256((size_t)S * 2 * I * 4);
+  const size_t bq = al256((size_t)S * W), bs = al256((size_t)S * (W / 32) * 4);
+  void* sp;
+  int rc = arena_get(d->scratch, bh + bgu + bq + 2 * bs, &sp);
+  if (rc) return rc;
+  float* h = (float*)sp;
+  float* g2 = (float*)((char*)sp + bh);
+  int8_t* xq = (int8_t*)((char*)sp + bh + bgu);
+  float* xs = (float*)((char*)sp + bh + bgu + bq);
+  int32_t* xm = (int32_t*)((char*)sp + bh + bgu + bq + bs);
+  rc = S == 1 ? launch_r4_gate_up_silu(q8, x, gu, gs16, h, D, I, st) : MOTY_EUNSUP;
+  if (rc == MOTY_EUNSUP) {
+    if ((rc = launch_r4_matmul(q8, x, gu, gs16, g2, S, D, 2 * I, xq, xs, xm, st))) return rc;
+    rc = launch_silu_rows(h, g2, S, I, st);
+  }
+  if (rc) return rc;
+  rc = launch_r4_matmul(q8, h, dn, ds16, out, S, I, D, xq, xs, xm, st);
+  if (rc == MOTY_EUNSUP) set_error("%s: shape S=%d D=%d I=%d unsupported", what, S, D, I);
+  return rc;
+}
+
+int moty_hip_dense_ffn_q4r4_dev(float* out, const float* x, int S, const uint8_t* gate_up, const uint16_t* gus16,
+                                const uint8_t* down, const uint16_t* ds16, int D, int I, void* stream) {
+  return r4_ffn(false, "dense_ffn_q4r4", out, x, S, gate_up, gus16, down, ds16, D, I, stream);
+}
+
+int moty_hip_dense_ffn_q8r4_dev(float* out, const float* x, int S, const int8_t* gate_up, const uint16_t* gus16,
+                                const int8_t* down, const uint16_t* ds16, int D, int I, void* stream) {
+  return r4_ffn(true, "dense_ffn_q8r4", out, x, S, (const uint8_t*)gate_up, gus16, (const uint8_t*)down, ds16, D, I,
+                stream);
+}
+
 int moty_hip_quant_g32_dev(const float* x, int8_t* xq, float* xs, int32_t* xsum, int S, int I, void* stream) {
   CUR(d);
   if (S < 0 || I <= 0 || !x || !xq || !xs || !xsum) return set_error("quant_g32: bad arguments"), MOTY_EINVAL;

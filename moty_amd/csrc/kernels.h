@@ -36,10 +36,13 @@ int launch_i4g_f32(const float* x, const uint8_t* q4, const float* scl, float* y
 int launch_quant_g32(const float* x, int8_t* xq, float* xs, int32_t* xm, int S, int I, hipStream_t st);
 int launch_r4_matmul(bool q8, const float* x, const uint8_t* W, const uint16_t* d16, float* y, int S, int I, int O,
                      int8_t* xq, float* xs, int32_t* xm, hipStream_t st);
+int launch_r4_gate_up_silu(bool q8, const float* x, const uint8_t* W, const uint16_t* d16, float* h, int D, int I,
+                           hipStream_t st);
 int launch_pack_r4(bool q8, const float* w, uint8_t* q, uint16_t* d16, int O, int I, hipStream_t st);
 
 int launch_matmul_f32(const float* x, const float* W, float* y, int S, int I, int O, hipStream_t st);
 int launch_silu_mul(float* g, const float* u, int64_t n, hipStream_t st);
+int launch_silu_rows(float* h, const float* gu, int S, int I, hipStream_t st);
 int launch_expf(const float* x, float* y, int64_t n, hipStream_t st);
 int launch_softmax_rows(float* x, int S, int n, hipStream_t st);
 

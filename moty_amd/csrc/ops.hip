@@ -26,6 +26,15 @@ __global__ void k_silu_mul(float* __restrict__ g, const float* __restrict__ u, i
   if (i < n) g[i] = ref_silu_mul(g[i], u[i]);
 }
 
+// silu_rows over a row-fused gate_up output (nn/ffn.c:8-24): h [S][I] =
+// silu(gu[s][i]) * gu[s][I + i]
+__global__ void k_silu_rows(float* __restrict__ h, const float* __restrict__ gu, int S, int I) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)S * I) return;
+  const int64_t s = i / I, c = i % I;
+  h[i] = ref_silu_mul(gu[s * 2 * I + c], gu[s * 2 * I + I + c]);
+}
+
 __global__ void k_expf(const float* __restrict__ x, float* __restrict__ y, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) y[i] = ref_expf(x[i]);
@@ -69,6 +78,14 @@ int launch_matmul_f32(const float* x, const float* W, float* y, int S, int I, in
   const int64_t nb = (n + MF_NT / 32 - 1) / (MF_NT / 32);
   hipLaunchKernelGGL(k_matmul_f32, dim3((unsigned)nb), dim3(MF_NT), 0, st, x, W, y, S, I, O);
   LAUNCH_TRY("k_matmul_f32");
+  return MOTY_OK;
+}
+
+int launch_silu_rows(float* h, const float* gu, int S, int I, hipStream_t st) {
+  const int64_t n = (int64_t)S * I;
+  if (n <= 0) return MOTY_OK;
+  hipLaunchKernelGGL(k_silu_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, h, gu, S, I);
+  LAUNCH_TRY("k_silu_rows");
   return MOTY_OK;
 }
 

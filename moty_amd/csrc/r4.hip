@@ -86,10 +86,12 @@ __device__ __forceinline__ int4 r4_hi(int4 w) {
 // it, and parks the two operands of the chain step, (s - 8*xsum, dd*xs), in
 // the wave's LDS slice ([row][token][group]); one lane per (row, token) then
 // runs acc = fma(a, b, acc) over the groups in order.
-template <bool Q8, int S_, int IC, int NT>
+template <bool Q8, int S_, int IC, int NT, bool PAIR = false>
 __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, const uint8_t* __restrict__ W,
                                                 const uint16_t* __restrict__ d16, float* __restrict__ y, int S,
                                                 int I, int O) {
+  static_assert(!PAIR || S_ == 1, "the fused gate/up form serves one token");
+  constexpr int NM = PAIR ? 2 : 1;  // matrices: gate (and up)
   constexpr int GB = Q8 ? 128 : 64;        // bytes per (block, group)
   constexpr int NCH = IC * (Q8 ? 4 : 2);   // weight chunks per lane
   constexpr int DCH = (IC + 1) / 2;        // scale chunks (groups) per lane
@@ -102,7 +104,7 @@ __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, con
   int8_t* xq_s = lds;
   float* xs_s = (float*)(lds + S_ * I);
   int* xm_s = (int*)(xs_s + S_ * nb);
-  float2* op_s = (float2*)(xm_s + S_ * nb) + (size_t)wv * (4 * S_ * nb);
+  float2* op_s = (float2*)(xm_s + S_ * nb) + (size_t)wv * (4 * NM * S_ * nb);
   int blk = blockIdx.x * WAVES + wv;
   const bool live = blk < O4;
   blk = live ? blk : O4 - 1;
@@ -116,21 +118,29 @@ __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, con
       const int e = (c * NT + threadIdx.x) * 4;
       xr[t][c] = *(const float4*)(x + (size_t)(t < S ? t : 0) * I + (e < I ? e : 0));
     }
-  const uint8_t* wb = W + (size_t)blk * nb * GB;
+  // PAIR: W is the row-fused [gate; up] matrix (moty_mat_fuse_rows), the up
+  // rows' blocks start O/4 blocks after the gate rows'
   const int nchunk = nb * GB / 16;
-  int4 wc[NCH];
+  int4 wc[NM][NCH];
 #pragma unroll
-  for (int k = 0; k < NCH; k++) {
-    const int ci = lane + 64 * k;
-    wc[k] = *(const int4*)(wb + (size_t)(ci < nchunk ? ci : 0) * 16);
+  for (int m = 0; m < NM; m++) {
+    const uint8_t* wb = W + (size_t)(blk + m * O4) * nb * GB;
+#pragma unroll
+    for (int k = 0; k < NCH; k++) {
+      const int ci = lane + 64 * k;
+      wc[m][k] = *(const int4*)(wb + (size_t)(ci < nchunk ? ci : 0) * 16);
+    }
   }
   // lane l, chunk k: the 4 rows' f16 scales of group l + 64k
-  const uint16_t* db = d16 + (size_t)blk * nb * 4;
-  uint2 dc[DCH];
+  uint2 dc[NM][DCH];
 #pragma unroll
-  for (int k = 0; k < DCH; k++) {
-    const int g = lane + 64 * k;
-    dc[k] = *(const uint2*)(db + (size_t)(g < nb ? g : 0) * 4);
+  for (int m = 0; m < NM; m++) {
+    const uint16_t* db = d16 + (size_t)(blk + m * O4) * nb * 4;
+#pragma unroll
+    for (int k = 0; k < DCH; k++) {
+      const int g = lane + 64 * k;
+      dc[m][k] = *(const uint2*)(db + (size_t)(g < nb ? g : 0) * 4);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -174,32 +184,35 @@ __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, con
     const int g = Q8 ? (ci >> 3) : (ci >> 2), r = Q8 ? ((ci >> 1) & 3) : (ci & 3), h = Q8 ? (ci & 1) : 0;
     const bool ok = ci < nchunk;
     const int gc = ok ? g : 0;
-    const uint2 dsrc = dc[Q8 ? k / 8 : k / 4];
-    const uint32_t dx = __shfl(dsrc.x, g & 63, 64), dy = __shfl(dsrc.y, g & 63, 64);
-    const float dd = f16_to_f32(((r < 2 ? dx : dy) >> (16 * (r & 1))) & 0xffffu);
 #pragma unroll
-    for (int t = 0; t < S_; t++) {
-      const int8_t* xg = xq_s + t * I + gc * 32;
-      int sacc;
-      if (Q8) {
-        sacc = dot16(wc[k], *(const int4*)(xg + 16 * h), 0);
-        sacc += __shfl_xor(sacc, 1, 64);  // the row's other half: lanes 2i, 2i+1 hold (g, r, h = 0/1)
-      } else {
-        sacc = dot16(r4_lo(wc[k]), *(const int4*)xg, dot16(r4_hi(wc[k]), *(const int4*)(xg + 16), 0));
-        sacc -= 8 * xm_s[t * nb + gc];
+    for (int m = 0; m < NM; m++) {
+      const uint2 dsrc = dc[m][Q8 ? k / 8 : k / 4];
+      const uint32_t dx = __shfl(dsrc.x, g & 63, 64), dy = __shfl(dsrc.y, g & 63, 64);
+      const float dd = f16_to_f32(((r < 2 ? dx : dy) >> (16 * (r & 1))) & 0xffffu);
+#pragma unroll
+      for (int t = 0; t < S_; t++) {
+        const int8_t* xg = xq_s + t * I + gc * 32;
+        int sacc;
+        if (Q8) {
+          sacc = dot16(wc[m][k], *(const int4*)(xg + 16 * h), 0);
+          sacc += __shfl_xor(sacc, 1, 64);  // the row's other half: lanes 2i, 2i+1 hold (g, r, h = 0/1)
+        } else {
+          sacc = dot16(r4_lo(wc[m][k]), *(const int4*)xg, dot16(r4_hi(wc[m][k]), *(const int4*)(xg + 16), 0));
+          sacc -= 8 * xm_s[t * nb + gc];
+        }
+        if (ok && h == 0) op_s[((m * 4 + r) * S_ + t) * nb + g] = float2{(float)sacc, dd * xs_s[t * nb + gc]};
       }
-      if (ok && h == 0) op_s[(r * S_ + t) * nb + g] = float2{(float)sacc, dd * xs_s[t * nb + gc]};
     }
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // 4. lane (t*4 + r) runs row r's chain for token t over the groups in order
-  if (lane < 4 * S_) {
-    const int r = lane & 3, t = lane >> 2;
-    const float2* op = op_s + (r * S_ + t) * nb;
-    float acc = 0.f;
+  // 4. lane (t*4 + r) runs row r's chain for token t over the groups in
+  // order (PAIR: lane 4 + r the up row's)
+  float acc = 0.f;
+  if (lane < 4 * NM * S_) {
+    const float2* op = op_s + lane * nb;  // lane = (m*4 + r)*S_ + t with S_ = 1 for PAIR
     int g = 0;
     for (; g + 8 <= nb; g += 8) {
       float2 v[8];
@@ -209,52 +222,60 @@ __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, con
       for (int u = 0; u < 8; u++) acc = __fmaf_rn(v[u].x, v[u].y, acc);
     }
     for (; g < nb; g++) acc = __fmaf_rn(op[g].x, op[g].y, acc);
+  }
+  if (PAIR) {
+    const float u = __shfl(acc, (lane + 4) & 63, 64);
+    const int o = blk * 4 + lane;
+    if (live && lane < 4 && o < O) y[o] = ref_silu_mul(acc, u);
+  } else if (lane < 4 * S_) {
+    // lane = r*S_ + t
+    const int r = lane / S_, t = lane % S_;
     const int o = blk * 4 + r;
     if (live && t < S && o < O) y[(size_t)t * O + o] = acc;
   }
 }
 
-template <bool Q8, int S_, int IC, int NT>
+template <int S_, int NT, bool PAIR>
 static size_t r4_gemv_lds(int I) {
   const int nb = I / 32;
-  return (size_t)S_ * I + (size_t)S_ * nb * 8 + (size_t)(NT / MOTY_WAVE) * 4 * S_ * nb * 8;
+  return (size_t)S_ * I + (size_t)S_ * nb * 8 + (size_t)(NT / MOTY_WAVE) * 4 * (PAIR ? 2 : 1) * S_ * nb * 8;
 }
 
-template <bool Q8, int S_, int IC, int NT>
+template <bool Q8, int S_, int IC, int NT, bool PAIR>
 static int go_r4_gemv(const float* x, const uint8_t* W, const uint16_t* d16, float* y, int S, int I, int O,
                       hipStream_t st) {
   const int O4 = (O + 3) / 4, waves = NT / MOTY_WAVE;
-  const size_t lds = r4_gemv_lds<Q8, S_, IC, NT>(I);
-  hipLaunchKernelGGL((k_r4_gemv<Q8, S_, IC, NT>), dim3((unsigned)((O4 + waves - 1) / waves)), dim3(NT), lds, st, x,
-                     W, d16, y, S, I, O);
+  const size_t lds = r4_gemv_lds<S_, NT, PAIR>(I);
+  hipLaunchKernelGGL((k_r4_gemv<Q8, S_, IC, NT, PAIR>), dim3((unsigned)((O4 + waves - 1) / waves)), dim3(NT), lds,
+                     st, x, W, d16, y, S, I, O);
   LAUNCH_TRY("k_r4_gemv");
   return MOTY_OK;
 }
 
 // 4-wave workgroups when the LDS fits, else 2-wave ones
-template <bool Q8, int S_, int IC>
+template <bool Q8, int S_, int IC, bool PAIR>
 static int go_r4_gemv_nt(const float* x, const uint8_t* W, const uint16_t* d16, float* y, int S, int I, int O,
                          hipStream_t st) {
-  if (r4_gemv_lds<Q8, S_, IC, 256>(I) <= 64 * 1024) return go_r4_gemv<Q8, S_, IC, 256>(x, W, d16, y, S, I, O, st);
-  if (r4_gemv_lds<Q8, S_, IC, 128>(I) <= 64 * 1024) return go_r4_gemv<Q8, S_, IC, 128>(x, W, d16, y, S, I, O, st);
+  if (r4_gemv_lds<S_, 256, PAIR>(I) <= 64 * 1024) return go_r4_gemv<Q8, S_, IC, 256, PAIR>(x, W, d16, y, S, I, O, st);
+  if (r4_gemv_lds<S_, 128, PAIR>(I) <= 64 * 1024) return go_r4_gemv<Q8, S_, IC, 128, PAIR>(x, W, d16, y, S, I, O, st);
   return MOTY_EUNSUP;
 }
 
 // instances: activation float4 per thread and weight chunks per lane stay
-// within a register budget (S_ * IC <= 16, Q8R4 IC <= 8)
-template <bool Q8, int S_>
+// within a register budget (S_ * IC <= 16, Q8R4 IC <= 8; PAIR IC <= 8)
+template <bool Q8, int S_, bool PAIR = false>
 static int go_r4_gemv_ic(const float* x, const uint8_t* W, const uint16_t* d16, float* y, int S, int I, int O,
                          hipStream_t st) {
   const int ic = (I + 1023) / 1024;
-  if (ic <= 1) return go_r4_gemv_nt<Q8, S_, 1>(x, W, d16, y, S, I, O, st);
-  if (ic <= 2) return go_r4_gemv_nt<Q8, S_, 2>(x, W, d16, y, S, I, O, st);
-  if (ic <= 4) return go_r4_gemv_nt<Q8, S_, 4>(x, W, d16, y, S, I, O, st);
-  if constexpr (S_ <= 2) {
-    if (ic <= 8) return go_r4_gemv_nt<Q8, S_, 8>(x, W, d16, y, S, I, O, st);
+  if (ic <= 1) return go_r4_gemv_nt<Q8, S_, 1, PAIR>(x, W, d16, y, S, I, O, st);
+  if (ic <= 2) return go_r4_gemv_nt<Q8, S_, 2, PAIR>(x, W, d16, y, S, I, O, st);
+  if (ic <= 4) return go_r4_gemv_nt<Q8, S_, 4, PAIR>(x, W, d16, y, S, I, O, st);
+  if constexpr (S_ <= 2 && !(Q8 && PAIR)) {
+    if (ic <= 8) return go_r4_gemv_nt<Q8, S_, 8, PAIR>(x, W, d16, y, S, I, O, st);
   }
-  if constexpr (!Q8 && S_ == 1) {
-    if (ic <= 12) return go_r4_gemv_nt<Q8, S_, 12>(x, W, d16, y, S, I, O, st);
-    if (ic <= 16) return go_r4_gemv_nt<Q8, S_, 16>(x, W, d16, y, S, I, O, st);
+  if constexpr (!Q8 && !PAIR && S_ == 1) {
+    if (ic <= 12) return go_r4_gemv_nt<Q8, S_, 12, PAIR>(x, W, d16, y, S, I, O, st);
+    if (ic <= 16) return go_r4_gemv_nt<Q8, S_, 16, PAIR>(x, W, d16, y, S, I, O, st);
   }
   return MOTY_EUNSUP;
 }
@@ -454,6 +475,15 @@ int launch_r4_matmul(bool q8, const float* x, const uint8_t* W, const uint16_t* 
     hipLaunchKernelGGL(k_r4_gemm<false>, grid, dim3(R4M_NT), 0, st, xq, xs, xm, W, d16, y, S, I, O);
   LAUNCH_TRY("k_r4_gemm");
   return MOTY_OK;
+}
+
+// Decode gate/up + SiLU over a row-fused [gate; up] R4 matrix (2*I rows,
+// the gate_up of nn/ffn.c:28-37): h [I] = silu(x.gate^T) * (x.up^T), one token.
+int launch_r4_gate_up_silu(bool q8, const float* x, const uint8_t* W, const uint16_t* d16, float* h, int D, int I,
+                           hipStream_t st) {
+  if (D % 32 || D <= 0 || I % 4 || I <= 0) return MOTY_EUNSUP;
+  return q8 ? go_r4_gemv_ic<true, 1, true>(x, W, d16, h, 1, D, I, st)
+            : go_r4_gemv_ic<false, 1, true>(x, W, d16, h, 1, D, I, st);
 }
 
 // ---------------------------------------------------------------------------

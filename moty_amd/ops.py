@@ -126,6 +126,26 @@ def matmul_r4(x, q, d, O, q8=False, out=None):
     return y
 
 
+def gate_up_silu_r4(x, gu, gus, I, q8=False, out=None):
+    """Decode gate/up + SiLU over a row-fused [gate; up] R4 matrix: h [1, I]."""
+    _dev(x, gu, gus)
+    S, D = x.shape
+    h = out if out is not None else torch.empty((1, I), dtype=torch.float32, device=x.device)
+    fn = lib().moty_hip_gate_up_silu_q8r4_dev if q8 else lib().moty_hip_gate_up_silu_q4r4_dev
+    check(fn(_p(h), _p(x), _p(gu), _p(gus), D, I, _stream()), "gate_up_silu_r4")
+    return h
+
+
+def dense_ffn_r4(x, gu, gus, dn, dns, I, q8=False, out=None):
+    """nn/ffn.c:26-41 with a row-fused R4 gate_up [2I, D] and down [D, I]."""
+    _dev(x, gu, gus, dn, dns)
+    S, D = x.shape
+    y = out if out is not None else torch.empty((S, D), dtype=torch.float32, device=x.device)
+    fn = lib().moty_hip_dense_ffn_q8r4_dev if q8 else lib().moty_hip_dense_ffn_q4r4_dev
+    check(fn(_p(y), _p(x), S, _p(gu), _p(gus), _p(dn), _p(dns), D, I, _stream()), "dense_ffn_r4")
+    return y
+
+
 def matmul(x, W, out=None):
     """nn/matmul.c:15-27 (f32, dot_f32 AVX512 order)."""
     _dev(x, W)

@@ -19,7 +19,13 @@ F32 = C.c_float
 
 
 def ptr(a):
-    return None if a is None else C.c_void_p(a.ctypes.data)
+    """Address of a numpy array; the pointer object keeps the array alive, so
+    a temporary (e.g. ptr(f32(x)) after a conversion) outlives the call."""
+    if a is None:
+        return None
+    p = C.c_void_p(a.ctypes.data)
+    p._keep = a
+    return p
 
 
 _SIGS = {

@@ -119,3 +119,48 @@ def test_matmul_r4_host_dropin(ops, q8):
         assert rc == 0, lib.moty_hip_last_error()
         assert same_bits(y, o_matmul_r4(x, q, d, O, q8))
     assert lib.moty_hip_weight_forget(C.c_void_p(q.ctypes.data)) == 0
+
+
+def o_silu(g, u):
+    from cpu_libs import oracle, ptr
+    g = np.ascontiguousarray(g, np.float32).copy()
+    u = np.ascontiguousarray(u, np.float32)  # held: ptr() does not keep a temporary alive
+    oracle().o_silu_mul(ptr(g), ptr(u), g.size)
+    return g
+
+
+@pytest.mark.parametrize("q8", [False, True])
+@pytest.mark.parametrize("D,I", [(1024, 3072), (4096, 1024), (96, 40), (2048, 5632), (8192, 256)])
+def test_gate_up_silu_r4(ops, q8, D, I):
+    # one pass over the row-fused [gate; up] matrix (moty_mat_fuse_rows)
+    say("gate_up_silu_r4", q8, D, I)
+    if q8 and D > 4096:
+        pytest.skip("the fused Q8R4 gate/up GEMV serves D <= 4096 (register budget); the FFN entry point "
+                    "falls back to the GEMM there")
+    gu = randn(D + I, (2 * I, D)) * 0.02
+    x = randn(D + 1, (1, D))
+    q, d = o_pack_r4(gu, q8)
+    qd, dd = dev_r4(q, d)
+    h = to_np(ops.gate_up_silu_r4(to_dev(x), qd, dd, I, q8))
+    y = o_matmul_r4(x, q, d, 2 * I, q8)
+    h2 = o_silu(y[:, :I], y[:, I:])
+    assert same_bits(h, h2), mismatch(h, h2)
+
+
+@pytest.mark.parametrize("q8", [False, True])
+@pytest.mark.parametrize("S,D,I", [(1, 1024, 3072), (2, 256, 512), (5, 512, 256), (33, 256, 1024), (1, 4096, 1024)])
+def test_dense_ffn_r4(ops, q8, S, D, I):
+    # moty_nn_dense_ffn with the fused gate_up (nn/ffn.c:26-41)
+    say("dense_ffn_r4", q8, S, D, I)
+    gu = randn(S + D, (2 * I, D)) * 0.02
+    dn = randn(S + I, (D, I)) * 0.02
+    x = randn(S + 7, (S, D))
+    q, d = o_pack_r4(gu, q8)
+    q2, d2 = o_pack_r4(dn, q8)
+    qd, dd = dev_r4(q, d)
+    q2d, d2d = dev_r4(q2, d2)
+    out = to_np(ops.dense_ffn_r4(to_dev(x), qd, dd, q2d, d2d, I, q8))
+    y = o_matmul_r4(x, q, d, 2 * I, q8)
+    h = o_silu(y[:, :I], y[:, I:])
+    ref = o_matmul_r4(h, q2, d2, D, q8)
+    assert same_bits(out, ref), mismatch(out, ref)
