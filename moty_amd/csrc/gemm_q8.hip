@@ -20,11 +20,11 @@ constexpr int GM_LS = 144;  // padded LDS row stride
 // y[M][O] from xq[M][K], W[O][K]; K % 16 == 0.  Block tile BM x BN with
 // BM = 64*WM, BN = 64*WN; wave (wm, wn) owns (32*WM) x (32*WN) outputs as
 // WM x WN v_mfma_i32_32x32x32_i8 tiles.  Per 128-byte K block the tile is
-// staged in LDS by whole-line loads (8 lanes x 16 B per row); two register
-// sets keep the next two blocks' loads in flight during the MFMAs.  MFMA step j takes, in lane l,
-// bytes [64*(l/32) + 16j, +16) of row (l % 32): a k-permutation shared by
-// both operands, exact for integer dots.
-template <int WM, int WN>
+// staged in LDS by whole-line loads (8 lanes x 16 B per row); NS register
+// sets keep the next K blocks' loads in flight during the MFMAs.  MFMA step
+// j takes, in lane l, bytes [64*(l/32) + 16j, +16) of row (l % 32): a
+// k-permutation shared by both operands, exact for integer dots.
+template <int WM, int WN, int NS = 2>
 __global__ __launch_bounds__(GM_NT, 2) void k_gemm_q8(const int8_t* __restrict__ xq, const float* __restrict__ sx,
                                                       const int8_t* __restrict__ W, const float* __restrict__ scale,
                                                       float* __restrict__ y, int M, int K, int O) {
@@ -52,13 +52,13 @@ __global__ __launch_bounds__(GM_NT, 2) void k_gemm_q8(const int8_t* __restrict__
     n = n < O ? n : O - 1;
     srcB[i] = W + (int64_t)n * K + col;
   }
-  // two register sets: while one K block is consumed from LDS, the next two
+  // NS register sets: while one K block is consumed from LDS, the next NS
   // are in flight from HBM.  Every load is unconditional, from a clamped
   // address (a chunk past the row end re-reads the row start; a K block past
   // the end re-reads the last block, an L2 hit), and chunks past the end are
   // zeroed when written to LDS: with no branch around a load, the compiler
   // waits only for the register set about to be consumed.
-  int4 ra0[NA], rb0[NB], ra1[NA], rb1[NB];
+  int4 setA[NS][NA], setB[NS][NB];
   const int klast = (K - 1) / GM_KB * GM_KB;
   auto gload = [&](int k0, int4(&ra)[NA], int4(&rb)[NB]) {
     const int kc = k0 < K ? k0 : klast;
@@ -97,7 +97,8 @@ __global__ __launch_bounds__(GM_NT, 2) void k_gemm_q8(const int8_t* __restrict__
 #pragma unroll
     for (int i = 0; i < NB; i++) *(int4*)(sB + ((tid + i * GM_NT) >> 3) * GM_LS + col) = sel4(ok, rb[i]);
     __syncthreads();
-    gload(k0 + 2 * GM_KB, ra, rb);
+    gload(k0 + NS * GM_KB, ra, rb);
+    if (k0 < K) {  // a trailing block past the end adds nothing: skip it
 #pragma unroll
     for (int st = 0; st < 4; st++) {
       v4i fa[WM], fb[WN];
@@ -112,14 +113,14 @@ __global__ __launch_bounds__(GM_NT, 2) void k_gemm_q8(const int8_t* __restrict__
 #pragma unroll
         for (int j = 0; j < WN; j++) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
     }
+    }
     __syncthreads();
   };
-  gload(0, ra0, rb0);
-  gload(GM_KB, ra1, rb1);
-  // an odd number of K blocks runs one all-zero block (adds exactly 0)
-  for (int k0 = 0; k0 < K; k0 += 2 * GM_KB) {
-    stage(k0, ra0, rb0);
-    stage(k0 + GM_KB, ra1, rb1);
+#pragma unroll
+  for (int i = 0; i < NS; i++) gload(i * GM_KB, setA[i], setB[i]);
+  for (int k0 = 0; k0 < K; k0 += NS * GM_KB) {
+#pragma unroll
+    for (int i = 0; i < NS; i++) stage(k0 + i * GM_KB, setA[i], setB[i]);
   }
   // retire every load still in flight (the clamped prefetches past the end)
   // once, here: otherwise the compiler waits for all memory operations --
@@ -146,13 +147,16 @@ int launch_gemm_q8(const int8_t* xq, const float* sx, const int8_t* W, const flo
                    int K, int O, hipStream_t st) {
   if (K % 16) return MOTY_EUNSUP;
   if (M <= 0 || O <= 0) return MOTY_OK;
-  // largest tile that still yields a workgroup per CU on the 256-CU part
+  // Tiles and prefetch depth from a sweep on MI355X (M = 512, the C2
+  // projections): 64 x 64 tiles beat 128 x 128 until the grid holds several
+  // workgroups per CU (N=10240, K=1024: 17.1 us vs 18.5); long K rows keep
+  // four K blocks in flight (K=2048: 9.6 us vs 10.1, K=3072: 12.5 vs 13.5).
   auto nblk = [&](int bm, int bn) { return (int64_t)((M + bm - 1) / bm) * ((O + bn - 1) / bn); };
-  if (nblk(128, 128) >= 256) {
+  if (nblk(128, 128) >= 1024) {
     hipLaunchKernelGGL((k_gemm_q8<2, 2>), dim3((O + 127) / 128, (M + 127) / 128), dim3(GM_NT), 0, st, xq, sx, W,
                        scale, y, M, K, O);
-  } else if (nblk(64, 128) >= 256) {
-    hipLaunchKernelGGL((k_gemm_q8<1, 2>), dim3((O + 127) / 128, (M + 63) / 64), dim3(GM_NT), 0, st, xq, sx, W,
+  } else if (K >= 2048) {
+    hipLaunchKernelGGL((k_gemm_q8<1, 1, 4>), dim3((O + 63) / 64, (M + 63) / 64), dim3(GM_NT), 0, st, xq, sx, W,
                        scale, y, M, K, O);
   } else {
     hipLaunchKernelGGL((k_gemm_q8<1, 1>), dim3((O + 63) / 64, (M + 63) / 64), dim3(GM_NT), 0, st, xq, sx, W, scale,
