@@ -400,33 +400,54 @@ __global__ __launch_bounds__(R4M_NT, 2) void k_r4_gemm(const int8_t* __restrict_
     }
     __syncthreads();
     gload(g0 + 2 * R4M_KG, sv);
-    const int ngk = (nb - g0) < R4M_KG ? (nb - g0) : R4M_KG;
+    if constexpr (Q8) {
+      // Straight-line over the block's groups -- fragments, the MFMAs, then
+      // the epilogues in group order -- so the MFMAs overlap.  Groups past
+      // the row end hold zero codes and scales: their steps add exactly
+      // nothing (fma(0, 0, acc) = acc; acc is never -0).
+      if (g0 < nb) {
+        v4i af[R4M_KG], bf[R4M_KG];
 #pragma unroll
-    for (int gg = 0; gg < R4M_KG; gg++) {
-      if (gg >= ngk) break;  // wave-uniform
-      const v4i a = *(const v4i*)(sA + (wm * 32 + r32) * R4M_AS + gg * 32 + hk * 16);
-      v4i b;
-      if (Q8) {
-        b = *(const v4i*)(sB + (wn * 32 + r32) * BS + gg * RB + hk * 16);
-      } else {
+        for (int gg = 0; gg < R4M_KG; gg++) {
+          af[gg] = *(const v4i*)(sA + (wm * 32 + r32) * R4M_AS + gg * 32 + hk * 16);
+          bf[gg] = *(const v4i*)(sB + (wn * 32 + r32) * BS + gg * RB + hk * 16);
+        }
+        v16i dsum[R4M_KG];
+#pragma unroll
+        for (int gg = 0; gg < R4M_KG; gg++)
+          dsum[gg] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[gg], bf[gg], v16i{}, 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);  // all MFMAs issue before the epilogues
+#pragma unroll
+        for (int gg = 0; gg < R4M_KG; gg++) {
+          const float dd = sD[(wn * 32 + r32) * R4M_KG + gg];
+          // D layout: lane l, register r -> token 8*(r/4) + 4*(l/32) + r%4, row l%32
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const float4 xv = *(const float4*)(sX + gg * 64 + wm * 32 + 8 * q + 4 * hk);
+            accf[4 * q + 0] = __fmaf_rn((float)dsum[gg][4 * q + 0], dd * xv.x, accf[4 * q + 0]);
+            accf[4 * q + 1] = __fmaf_rn((float)dsum[gg][4 * q + 1], dd * xv.y, accf[4 * q + 1]);
+            accf[4 * q + 2] = __fmaf_rn((float)dsum[gg][4 * q + 2], dd * xv.z, accf[4 * q + 2]);
+            accf[4 * q + 3] = __fmaf_rn((float)dsum[gg][4 * q + 3], dd * xv.w, accf[4 * q + 3]);
+          }
+        }
+      }
+    } else {
+      // Q4R4 (a heavier epilogue): group by group, within the register budget
+      const int ngk = (nb - g0) < R4M_KG ? (nb - g0) : R4M_KG;
+#pragma unroll
+      for (int gg = 0; gg < R4M_KG; gg++) {
+        if (gg >= ngk) break;  // wave-uniform
+        const v4i a = *(const v4i*)(sA + (wm * 32 + r32) * R4M_AS + gg * 32 + hk * 16);
         const int4 w = *(const int4*)(sB + (wn * 32 + r32) * BS + gg * RB);
         const int4 u = hk ? r4_hi(w) : r4_lo(w);
-        b = v4i{u.x, u.y, u.z, u.w};
-      }
-      v16i dsum = {};
-      dsum = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, dsum, 0, 0, 0);
-      const float dd = sD[(wn * 32 + r32) * R4M_KG + gg];
-      // D layout: lane l, register r -> token 8*(r/4) + 4*(l/32) + r%4, row l%32
+        v16i dsum = {};
+        dsum = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, v4i{u.x, u.y, u.z, u.w}, dsum, 0, 0, 0);
+        const float dd = sD[(wn * 32 + r32) * R4M_KG + gg];
+        // D layout: lane l, register r -> token 8*(r/4) + 4*(l/32) + r%4, row l%32
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const int tb = wm * 32 + 8 * q + 4 * hk;
-        const float4 xv = *(const float4*)(sX + gg * 64 + tb);
-        if (Q8) {
-          accf[4 * q + 0] = __fmaf_rn((float)dsum[4 * q + 0], dd * xv.x, accf[4 * q + 0]);
-          accf[4 * q + 1] = __fmaf_rn((float)dsum[4 * q + 1], dd * xv.y, accf[4 * q + 1]);
-          accf[4 * q + 2] = __fmaf_rn((float)dsum[4 * q + 2], dd * xv.z, accf[4 * q + 2]);
-          accf[4 * q + 3] = __fmaf_rn((float)dsum[4 * q + 3], dd * xv.w, accf[4 * q + 3]);
-        } else {
+        for (int q = 0; q < 4; q++) {
+          const int tb = wm * 32 + 8 * q + 4 * hk;
+          const float4 xv = *(const float4*)(sX + gg * 64 + tb);
           const int4 mv = *(const int4*)(sM + gg * 64 + tb);
           const float4 cv = *(const float4*)(sC + gg * 64 + tb);
           accf[4 * q + 0] = __fmaf_rn(-dd, cv.x, __fmaf_rn((float)(dsum[4 * q + 0] + mv.x), dd * xv.x, accf[4 * q + 0]));
