@@ -283,6 +283,52 @@ def bench_c3_r4(c, steps, warmup):
                         "I=12288, M=1 and M=256", **res}
 
 
+def bench_gguf(c, steps, warmup):
+    """Loading GGUF weights on the device (io/gguf.h): the lossless Q4_0 ->
+    grouped-int4 repack (runtime/rt_model_load.h:26-34) and the block
+    dequantisers, on one 8B-model FFN matrix (12288 x 4096).  Pure byte
+    streams: algorithmic bytes = block bytes read + output bytes written."""
+    torch, ops = c.torch, c.ops
+    O, I = 12288, 4096
+    n = O * I
+    blk = {4: (32, 34), 5: (32, 18), 6: (256, 144), 7: (256, 176), 8: (256, 210)}
+    names = {4: "Q8_0", 5: "Q4_0", 6: "Q4_K", 7: "Q5_K", 8: "Q6_K"}
+    g = c.gen(6, 1)
+    res = {}
+
+    def raws(dt):
+        E, B = blk[dt]
+        nb = n // E * B
+        return [torch.randint(0, 256, (nb,), generator=g, device="cuda:0", dtype=torch.uint8)
+                for _ in range(n_copies(nb + n * 4, lo=3))]
+
+    rs = raws(5)
+    q4 = [torch.empty((O, I // 2), dtype=torch.uint8, device="cuda:0") for _ in range(2)]
+    qs = [torch.empty((O, I // 32), device="cuda:0") for _ in range(2)]
+    lib, P = ops.lib(), ops._p  # raw entry points: no output allocation per call
+    fns = [lambda r=r, k=k: ops.check(lib.moty_hip_gguf_repack_q4_0_dev(P(r), P(q4[k % 2]), P(qs[k % 2]), O, I,
+                                                                        ops._stream()), "repack")
+           for k, r in enumerate(rs)]
+    t, _ = c.time_steps(fns, steps, warmup)
+    algo = n // 32 * (18 + 16 + 4)
+    res["repack_Q4_0"] = {"us": round(t * 1e6, 2), "algo_bytes": algo,
+                          **roofline("hbm", algo / t / 1e9, HBM_PEAK_GBS, "GB/s")}
+    outs = [torch.empty(n, device="cuda:0") for _ in range(2)]
+    for dt in sorted(blk):
+        rs = raws(dt)
+        fns = [lambda r=r, k=k, dt=dt: ops.check(lib.moty_hip_gguf_dequant_dev(dt, P(r), n, P(outs[k % 2]),
+                                                                               ops._stream()), "dequant")
+               for k, r in enumerate(rs)]
+        t, _ = c.time_steps(fns, steps, warmup)
+        E, B = blk[dt]
+        algo = n // E * B + n * 4
+        res["dequant_" + names[dt]] = {"us": round(t * 1e6, 2), "algo_bytes": algo,
+                                       **roofline("hbm", algo / t / 1e9, HBM_PEAK_GBS, "GB/s")}
+        del rs
+    return {"workload": "GGUF -> device layouts on a 12288 x 4096 matrix (Q4_0 repack to grouped int4; "
+                        "Q8_0/Q4_0/Q4_K/Q5_K/Q6_K dequant to f32)", **res}
+
+
 def pmc_probe(c):
     """For the rocprofv3 --pmc runs behind roofline.traffic: the C1 gate+up
     GEMV on 8 distinct weight copies (3 rounds), then a plain 64 MiB
@@ -407,6 +453,8 @@ def main():
         extra.append(bench_c3(c, args.steps, args.warmup))
         log("C3 in Q4R4")
         extra.append(bench_c3_r4(c, args.steps, args.warmup))
+        log("GGUF loading")
+        extra.append(bench_gguf(c, args.steps, args.warmup))
         log("C5")
         E5 = 128
         bias = torch.zeros(E5, device="cuda:0")

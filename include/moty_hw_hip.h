@@ -102,6 +102,24 @@ typedef struct MotyHipMoe {
  * Host pointers; out [S][D].  Served for D, I multiples of 32, E <= 256, K <= 64. */
 int moty_hip_moe_topk(const MotyHipMoe *m, const float *x, int S, float *out);
 
+/* GGUF block types (io/st.h:74): the dtype argument of the GGUF calls */
+#define MOTY_GGUF_Q8_0 4
+#define MOTY_GGUF_Q4_0 5
+#define MOTY_GGUF_Q4_K 6
+#define MOTY_GGUF_Q5_K 7
+#define MOTY_GGUF_Q6_K 8
+
+/* gguf_dequant (io/gguf.h:316-326), the g_st_dequant_fn hook of
+ * st_read_f32: numel elements (a multiple of the type's block: 32 or 256)
+ * from raw blocks to f32.  Host pointers; unknown types -> EUNSUP (the
+ * reference exits). */
+int moty_hip_gguf_dequant(int dtype, const void *raw, int64_t numel, float *out);
+/* gguf_repack_q4_0 (io/gguf.h:340-357) as load_mat_q4_0 uses it
+ * (runtime/rt_model_load.h:26-34): Q4_0 blocks of an [O][I] matrix ->
+ * grouped int4 q4 [O][I/2] + f32 scales qs [O][I/32], bit-preserving.
+ * I a multiple of 32.  Host pointers. */
+int moty_hip_gguf_repack_q4_0(const uint8_t *blocks, uint8_t *q4, float *qs, int64_t O, int64_t I);
+
 /* Drop the cached device copy of a host weight buffer (after the caller
  * frees or rewrites it). */
 int moty_hip_weight_forget(const void *host_ptr);
@@ -182,6 +200,14 @@ int moty_hip_quant_g32_dev(const float *x, int8_t *xq, float *xs, int32_t *xsum,
  * (nn/quant.c:135-177) over every 4-row block of w [O][I] f32. */
 int moty_hip_pack_q4r4_dev(const float *w, uint8_t *q4, uint16_t *s16, int O, int I, void *stream);
 int moty_hip_pack_q8r4_dev(const float *w, int8_t *q8, uint16_t *s16, int O, int I, void *stream);
+/* GGUF loading on the device: the same two conversions with raw, out,
+ * blocks, q4, qs in device memory (out and q4 16-byte aligned, qs 4-byte).
+ * Chained with moty_hip_quantize_rows_dev / moty_hip_pack_int4_grouped_dev
+ * they give load_mat_bits' QBITS=8 / QBITS=4 paths for every GGUF block
+ * type (runtime/rt_model_load.h:122-157). */
+int moty_hip_gguf_dequant_dev(int dtype, const void *raw, int64_t numel, float *out, void *stream);
+int moty_hip_gguf_repack_q4_0_dev(const uint8_t *blocks, uint8_t *q4, float *qs, int64_t O, int64_t I,
+                                  void *stream);
 /* the MoE layer, all pointers in m and x/out on the device */
 int moty_hip_moe_topk_dev(const MotyHipMoe *m, const float *x, int S, float *out, void *stream);
 

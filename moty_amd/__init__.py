@@ -47,6 +47,10 @@ SIGNATURES = {
     "moty_hip_dense_ffn_q8r4_dev": (I32, [P, P, I32, P, P, P, P, I32, I32, P]),
     "moty_hip_pack_q4r4_dev": (I32, [P, P, P, I32, I32, P]),
     "moty_hip_pack_q8r4_dev": (I32, [P, P, P, I32, I32, P]),
+    "moty_hip_gguf_dequant": (I32, [I32, P, I64, P]),
+    "moty_hip_gguf_repack_q4_0": (I32, [P, P, P, I64, I64]),
+    "moty_hip_gguf_dequant_dev": (I32, [I32, P, I64, P, P]),
+    "moty_hip_gguf_repack_q4_0_dev": (I32, [P, P, P, I64, I64, P]),
     "moty_hip_matmul": (I32, [P, P, P, I32, I32, I32]),
     "moty_hip_moe_topk": (I32, [C.POINTER(MotyHipMoe), P, I32, P]),
     "moty_hip_weight_forget": (I32, [P]),

@@ -576,6 +576,65 @@ int moty_hip_pack_q8r4_dev(const float* w, int8_t* q8, uint16_t* s16, int O, int
   return launch_pack_r4(true, w, (uint8_t*)q8, s16, O, I, STREAM(stream));
 }
 
+// ---- GGUF block formats (io/gguf.h:231-357) ----
+static int gguf_check(int dtype, int64_t numel, const void* raw, const void* out, const char* what) {
+  int E, B;
+  if (numel < 0 || (numel && (!raw || !out))) return set_error("%s: bad arguments", what), MOTY_EINVAL;
+  if (!gguf_block(dtype, &E, &B)) return set_error("%s: GGUF type %d not supported", what, dtype), MOTY_EUNSUP;
+  if (numel % E) return set_error("%s: numel=%lld is not a multiple of %d", what, (long long)numel, E), MOTY_EINVAL;
+  return MOTY_OK;
+}
+
+int moty_hip_gguf_dequant_dev(int dtype, const void* raw, int64_t numel, float* out, void* stream) {
+  CUR(d);
+  int rc = gguf_check(dtype, numel, raw, out, "gguf_dequant");
+  if (rc) return rc;
+  if ((uintptr_t)out & 15) return set_error("gguf_dequant: out must be 16-byte aligned"), MOTY_EINVAL;
+  return launch_gguf_dequant(dtype, raw, out, numel, STREAM(stream));
+}
+
+static int q40_check(const void* blocks, const void* q4, const void* qs, int64_t O, int64_t I) {
+  if (O < 0 || I <= 0 || (O && (!blocks || !q4 || !qs))) return set_error("gguf_repack_q4_0: bad arguments"), MOTY_EINVAL;
+  if (I % 32) return set_error("gguf_repack_q4_0: I=%lld must be a multiple of 32", (long long)I), MOTY_EINVAL;
+  return MOTY_OK;
+}
+
+int moty_hip_gguf_repack_q4_0_dev(const uint8_t* blocks, uint8_t* q4, float* qs, int64_t O, int64_t I,
+                                  void* stream) {
+  CUR(d);
+  int rc = q40_check(blocks, q4, qs, O, I);
+  if (rc) return rc;
+  if ((uintptr_t)q4 & 15 || (uintptr_t)qs & 3)
+    return set_error("gguf_repack_q4_0: q4 must be 16-byte and qs 4-byte aligned"), MOTY_EINVAL;
+  return launch_gguf_repack_q4_0(blocks, q4, qs, O * (I / 32), STREAM(stream));
+}
+
+int moty_hip_gguf_dequant(int dtype, const void* raw, int64_t numel, float* out) {
+  CUR(d);
+  int rc = gguf_check(dtype, numel, raw, out, "gguf_dequant");
+  if (rc || numel == 0) return rc;
+  int E, B;
+  gguf_block(dtype, &E, &B);
+  void *dr, *dy;
+  if ((rc = stage_io(d, raw, (size_t)(numel / E) * B, (size_t)numel * 4, &dr, &dy))) return rc;
+  if ((rc = launch_gguf_dequant(dtype, dr, (float*)dy, numel, d->stream))) return rc;
+  return finish_io(d, out, dy, (size_t)numel * 4);
+}
+
+int moty_hip_gguf_repack_q4_0(const uint8_t* blocks, uint8_t* q4, float* qs, int64_t O, int64_t I) {
+  CUR(d);
+  int rc = q40_check(blocks, q4, qs, O, I);
+  if (rc || O == 0) return rc;
+  const int64_t nblk = O * (I / 32);
+  void *dr, *dy;
+  if ((rc = stage_io(d, blocks, (size_t)nblk * 18, (size_t)nblk * 20, &dr, &dy))) return rc;
+  uint8_t* dq = (uint8_t*)dy;
+  float* ds = (float*)(dq + nblk * 16);
+  if ((rc = launch_gguf_repack_q4_0(dr, dq, ds, nblk, d->stream))) return rc;
+  HIP_TRY(hipMemcpyAsync(q4, dq, (size_t)nblk * 16, hipMemcpyDeviceToHost, d->stream));
+  return finish_io(d, qs, ds, (size_t)nblk * 4);
+}
+
 void moty_hip_hw_matmul_i8(float* y, const float* x, const int8_t* q, const float* scale, int S, int I, int O) {
   (void)moty_hip_matmul_q_s(y, x, q, scale, S, I, O);
 }

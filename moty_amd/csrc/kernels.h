@@ -40,6 +40,13 @@ int launch_r4_gate_up_silu(bool q8, const float* x, const uint8_t* W, const uint
                            hipStream_t st);
 int launch_pack_r4(bool q8, const float* w, uint8_t* q, uint16_t* d16, int O, int I, hipStream_t st);
 
+// GGUF block formats (type ids of io/st.h:74): block dequantization to f32
+// and the lossless Q4_0 -> grouped-int4 (gs = 32) repack
+enum { GG_Q8_0 = 4, GG_Q4_0 = 5, GG_Q4_K = 6, GG_Q5_K = 7, GG_Q6_K = 8 };
+int gguf_block(int dtype, int* elems, int* bytes);
+int launch_gguf_dequant(int dtype, const void* raw, float* out, int64_t numel, hipStream_t st);
+int launch_gguf_repack_q4_0(const void* raw, uint8_t* q4, float* qs, int64_t nblk, hipStream_t st);
+
 int launch_matmul_f32(const float* x, const float* W, float* y, int S, int I, int O, hipStream_t st);
 int launch_silu_mul(float* g, const float* u, int64_t n, hipStream_t st);
 int launch_silu_rows(float* h, const float* gu, int S, int I, hipStream_t st);

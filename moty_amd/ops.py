@@ -116,6 +116,34 @@ def quant_g32(x):
     return xq, xs, xm
 
 
+GGUF_BLOCK = {4: (32, 34), 5: (32, 18), 6: (256, 144), 7: (256, 176), 8: (256, 210)}
+
+
+def gguf_dequant(dtype, raw, numel, out=None):
+    """io/gguf.h:316-326 (gguf_dequant): `numel` elements of GGUF block type
+    `dtype` (4 Q8_0, 5 Q4_0, 6 Q4_K, 7 Q5_K, 8 Q6_K) from the raw uint8 block
+    bytes to f32."""
+    _dev(raw)
+    E, B = GGUF_BLOCK.get(dtype, (0, 0))
+    if E and (numel % E or raw.numel() < numel // E * B):
+        raise ValueError("gguf_dequant: raw holds fewer than numel/%d blocks of %d bytes" % (E, B))
+    y = out if out is not None else torch.empty(numel, dtype=torch.float32, device=raw.device)
+    check(lib().moty_hip_gguf_dequant_dev(dtype, _p(raw), numel, _p(y), _stream()), "gguf_dequant")
+    return y
+
+
+def gguf_repack_q4_0(blocks, O, I):
+    """io/gguf.h:340-357: Q4_0 blocks of an [O, I] matrix -> (q4 uint8 [O, I/2],
+    scales f32 [O, I/32]), the grouped int4 layout with gs = 32."""
+    _dev(blocks)
+    if I % 32 or blocks.numel() < O * (I // 32) * 18:
+        raise ValueError("gguf_repack_q4_0: needs I %% 32 == 0 and O*I/32 blocks of 18 bytes")
+    q4 = torch.empty((O, I // 2), dtype=torch.uint8, device=blocks.device)
+    qs = torch.empty((O, I // 32), dtype=torch.float32, device=blocks.device)
+    check(lib().moty_hip_gguf_repack_q4_0_dev(_p(blocks), _p(q4), _p(qs), O, I, _stream()), "gguf_repack_q4_0")
+    return q4, qs
+
+
 def matmul_r4(x, q, d, O, q8=False, out=None):
     """moty_matmul_q4r4_s / moty_matmul_q8r4_s (nn/matmul.c:395-466): y [S, O]."""
     _dev(x, q, d)

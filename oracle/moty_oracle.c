@@ -28,6 +28,11 @@
  *       _ref bit-exact (moty_hw_quant_g32, moty_pack_q{4,8}r4_block,
  *       moty_matmul_q{4,8}r4_s), the no-clip packing bounds and the double
  *       dequantized reference of c/tests/q4r4_tests.c
+ *   o_gguf_repack_q4_0, o_gguf_dequant -> _ref bit-exact (io/gguf.h built
+ *       from the reference tree), the hand-built known-answer blocks of
+ *       c/tests/headers_tests.c:131-211 and qwen_tests.c:799-847, and
+ *       repack/dequant agreement (dequantizing the repacked int4 equals
+ *       the Q4_0 dequant)
  */
 #include <math.h>
 #include <stdint.h>
@@ -655,4 +660,105 @@ O_EXPORT void o_matmul_q8r4(float *y, const float *x, const int8_t *q, const uin
         }
     }
     free(xq); free(xs); free(xm);
+}
+
+/* ------------------------------------------------------------------ */
+/* GGUF block formats -> device layouts.                               */
+/* io/gguf.h:231-357 (block dequantisers and the Q4_0 repack),         */
+/* io/st.h:74-80 (type ids and block sizes)                            */
+enum { O_GG_Q8_0 = 4, O_GG_Q4_0 = 5, O_GG_Q4_K = 6, O_GG_Q5_K = 7, O_GG_Q6_K = 8 };
+
+static uint16_t o_rd16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* elements per block and bytes per block; 0 if the id is not a block type */
+O_EXPORT int o_gguf_block(int dtype, int *elems, int *bytes) {
+    static const int E[9] = {0, 0, 0, 0, 32, 32, 256, 256, 256};
+    static const int B[9] = {0, 0, 0, 0, 34, 18, 144, 176, 210};
+    if (dtype < 4 || dtype > 8) return 0;
+    *elems = E[dtype]; *bytes = B[dtype];
+    return 1;
+}
+
+/* Q4_0 holds element i of a 32-block in the low nibble of byte i and element
+ * i+16 in the high nibble; the grouped int4 layout holds elements 2k, 2k+1 in
+ * byte k (low, high).  Both store v+8, so the repack moves nibbles and
+ * widens the f16 scale (io/gguf.h:335-357). */
+O_EXPORT void o_gguf_repack_q4_0(const uint8_t *blocks, uint8_t *q4, float *qs, int64_t O, int64_t I) {
+    int64_t nblk = O * (I / 32);
+    for (int64_t b = 0; b < nblk; b++) {
+        const uint8_t *src = blocks + b * 18, *nib = src + 2;
+        qs[b] = o_f16_to_f32(o_rd16(src));
+        uint8_t el[32];
+        for (int i = 0; i < 16; i++) { el[i] = nib[i] & 15; el[i + 16] = nib[i] >> 4; }
+        for (int k = 0; k < 16; k++) q4[b * 16 + k] = (uint8_t)(el[2 * k] | (el[2 * k + 1] << 4));
+    }
+}
+
+/* K-quant 6-bit sub-block scale and min, j = 0..7 (io/gguf.h:253-260):
+ * bytes 0-3 carry scales 0-3, bytes 4-7 mins 0-3 (low six bits each);
+ * sub-blocks 4-7 take their low four bits from bytes 8-11 and their top two
+ * from the spare high bits of bytes 0-7. */
+static void o_k4_sm(const uint8_t *s, int j, float d, float dmin, float *sc, float *mn) {
+    int a, m;
+    if (j < 4) { a = s[j] & 63; m = s[j + 4] & 63; }
+    else { a = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4); m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4); }
+    *sc = d * (float)a;
+    *mn = dmin * (float)m;
+}
+
+/* Block dequantisers behind st_read_f32 (io/gguf.h:231-330).  Q4_K / Q5_K
+ * compute sc*q - mn, which the reference's x86 build fuses into one FMA; the
+ * fusion cannot change a result (sc = f16 * 6-bit integer and q < 32, so
+ * sc*q is exact in f32), and the FMA is kept only to mirror that build. */
+O_EXPORT int o_gguf_dequant(int dtype, const uint8_t *raw, int64_t numel, float *out) {
+    int E, B;
+    if (!o_gguf_block(dtype, &E, &B) || numel % E) return -1;
+    int64_t nblk = numel / E;
+    for (int64_t b = 0; b < nblk; b++) {
+        const uint8_t *p = raw + b * B;
+        float *y = out + b * E;
+        if (dtype == O_GG_Q8_0) {
+            float d = o_f16_to_f32(o_rd16(p));
+            for (int i = 0; i < 32; i++) y[i] = d * (float)(int8_t)p[2 + i];
+        } else if (dtype == O_GG_Q4_0) {
+            float d = o_f16_to_f32(o_rd16(p));
+            for (int i = 0; i < 16; i++) {
+                y[i] = d * (float)((p[2 + i] & 15) - 8);
+                y[i + 16] = d * (float)((p[2 + i] >> 4) - 8);
+            }
+        } else if (dtype == O_GG_Q4_K || dtype == O_GG_Q5_K) {
+            /* 4 chunks of 64: low nibbles of 32 bytes (sub-block 2c), then the
+             * high nibbles (sub-block 2c+1); Q5_K adds 16 from bit 2c / 2c+1
+             * of qh[l] */
+            int q5 = dtype == O_GG_Q5_K;
+            float d = o_f16_to_f32(o_rd16(p)), dmin = o_f16_to_f32(o_rd16(p + 2));
+            const uint8_t *s = p + 4, *qh = p + 16, *ql = p + (q5 ? 48 : 16);
+            for (int c = 0; c < 4; c++)
+                for (int h = 0; h < 2; h++) {
+                    float sc, mn;
+                    o_k4_sm(s, 2 * c + h, d, dmin, &sc, &mn);
+                    for (int l = 0; l < 32; l++) {
+                        int v = h ? ql[32 * c + l] >> 4 : ql[32 * c + l] & 15;
+                        if (q5 && ((qh[l] >> (2 * c + h)) & 1)) v += 16;
+                        y[64 * c + 32 * h + l] = fmaf(sc, (float)v, -mn);
+                    }
+                }
+        } else {
+            /* Q6_K: two halves of 128; element 128n + 32r + l takes its low
+             * four bits from ql[64n + l + 32(r&1)] (nibble r>>1), its top two
+             * from bits 2r of qh[32n + l], and int8 scale sc[8n + l/16 + 2r];
+             * value (d*sc)*(q-32) */
+            const uint8_t *ql = p, *qh = p + 128;
+            const int8_t *sc = (const int8_t *)(p + 192);
+            float d = o_f16_to_f32(o_rd16(p + 208));
+            for (int n = 0; n < 2; n++)
+                for (int r = 0; r < 4; r++)
+                    for (int l = 0; l < 32; l++) {
+                        uint8_t lo = ql[64 * n + l + 32 * (r & 1)];
+                        int v = ((r >> 1) ? lo >> 4 : lo & 15) | (((qh[32 * n + l] >> (2 * r)) & 3) << 4);
+                        y[128 * n + 32 * r + l] = d * (float)sc[8 * n + l / 16 + 2 * r] * (float)(v - 32);
+                    }
+        }
+    }
+    return 0;
 }

@@ -14,6 +14,7 @@
 #include "nn/nn_matmul.h"
 #include "nn/nn_norm.h"
 #include "nn/moe.h"
+#include "io/gguf.h"
 
 #define R_EXPORT __attribute__((visibility("default")))
 
@@ -114,4 +115,13 @@ R_EXPORT void ref_moe_olmoe(float *out, const float *x, int S, const float *Wr,
         }
     }
     free(logits); free(g); free(u); free(hh);
+}
+
+/* GGUF block formats (io/gguf.h, header-only): the lossless Q4_0 -> int4
+ * grouped repack and the block dequantisers behind st_read_f32. */
+R_EXPORT void ref_gguf_repack_q4_0(const uint8_t *blocks, uint8_t *q4, float *qs, int64_t O, int64_t I) {
+    gguf_repack_q4_0(blocks, q4, qs, O, I);
+}
+R_EXPORT void ref_gguf_dequant(int dtype, const void *raw, int64_t numel, float *out) {
+    gguf_dequant(dtype, raw, numel, out);
 }

@@ -57,6 +57,11 @@ _SIGS = {
     "o_pack_q8r4": (None, [P, I32, I32, P, P]),
     "o_matmul_q4r4": (None, [P, P, P, P, I32, I32, I32]),
     "o_matmul_q8r4": (None, [P, P, P, P, I32, I32, I32]),
+    "o_gguf_block": (I32, [I32, P, P]),
+    "o_gguf_repack_q4_0": (None, [P, P, P, I64, I64]),
+    "o_gguf_dequant": (I32, [I32, P, I64, P]),
+    "ref_gguf_repack_q4_0": (None, [P, P, P, I64, I64]),
+    "ref_gguf_dequant": (None, [I32, P, I64, P]),
     # the reference's own R4 symbols (nn/quant.c, hw/hw_q4r4.h, nn/matmul.c)
     "moty_hw_f16_to_f32": (F32, [C.c_uint16]),
     "moty_f32_to_f16": (C.c_uint16, [F32]),
@@ -304,3 +309,51 @@ def ref_matmul_r4(r, x, q, d, O, q8=False):
     y = np.empty((S, O), np.float32)
     (r.moty_matmul_q8r4_s if q8 else r.moty_matmul_q4r4_s)(ptr(y), ptr(x), ptr(q), ptr(d), S, I, O)
     return y
+
+
+# ---- GGUF block formats (io/gguf.h) ----
+GG_Q8_0, GG_Q4_0, GG_Q4_K, GG_Q5_K, GG_Q6_K = 4, 5, 6, 7, 8
+GG_BLOCK = {GG_Q8_0: (32, 34), GG_Q4_0: (32, 18), GG_Q4_K: (256, 144),
+            GG_Q5_K: (256, 176), GG_Q6_K: (256, 210)}
+# byte offsets of the f16 fields of each block type
+GG_F16 = {GG_Q8_0: (0,), GG_Q4_0: (0,), GG_Q4_K: (0, 2), GG_Q5_K: (0, 2), GG_Q6_K: (208,)}
+
+
+def gg_blocks(seed, dtype, nblk, finite=True):
+    """Random blocks of one GGUF type; with finite=True the f16 scale fields
+    hold finite halves in [2^-14, 2)*sign, so products stay finite."""
+    E, B = GG_BLOCK[dtype]
+    raw = rng(seed).integers(0, 256, size=(nblk, B), dtype=np.uint8)
+    if finite:
+        h = rng(seed + 1).integers(0x0400, 0x4000, size=(nblk, len(GG_F16[dtype])), dtype=np.uint16)
+        h |= (rng(seed + 2).integers(0, 2, size=h.shape, dtype=np.uint16) << 15)
+        for j, off in enumerate(GG_F16[dtype]):
+            raw[:, off] = (h[:, j] & 0xFF).astype(np.uint8)
+            raw[:, off + 1] = (h[:, j] >> 8).astype(np.uint8)
+    return np.ascontiguousarray(raw.reshape(-1))
+
+
+def o_gguf_dequant(dtype, raw, numel):
+    out = np.empty(numel, np.float32)
+    assert oracle().o_gguf_dequant(dtype, ptr(raw), numel, ptr(out)) == 0
+    return out
+
+
+def o_gguf_repack_q4_0(raw, O, I):
+    q4 = np.empty(O * I // 2, np.uint8)
+    qs = np.empty(O * I // 32, np.float32)
+    oracle().o_gguf_repack_q4_0(ptr(raw), ptr(q4), ptr(qs), O, I)
+    return q4, qs
+
+
+def ref_gguf_dequant(r, dtype, raw, numel):
+    out = np.empty(numel, np.float32)
+    r.ref_gguf_dequant(dtype, ptr(raw), numel, ptr(out))
+    return out
+
+
+def ref_gguf_repack_q4_0(r, raw, O, I):
+    q4 = np.empty(O * I // 2, np.uint8)
+    qs = np.empty(O * I // 32, np.float32)
+    r.ref_gguf_repack_q4_0(ptr(raw), ptr(q4), ptr(qs), O, I)
+    return q4, qs
