@@ -181,6 +181,67 @@ def bench_moe(c, cfg, T, E, K, I, D, norm, order, steps, warmup, bias=None, labe
     }
 
 
+def bench_moe_cached(c, steps):
+    """The C4 layer shape through the device expert cache (runtime/moecache.c
+    on HBM slots) in nn/moe.c's batch order: cap = 64 (every expert resident
+    after the first call: the cost over the uncached layer is the routing
+    read-back) and cap = 32 (half the experts stream from host memory each
+    call; bound by the host-to-device copies).  Eager calls: the cached layer
+    waits for its routing mid-call, so it is not graph-captured."""
+    import ctypes as C
+    import time
+    import numpy as np
+    import moty_amd
+    from moty_amd import LOAD_EXPERT_FN, MotyHipMoe, ORDER_EXPERT, lib
+    torch = c.torch
+    T, E, K, I, D = 256, 64, 8, 1024, 2048
+    G, GS, U, US, Dn, DS = (t.cpu().numpy() for t in moe_weights(c, 3, E, I, D))
+    host = {"g": G, "u": U, "d": Dn, "gs": GS, "us": US, "ds": DS}
+    ebytes = 3 * I * D + (2 * I + D) * 4
+
+    def load(ctx, layer, eid, slot, inter, hidden):
+        s = slot.contents
+        for k in host:
+            a = host[k][eid]
+            C.memmove(getattr(s, k), a.ctypes.data, a.nbytes)
+
+    fn = LOAD_EXPERT_FN(load)
+    Wr = c.randn((E, D), c.gen(3, 1), 0.02)
+    x = c.randn((T, D), c.gen(3, 2))
+    out = torch.empty((T, D), device="cuda:0")
+    m = MotyHipMoe()
+    m.router = C.c_void_p(Wr.data_ptr())
+    m.E, m.K, m.I, m.D = E, K, I, D
+    m.norm_topk, m.combine_order = 1, ORDER_EXPERT
+    st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    res = {}
+    for cap, n in ((64, max(10, steps // 16)), (32, 5)):
+        cache = C.c_void_p()
+        moty_amd.check(lib().moty_hip_expert_cache_init(C.byref(cache), cap, E), "cache init")
+
+        def call():
+            moty_amd.check(lib().moty_hip_moe_topk_cached_dev(C.byref(m), cache, None, 0, fn, C.c_void_p(x.data_ptr()),
+                                                              T, C.c_void_p(out.data_ptr()), st), "moe cached")
+        for _ in range(3):
+            call()
+        torch.cuda.synchronize()
+        miss0 = C.c_longlong()
+        lib().moty_hip_expert_cache_stats(cache, None, None, None, None, None, None, C.byref(miss0))
+        t0 = time.perf_counter()
+        for _ in range(n):
+            call()
+        torch.cuda.synchronize()
+        t = (time.perf_counter() - t0) / n
+        miss = C.c_longlong()
+        lib().moty_hip_expert_cache_stats(cache, None, None, None, None, None, None, C.byref(miss))
+        loads = (miss.value - miss0.value) / n
+        res["cap%d" % cap] = {"ms_per_layer": round(t * 1e3, 4), "tokens_per_s": round(T / t, 1),
+                              "loads_per_call": loads, "h2d_gbs": round(loads * ebytes / t / 1e9, 2)}
+        moty_amd.check(lib().moty_hip_expert_cache_free(cache), "cache free")
+    return {"workload": "C4 MoE layer shape through the device expert cache (batch order), T=256, E=64, top-8, "
+                        "cap=64 resident / cap=32 streaming from host memory", **res}
+
+
 def bench_c2(c, steps, warmup):
     """Qwen3-0.6B layer, the seven projections as Q8 prefill GEMMs, M=512.
     q, k, v, gate and up share their input, so their rows are stored
@@ -453,6 +514,8 @@ def main():
         extra.append(bench_c3(c, args.steps, args.warmup))
         log("C3 in Q4R4")
         extra.append(bench_c3_r4(c, args.steps, args.warmup))
+        log("C4 through the expert cache")
+        extra.append(bench_moe_cached(c, args.steps))
         log("GGUF loading")
         extra.append(bench_gguf(c, args.steps, args.warmup))
         log("C5")

@@ -102,6 +102,46 @@ typedef struct MotyHipMoe {
  * Host pointers; out [S][D].  Served for D, I multiples of 32, E <= 256, K <= 64. */
 int moty_hip_moe_topk(const MotyHipMoe *m, const float *x, int S, float *out);
 
+/* ---- expert residency (runtime/moe.h:35-102, runtime/moecache.c:4-95) ----
+ * The per-layer ExpertCache with its slots in device memory.  Bookkeeping
+ * is the reference's decision for decision (LFRU = heat << 8 | recency,
+ * io/tier.c:23-26; pins; hit/miss counters), so the same expert lands in
+ * the same slot.  A load calls the caller's loader on a host slot (pinned
+ * staging buffers owned by the cache), then copies it to the device slot. */
+typedef struct MotyHipExpertSlot { /* ExpertSlot (runtime/moe.h:35-39) */
+    int eid;
+    int8_t *g, *u, *d;     /* gate [inter][hidden], up [inter][hidden], down [hidden][inter] */
+    float *gs, *us, *ds;   /* row scales [inter], [inter], [hidden] */
+} MotyHipExpertSlot;
+/* LoadExpertFn (runtime/moe.h:54-56): fill s->g/u/d/gs/us/ds (host memory) */
+typedef void (*MotyHipLoadExpertFn)(void *ctx, int layer, int eid, MotyHipExpertSlot *s, int inter, int hidden);
+typedef struct MotyHipExpertCache MotyHipExpertCache;
+/* moty_expert_cache_init / _free (runtime/moecache.c:4-22): cap slots
+ * (cap < 1 -> 1), heat/pin tracking for n_experts (0 = none).  Device
+ * memory is taken on the first load, for that load's inter/hidden. */
+int moty_hip_expert_cache_init(MotyHipExpertCache **lc, int cap, int n_experts);
+int moty_hip_expert_cache_free(MotyHipExpertCache *lc);
+/* moty_expert_get / moty_expert_pin (runtime/moecache.c:24-89): *slot gets
+ * the expert's device slot (device pointers), loaded and ready on return.
+ * A slot evicted here must no longer be read by work the caller queued. */
+int moty_hip_expert_get(MotyHipExpertCache *lc, void *ctx, int layer, int eid, MotyHipLoadExpertFn fn, int inter,
+                        int hidden, MotyHipExpertSlot **slot);
+int moty_hip_expert_pin(MotyHipExpertCache *lc, void *ctx, int layer, int eid, MotyHipLoadExpertFn fn, int inter,
+                        int hidden, MotyHipExpertSlot **slot);
+/* the bookkeeping: filled slots, slot_eids [cap], heat/last [n_experts]
+ * (any pointer may be NULL) */
+int moty_hip_expert_cache_stats(const MotyHipExpertCache *lc, int *n, int *slot_eids, uint32_t *heat,
+                                uint32_t *last, uint32_t *clock, long long *hits, long long *misses);
+/* moty_moe_route_bias (runtime/moecache.c:91-95) on host logits [E] */
+void moty_hip_moe_route_bias(float *logits, const MotyHipExpertCache *lc, float bias);
+/* The MoE layer of moty_hip_moe_topk with the experts behind the cache
+ * (m->g/u/d/gs/us/ds unused): moe_batch_core's expert_get per active expert
+ * in ascending id (combine_order EXPERT, nn/moe.c:186-203) or olmoe's per
+ * token in top-k order (TOPK, engines/olmoe.c:230-233).  Output identical
+ * to the uncached layer; reads the routing back to the host once per call. */
+int moty_hip_moe_topk_cached(const MotyHipMoe *m, MotyHipExpertCache *lc, void *ctx, int layer,
+                             MotyHipLoadExpertFn fn, const float *x, int S, float *out);
+
 /* GGUF block types (io/st.h:74): the dtype argument of the GGUF calls */
 #define MOTY_GGUF_Q8_0 4
 #define MOTY_GGUF_Q4_0 5
@@ -210,6 +250,10 @@ int moty_hip_gguf_repack_q4_0_dev(const uint8_t *blocks, uint8_t *q4, float *qs,
                                   void *stream);
 /* the MoE layer, all pointers in m and x/out on the device */
 int moty_hip_moe_topk_dev(const MotyHipMoe *m, const float *x, int S, float *out, void *stream);
+/* the cached layer with m's router/bias/outputs and x/out on the device;
+ * synchronises `stream` once (the routing read-back) */
+int moty_hip_moe_topk_cached_dev(const MotyHipMoe *m, MotyHipExpertCache *lc, void *ctx, int layer,
+                                 MotyHipLoadExpertFn fn, const float *x, int S, float *out, void *stream);
 
 #ifdef __cplusplus
 }

@@ -28,6 +28,14 @@ class MotyHipMoe(C.Structure):
     ]
 
 
+class MotyHipExpertSlot(C.Structure):
+    _fields_ = [("eid", I32), ("g", P), ("u", P), ("d", P), ("gs", P), ("us", P), ("ds", P)]
+
+
+# MotyHipLoadExpertFn(ctx, layer, eid, slot, inter, hidden)
+LOAD_EXPERT_FN = C.CFUNCTYPE(None, P, I32, I32, C.POINTER(MotyHipExpertSlot), I32, I32)
+
+
 # name -> (restype, argtypes): every symbol include/moty_hw_hip.h declares
 SIGNATURES = {
     "moty_hip_init": (I32, [I32]),
@@ -51,6 +59,14 @@ SIGNATURES = {
     "moty_hip_gguf_repack_q4_0": (I32, [P, P, P, I64, I64]),
     "moty_hip_gguf_dequant_dev": (I32, [I32, P, I64, P, P]),
     "moty_hip_gguf_repack_q4_0_dev": (I32, [P, P, P, I64, I64, P]),
+    "moty_hip_expert_cache_init": (I32, [C.POINTER(P), I32, I32]),
+    "moty_hip_expert_cache_free": (I32, [P]),
+    "moty_hip_expert_get": (I32, [P, P, I32, I32, LOAD_EXPERT_FN, I32, I32, C.POINTER(C.POINTER(MotyHipExpertSlot))]),
+    "moty_hip_expert_pin": (I32, [P, P, I32, I32, LOAD_EXPERT_FN, I32, I32, C.POINTER(C.POINTER(MotyHipExpertSlot))]),
+    "moty_hip_expert_cache_stats": (I32, [P, P, P, P, P, P, P, P]),
+    "moty_hip_moe_route_bias": (None, [P, P, C.c_float]),
+    "moty_hip_moe_topk_cached": (I32, [C.POINTER(MotyHipMoe), P, P, I32, LOAD_EXPERT_FN, P, I32, P]),
+    "moty_hip_moe_topk_cached_dev": (I32, [C.POINTER(MotyHipMoe), P, P, I32, LOAD_EXPERT_FN, P, I32, P, P]),
     "moty_hip_matmul": (I32, [P, P, P, I32, I32, I32]),
     "moty_hip_moe_topk": (I32, [C.POINTER(MotyHipMoe), P, I32, P]),
     "moty_hip_weight_forget": (I32, [P]),

@@ -16,8 +16,8 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmoty_hw_hip.so")
-SOURCES = ["quant.hip", "gemv_q8.hip", "gemm_q8.hip", "q4g.hip", "r4.hip", "moe.hip", "ops.hip", "gguf.hip", "api.cpp"]
-HEADERS = ["common.h", "kernels.h"]
+SOURCES = ["quant.hip", "gemv_q8.hip", "gemm_q8.hip", "q4g.hip", "r4.hip", "moe.hip", "ops.hip", "gguf.hip", "api.cpp", "expert_cache.cpp"]
+HEADERS = ["common.h", "kernels.h", "dev.h"]
 
 
 def hipcc():

@@ -15,6 +15,7 @@
 
 #include "../../include/moty_hw_hip.h"
 #include "common.h"
+#include "dev.h"
 #include "kernels.h"
 
 namespace moty {
@@ -32,24 +33,6 @@ int check_hip(hipError_t e, const char* what) {
   set_error("%s: %s", what, hipGetErrorString(e));
   return e == hipErrorOutOfMemory ? MOTY_ENOMEM : MOTY_EHIP;
 }
-
-struct WEntry {
-  void* dev;
-  size_t bytes;
-};
-
-struct Arena {
-  void* p = nullptr;
-  size_t cap = 0;
-};
-
-struct Dev {
-  bool ready = false;
-  int cus = 0;  // compute units
-  hipStream_t stream = nullptr;
-  Arena scratch, io;
-  std::unordered_map<const void*, WEntry> wcache;
-};
 
 constexpr int MAX_DEV = 16;
 static Dev g_dev[MAX_DEV];
@@ -76,7 +59,7 @@ static int dev_init(int d) {
   return MOTY_OK;
 }
 
-static int cur(Dev** out) {
+int cur(Dev** out) {
   if (t_dev < 0) {
     int rc = dev_init(0);
     if (rc) return rc;
@@ -89,7 +72,7 @@ static int cur(Dev** out) {
 
 // Grow an arena to at least `bytes`.  Waits for queued work that may still
 // read the old buffer before releasing it.
-static int arena_get(Arena& a, size_t bytes, void** p) {
+int arena_get(Arena& a, size_t bytes, void** p) {
   if (bytes == 0) bytes = 256;
   if (a.cap < bytes) {
     if (a.p) {
@@ -111,7 +94,6 @@ static int arena_get(Arena& a, size_t bytes, void** p) {
   return MOTY_OK;
 }
 
-static inline size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 // Device copy of a persistent host weight buffer.
 static int weight(Dev* d, const void* host, size_t bytes, const void** dev) {
@@ -144,17 +126,27 @@ static int env_int(const char* name, int dflt) {
   return e ? atoi(e) : dflt;
 }
 
+// Stage host x into the transfer arena; returns device x and y pointers.
+int stage_io(Dev* d, const void* x, size_t xbytes, size_t ybytes, void** dx, void** dy) {
+  void* p;
+  int rc = arena_get(d->io, al256(xbytes) + al256(ybytes), &p);
+  if (rc) return rc;
+  *dx = p;
+  *dy = (char*)p + al256(xbytes);
+  HIP_TRY(hipMemcpyAsync(*dx, x, xbytes, hipMemcpyHostToDevice, d->stream));
+  return MOTY_OK;
+}
+
+int finish_io(Dev* d, void* y, const void* dy, size_t ybytes) {
+  HIP_TRY(hipMemcpyAsync(y, dy, ybytes, hipMemcpyDeviceToHost, d->stream));
+  HIP_TRY(hipStreamSynchronize(d->stream));
+  return MOTY_OK;
+}
+
 }  // namespace moty
 
 using namespace moty;
 
-#define CUR(d)          \
-  Dev* d = nullptr;     \
-  {                     \
-    int _rc = cur(&d);  \
-    if (_rc) return _rc; \
-  }
-#define STREAM(s) ((hipStream_t)(s))
 
 extern "C" {
 
@@ -389,22 +381,6 @@ int moty_hip_moe_topk_dev(const MotyHipMoe* m, const float* x, int S, float* out
 
 // ---------------- host-pointer drop-ins ----------------
 
-// Stage host x into the transfer arena; returns device x and y pointers.
-static int stage_io(Dev* d, const void* x, size_t xbytes, size_t ybytes, void** dx, void** dy) {
-  void* p;
-  int rc = arena_get(d->io, al256(xbytes) + al256(ybytes), &p);
-  if (rc) return rc;
-  *dx = p;
-  *dy = (char*)p + al256(xbytes);
-  HIP_TRY(hipMemcpyAsync(*dx, x, xbytes, hipMemcpyHostToDevice, d->stream));
-  return MOTY_OK;
-}
-
-static int finish_io(Dev* d, void* y, const void* dy, size_t ybytes) {
-  HIP_TRY(hipMemcpyAsync(y, dy, ybytes, hipMemcpyDeviceToHost, d->stream));
-  HIP_TRY(hipStreamSynchronize(d->stream));
-  return MOTY_OK;
-}
 
 int moty_hip_matmul_q_s(float* y, const float* x, const int8_t* q, const float* scale, int S, int I, int O) {
   CUR(d);
@@ -672,7 +648,11 @@ int moty_hip_matmul(float* y, const float* x, const float* W, int S, int I, int 
   return finish_io(d, y, dy, (size_t)S * O * 4);
 }
 
-int moty_hip_moe_topk(const MotyHipMoe* m, const float* x, int S, float* out) {
+// Host-pointer MoE layer: router, bias and (uncached) the stacked experts go
+// to the device through the weight cache; with an expert cache the experts
+// come from its loader instead.
+static int moe_host(const MotyHipMoe* m, MotyHipExpertCache* c, void* ctx, int layer, MotyHipLoadExpertFn fn,
+                    const float* x, int S, float* out) {
   CUR(d);
   if (!m || !x || !out || S < 0 || m->E <= 0 || m->K <= 0 || m->I <= 0 || m->D <= 0)
     return set_error("moe_topk: bad arguments"), MOTY_EINVAL;
@@ -688,18 +668,20 @@ int moty_hip_moe_topk(const MotyHipMoe* m, const float* x, int S, float* out) {
     if ((rc = weight(d, m->logit_bias, (size_t)E * 4, &p))) return rc;
     dm.logit_bias = (const float*)p;
   }
-  if ((rc = weight(d, m->g, ne, &p))) return rc;
-  dm.g = (const int8_t*)p;
-  if ((rc = weight(d, m->u, ne, &p))) return rc;
-  dm.u = (const int8_t*)p;
-  if ((rc = weight(d, m->d, ne, &p))) return rc;
-  dm.d = (const int8_t*)p;
-  if ((rc = weight(d, m->gs, (size_t)E * I * 4, &p))) return rc;
-  dm.gs = (const float*)p;
-  if ((rc = weight(d, m->us, (size_t)E * I * 4, &p))) return rc;
-  dm.us = (const float*)p;
-  if ((rc = weight(d, m->ds, (size_t)E * D * 4, &p))) return rc;
-  dm.ds = (const float*)p;
+  if (!c) {
+    if ((rc = weight(d, m->g, ne, &p))) return rc;
+    dm.g = (const int8_t*)p;
+    if ((rc = weight(d, m->u, ne, &p))) return rc;
+    dm.u = (const int8_t*)p;
+    if ((rc = weight(d, m->d, ne, &p))) return rc;
+    dm.d = (const int8_t*)p;
+    if ((rc = weight(d, m->gs, (size_t)E * I * 4, &p))) return rc;
+    dm.gs = (const float*)p;
+    if ((rc = weight(d, m->us, (size_t)E * I * 4, &p))) return rc;
+    dm.us = (const float*)p;
+    if ((rc = weight(d, m->ds, (size_t)E * D * 4, &p))) return rc;
+    dm.ds = (const float*)p;
+  }
   // outputs: out, then optional idx/w/counts after it in the transfer arena
   const size_t b_out = al256((size_t)S * D * 4), b_kw = al256((size_t)S * K * 4), b_c = al256((size_t)E * 4);
   void *dx, *dy;
@@ -708,12 +690,24 @@ int moty_hip_moe_topk(const MotyHipMoe* m, const float* x, int S, float* out) {
   dm.idx_out = m->idx_out ? (int32_t*)extra : nullptr;
   dm.w_out = m->w_out ? (float*)(extra + b_kw) : nullptr;
   dm.counts_out = m->counts_out ? (int32_t*)(extra + 2 * b_kw) : nullptr;
-  if ((rc = moty_hip_moe_topk_dev(&dm, (const float*)dx, S, (float*)dy, d->stream))) return rc;
+  rc = c ? moty_hip_moe_topk_cached_dev(&dm, c, ctx, layer, fn, (const float*)dx, S, (float*)dy, d->stream)
+         : moty_hip_moe_topk_dev(&dm, (const float*)dx, S, (float*)dy, d->stream);
+  if (rc) return rc;
   if (m->idx_out) HIP_TRY(hipMemcpyAsync(m->idx_out, dm.idx_out, (size_t)S * K * 4, hipMemcpyDeviceToHost, d->stream));
   if (m->w_out) HIP_TRY(hipMemcpyAsync(m->w_out, dm.w_out, (size_t)S * K * 4, hipMemcpyDeviceToHost, d->stream));
   if (m->counts_out)
     HIP_TRY(hipMemcpyAsync(m->counts_out, dm.counts_out, (size_t)E * 4, hipMemcpyDeviceToHost, d->stream));
   return finish_io(d, out, dy, (size_t)S * D * 4);
+}
+
+int moty_hip_moe_topk(const MotyHipMoe* m, const float* x, int S, float* out) {
+  return moe_host(m, nullptr, nullptr, 0, nullptr, x, S, out);
+}
+
+int moty_hip_moe_topk_cached(const MotyHipMoe* m, MotyHipExpertCache* c, void* ctx, int layer,
+                             MotyHipLoadExpertFn fn, const float* x, int S, float* out) {
+  if (!c || !fn) return set_error("moe_topk_cached: bad arguments"), MOTY_EINVAL;
+  return moe_host(m, c, ctx, layer, fn, x, S, out);
 }
 
 int moty_hip_weight_forget(const void* host_ptr) {

@@ -1,0 +1,49 @@
+// dev.h -- per-device state of libmoty-hw-hip shared by the C-ABI files
+// (api.cpp, expert_cache.cpp): the library stream, the growable scratch and
+// transfer arenas, and the weight cache keyed by host pointer.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+#include <unordered_map>
+
+namespace moty {
+
+struct WEntry {
+  void* dev;
+  size_t bytes;
+};
+
+struct Arena {
+  void* p = nullptr;
+  size_t cap = 0;
+};
+
+struct Dev {
+  bool ready = false;
+  int cus = 0;  // compute units
+  hipStream_t stream = nullptr;
+  Arena scratch, io;
+  std::unordered_map<const void*, WEntry> wcache;
+};
+
+// The calling thread's device (device 0 on first use), made current.
+int cur(Dev** out);
+// Grow an arena to at least `bytes`; waits for queued work before freeing.
+int arena_get(Arena& a, size_t bytes, void** p);
+// Stage host x into the transfer arena (device x and y returned), and copy
+// y back and synchronise.
+int stage_io(Dev* d, const void* x, size_t xbytes, size_t ybytes, void** dx, void** dy);
+int finish_io(Dev* d, void* y, const void* dy, size_t ybytes);
+
+inline size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+}  // namespace moty
+
+#define CUR(d)           \
+  moty::Dev* d = nullptr; \
+  {                      \
+    int _rc = moty::cur(&d); \
+    if (_rc) return _rc; \
+  }
+#define STREAM(s) ((hipStream_t)(s))

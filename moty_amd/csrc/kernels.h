@@ -69,5 +69,13 @@ struct MoeArgs {
 };
 size_t moe_scratch_size(int T, int D, int E, int K, int I, size_t* offsets);
 int launch_moe(const MoeArgs& a, void* scratch, hipStream_t st);
+// The layer in three phases, for callers that act between them (the expert
+// cache): router + top-k + grouping; the expert GEMMs (eslot: expert ->
+// weight slot in a.G/U/Dn and their scales, -1 = skip; null = identity);
+// the combine.  moe_routing gives the device idx [T*K] and counts [E].
+int launch_moe_route(const MoeArgs& a, void* scratch, hipStream_t st);
+int launch_moe_experts(const MoeArgs& a, void* scratch, const int* eslot, hipStream_t st);
+int launch_moe_combine(const MoeArgs& a, void* scratch, hipStream_t st);
+void moe_routing(const MoeArgs& a, void* scratch, const int** idx, const int** counts);
 
 }  // namespace moty

@@ -443,7 +443,7 @@ __global__ __launch_bounds__(MOTY_WAVE * MT * NW) void k_moe_gemm(
     const int8_t* __restrict__ W1, const float* __restrict__ S1,      // [E][N][K], [E][N]
     const int8_t* __restrict__ W2, const float* __restrict__ S2,      // up (GATEUP only)
     float* __restrict__ out,                                          // [P][N]
-    int N, int Kd) {
+    int N, int Kd, const int* __restrict__ eslot) {                  // expert -> weight slot, or null
   constexpr int NTH = MOTY_WAVE * MT * NW;  // MT groups of NW waves, one group per 64-slot sub-tile
   constexpr int BM = 64 * MT;               // slots per M-tile
   constexpr int BN = 32 * NW;               // weight rows per N-tile (32 per wave)
@@ -457,6 +457,10 @@ __global__ __launch_bounds__(MOTY_WAVE * MT * NW) void k_moe_gemm(
   if (tile >= ntiles[0]) return;
   const int2 tm = tiles[tile];
   const int e = tm.x, mb = tm.y;
+  // weight slot of the expert: itself, or its expert-cache slot (-1: not in
+  // this pass, the workgroup has nothing to do)
+  const int ws = eslot ? eslot[e] : e;
+  if (ws < 0) return;
   const int seg0 = offs[e], nseg = offs[e + 1] - seg0;
   const int tid = threadIdx.x, lane = tid % MOTY_WAVE, wv = tid / MOTY_WAVE;
   const int sub = wv / NW, wn = wv % NW;  // this wave: sub-tile, 32-row N slice
@@ -478,8 +482,8 @@ __global__ __launch_bounds__(MOTY_WAVE * MT * NW) void k_moe_gemm(
   }
   const int ncol = nb0 + wn * 32 + r32;
   const int ncl = ncol < N ? ncol : N - 1;
-  const float s1 = S1[(int64_t)e * N + ncl];
-  const float s2 = GATEUP ? S2[(int64_t)e * N + ncl] : 0.f;
+  const float s1 = S1[(int64_t)ws * N + ncl];
+  const float s2 = GATEUP ? S2[(int64_t)ws * N + ncl] : 0.f;
   // this thread's copy assignments: chunk q -> (row q/8, 16 B column q%8)
   const int8_t* srcA[NA];
   const int8_t* srcB[NBW];
@@ -499,7 +503,7 @@ __global__ __launch_bounds__(MOTY_WAVE * MT * NW) void k_moe_gemm(
     const int8_t* W = (GATEUP && row >= BN) ? W2 : W1;
     int n = nb0 + (GATEUP && row >= BN ? row - BN : row);
     n = n < N ? n : N - 1;
-    srcB[i] = W + ((int64_t)e * N + n) * Kd + col;
+    srcB[i] = W + ((int64_t)ws * N + n) * Kd + col;
   }
   // Two register sets: while one K block is consumed from LDS, the next two
   // are in flight from HBM.  Every load is unconditional, from a clamped
@@ -653,31 +657,52 @@ size_t moe_scratch_size(int T, int D, int E, int K, int I, size_t* offsets) {
   return o;
 }
 
-int launch_moe(const MoeArgs& a, void* scratch, hipStream_t st) {
-  const int T = a.T, D = a.D, E = a.E, K = a.K, I = a.I;
-  if (T <= 0) return MOTY_OK;
-  if (K < 1 || K > 64 || K > E || E > 4096 || (D % 32) || (I % 32) || (D % 4)) return MOTY_EUNSUP;
-  size_t off[MOE_NBUF];
-  moe_scratch_size(T, D, E, K, I, off);
-  char* b = (char*)scratch;
-  int8_t* xq = (int8_t*)(b + off[0]);
-  float* sx = (float*)(b + off[1]);
-  int* idx = (int*)(b + off[2]);
-  float* w = (float*)(b + off[3]);
-  int* offs = (int*)(b + off[4]);
-  int* slot_tok = (int*)(b + off[5]);
-  int* pair_slot = (int*)(b + off[6]);
-  int2* tiles = (int2*)(b + off[7]);
-  int* ntiles = (int*)(b + off[8]);
-  float* h = (float*)(b + off[9]);
-  int8_t* hq = (int8_t*)(b + off[10]);
-  float* sh = (float*)(b + off[11]);
-  float* y = (float*)(b + off[12]);
-  int* counts = (int*)(b + off[13]);
-  const int P = T * K;
+struct MoeBufs {
+  int8_t* xq;
+  float *sx, *w, *h, *sh, *y, *logits;
+  int *idx, *offs, *slot_tok, *pair_slot, *ntiles, *counts;
+  int2* tiles;
+  int8_t* hq;
+};
 
-  if (E > 64 * TK_PV) return MOTY_EUNSUP;
-  float* logits = (float*)(b + off[14]);
+static MoeBufs moe_bufs(const MoeArgs& a, void* scratch) {
+  size_t off[MOE_NBUF];
+  moe_scratch_size(a.T, a.D, a.E, a.K, a.I, off);
+  char* b = (char*)scratch;
+  MoeBufs m;
+  m.xq = (int8_t*)(b + off[0]);
+  m.sx = (float*)(b + off[1]);
+  m.idx = (int*)(b + off[2]);
+  m.w = (float*)(b + off[3]);
+  m.offs = (int*)(b + off[4]);
+  m.slot_tok = (int*)(b + off[5]);
+  m.pair_slot = (int*)(b + off[6]);
+  m.tiles = (int2*)(b + off[7]);
+  m.ntiles = (int*)(b + off[8]);
+  m.h = (float*)(b + off[9]);
+  m.hq = (int8_t*)(b + off[10]);
+  m.sh = (float*)(b + off[11]);
+  m.y = (float*)(b + off[12]);
+  m.counts = (int*)(b + off[13]);
+  m.logits = (float*)(b + off[14]);
+  return m;
+}
+
+// 128-slot M-tiles when experts average more than 48 slots (one pass over
+// an expert's weights for up to 128 slots), 64-slot tiles otherwise
+static int moe_mt(const MoeArgs& a) { return ((int64_t)a.T * a.K > 48 * (int64_t)a.E) ? 2 : 1; }
+
+void moe_routing(const MoeArgs& a, void* scratch, const int** idx, const int** counts) {
+  const MoeBufs m = moe_bufs(a, scratch);
+  *idx = m.idx;
+  *counts = m.counts;
+}
+
+int launch_moe_route(const MoeArgs& a, void* scratch, hipStream_t st) {
+  const int T = a.T, D = a.D, E = a.E, K = a.K, I = a.I;
+  if (K < 1 || K > 64 || K > E || E > 64 * TK_PV || (D % 32) || (I % 32) || (D % 4)) return MOTY_EUNSUP;
+  const MoeBufs m = moe_bufs(a, scratch);
+  const int P = T * K;
   // 4-token tiles while that leaves at most ~2 workgroups per CU (the
   // router is latency-bound at small T), 16-token tiles beyond (fewer router
   // re-reads); measured on MI355X: T=256, E=64: 8.0 us vs 10.5 (8-token);
@@ -685,44 +710,63 @@ int launch_moe(const MoeArgs& a, void* scratch, hipStream_t st) {
   const int eblk = (E + RG_TE - 1) / RG_TE;
   auto rgrid = [&](int tt) { return dim3((unsigned)(((T + tt - 1) / tt + 7) / 8 * 8 * eblk)); };
   if ((int64_t)((T + 3) / 4) * eblk <= 512)
-    hipLaunchKernelGGL(k_router_logits<1>, rgrid(4), dim3(RG_NT), 0, st, a.x, a.Wr, a.bias, T, D, E, logits);
+    hipLaunchKernelGGL(k_router_logits<1>, rgrid(4), dim3(RG_NT), 0, st, a.x, a.Wr, a.bias, T, D, E, m.logits);
   else
-    hipLaunchKernelGGL(k_router_logits<4>, rgrid(16), dim3(RG_NT), 0, st, a.x, a.Wr, a.bias, T, D, E, logits);
+    hipLaunchKernelGGL(k_router_logits<4>, rgrid(16), dim3(RG_NT), 0, st, a.x, a.Wr, a.bias, T, D, E, m.logits);
   LAUNCH_TRY("k_router_logits");
   hipLaunchKernelGGL(k_route_topk, dim3((T + TK_NT / 128 - 1) / (TK_NT / 128)), dim3(TK_NT),
-                     (size_t)(TK_NT / 128) * E * 4, st, a.x, logits, T, D, E, K, a.norm, idx, w, xq, sx,
+                     (size_t)(TK_NT / 128) * E * 4, st, a.x, m.logits, T, D, E, K, a.norm, m.idx, m.w, m.xq, m.sx,
                      a.probs_out);
   LAUNCH_TRY("k_route_topk");
-  // 128-slot M-tiles when experts average more than 48 slots (one pass over
-  // an expert's weights for up to 128 slots), 64-slot tiles otherwise
-  const int mt = (P > 48 * E) ? 2 : 1;
-  hipLaunchKernelGGL(k_group, dim3(1), dim3(GR_NT), (size_t)(3 * E + 1) * 4, st, idx, P, K, E, 64 * mt, offs,
-                     slot_tok, pair_slot, tiles, ntiles, counts);
+  const int mt = moe_mt(a);
+  hipLaunchKernelGGL(k_group, dim3(1), dim3(GR_NT), (size_t)(3 * E + 1) * 4, st, m.idx, P, K, E, 64 * mt, m.offs,
+                     m.slot_tok, m.pair_slot, m.tiles, m.ntiles, m.counts);
   LAUNCH_TRY("k_group");
+  return MOTY_OK;
+}
+
+int launch_moe_experts(const MoeArgs& a, void* scratch, const int* eslot, hipStream_t st) {
+  const int D = a.D, E = a.E, I = a.I;
+  const MoeBufs m = moe_bufs(a, scratch);
+  const int P = a.T * a.K, mt = moe_mt(a);
   const int maxt = P / (64 * mt) + E + 1;
   if (mt == 2)
-    hipLaunchKernelGGL((k_moe_gemm<true, 2, 4>), dim3((I + 127) / 128, maxt), dim3(512), 0, st, tiles, ntiles, offs,
-                       slot_tok, xq, sx, a.G, a.GS, a.U, a.US, h, I, D);
+    hipLaunchKernelGGL((k_moe_gemm<true, 2, 4>), dim3((I + 127) / 128, maxt), dim3(512), 0, st, m.tiles, m.ntiles,
+                       m.offs, m.slot_tok, m.xq, m.sx, a.G, a.GS, a.U, a.US, m.h, I, D, eslot);
   else
-    hipLaunchKernelGGL((k_moe_gemm<true, 1, 4>), dim3((I + 127) / 128, maxt), dim3(256), 0, st, tiles, ntiles, offs,
-                       slot_tok, xq, sx, a.G, a.GS, a.U, a.US, h, I, D);
+    hipLaunchKernelGGL((k_moe_gemm<true, 1, 4>), dim3((I + 127) / 128, maxt), dim3(256), 0, st, m.tiles, m.ntiles,
+                       m.offs, m.slot_tok, m.xq, m.sx, a.G, a.GS, a.U, a.US, m.h, I, D, eslot);
   LAUNCH_TRY("k_moe_gemm<gateup>");
-  int rc = launch_qrow_i8(h, hq, sh, nullptr, P, I, I, I, st);
+  int rc = launch_qrow_i8(m.h, m.hq, m.sh, nullptr, P, I, I, I, st);
   if (rc) return rc;
   if (mt == 2)
-    hipLaunchKernelGGL((k_moe_gemm<false, 2, 4>), dim3((D + 127) / 128, maxt), dim3(512), 0, st, tiles, ntiles, offs,
-                       slot_tok, hq, sh, a.Dn, a.DS, nullptr, nullptr, y, D, I);
+    hipLaunchKernelGGL((k_moe_gemm<false, 2, 4>), dim3((D + 127) / 128, maxt), dim3(512), 0, st, m.tiles, m.ntiles,
+                       m.offs, m.slot_tok, m.hq, m.sh, a.Dn, a.DS, nullptr, nullptr, m.y, D, I, eslot);
   else
-    hipLaunchKernelGGL((k_moe_gemm<false, 1, 4>), dim3((D + 127) / 128, maxt), dim3(256), 0, st, tiles, ntiles, offs,
-                       slot_tok, hq, sh, a.Dn, a.DS, nullptr, nullptr, y, D, I);
+    hipLaunchKernelGGL((k_moe_gemm<false, 1, 4>), dim3((D + 127) / 128, maxt), dim3(256), 0, st, m.tiles, m.ntiles,
+                       m.offs, m.slot_tok, m.hq, m.sh, a.Dn, a.DS, nullptr, nullptr, m.y, D, I, eslot);
   LAUNCH_TRY("k_moe_gemm<down>");
-  hipLaunchKernelGGL(k_moe_combine, dim3(T, (D / 4 + 255) / 256), dim3(256), 0, st, y, idx, w, pair_slot, a.out, D,
-                     K, a.order);
-  LAUNCH_TRY("k_moe_combine");
-  if (a.idx_out) HIP_TRY(hipMemcpyAsync(a.idx_out, idx, (size_t)P * 4, hipMemcpyDeviceToDevice, st));
-  if (a.w_out) HIP_TRY(hipMemcpyAsync(a.w_out, w, (size_t)P * 4, hipMemcpyDeviceToDevice, st));
-  if (a.counts_out) HIP_TRY(hipMemcpyAsync(a.counts_out, counts, (size_t)E * 4, hipMemcpyDeviceToDevice, st));
   return MOTY_OK;
+}
+
+int launch_moe_combine(const MoeArgs& a, void* scratch, hipStream_t st) {
+  const int T = a.T, D = a.D, K = a.K, P = a.T * a.K;
+  const MoeBufs m = moe_bufs(a, scratch);
+  hipLaunchKernelGGL(k_moe_combine, dim3(T, (D / 4 + 255) / 256), dim3(256), 0, st, m.y, m.idx, m.w, m.pair_slot,
+                     a.out, D, K, a.order);
+  LAUNCH_TRY("k_moe_combine");
+  if (a.idx_out) HIP_TRY(hipMemcpyAsync(a.idx_out, m.idx, (size_t)P * 4, hipMemcpyDeviceToDevice, st));
+  if (a.w_out) HIP_TRY(hipMemcpyAsync(a.w_out, m.w, (size_t)P * 4, hipMemcpyDeviceToDevice, st));
+  if (a.counts_out) HIP_TRY(hipMemcpyAsync(a.counts_out, m.counts, (size_t)a.E * 4, hipMemcpyDeviceToDevice, st));
+  return MOTY_OK;
+}
+
+int launch_moe(const MoeArgs& a, void* scratch, hipStream_t st) {
+  if (a.T <= 0) return MOTY_OK;
+  int rc = launch_moe_route(a, scratch, st);
+  if (!rc) rc = launch_moe_experts(a, scratch, nullptr, st);
+  if (!rc) rc = launch_moe_combine(a, scratch, st);
+  return rc;
 }
 
 }  // namespace moty

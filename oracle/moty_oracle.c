@@ -762,3 +762,113 @@ O_EXPORT int o_gguf_dequant(int dtype, const uint8_t *raw, int64_t numel, float 
     }
     return 0;
 }
+
+/* ------------------------------------------------------------------ */
+/* Expert cache bookkeeping (runtime/moecache.c:4-89, io/tier.c:23-26). */
+/* Slots, LFRU heat/recency, pins, hit/miss counters; the weights are   */
+/* not modelled (a load is reported to the caller instead).            */
+typedef struct {
+    int cap, n, n_experts;
+    uint32_t clock;
+    long long hits, misses;
+    int *eid;            /* [cap] */
+    uint32_t *heat, *last;
+    uint8_t *pinned;
+} OCache;
+
+O_EXPORT void *o_ecache_new(int cap, int n_experts) {
+    OCache *c = calloc(1, sizeof *c);
+    if (cap < 1) cap = 1;
+    c->cap = cap;
+    c->n_experts = n_experts;
+    c->eid = malloc(sizeof(int) * cap);
+    for (int i = 0; i < cap; i++) c->eid[i] = -1;
+    if (n_experts > 0) {
+        c->heat = calloc(n_experts, 4);
+        c->last = calloc(n_experts, 4);
+        c->pinned = calloc(n_experts, 1);
+    }
+    return c;
+}
+
+O_EXPORT void o_ecache_free(void *p) {
+    OCache *c = p;
+    free(c->eid); free(c->heat); free(c->last); free(c->pinned); free(c);
+}
+
+/* frequency in the high bits, recency (255 - age, floored at 0) in the low 8 */
+static uint64_t o_lfru(uint32_t heat, uint32_t last, uint32_t clock) {
+    uint32_t age = clock - last;
+    return ((uint64_t)heat << 8) | (age < 255 ? 255 - age : 0);
+}
+
+static int o_is_pinned(const OCache *c, int e) {
+    return c->pinned && e >= 0 && e < c->n_experts && c->pinned[e];
+}
+
+/* moty_expert_get: returns the slot; *loaded = 1 on a miss (the slot is
+ * refilled with eid).  Victim on a full cache: the unpinned resident of
+ * least score (first on ties; slot 0 if every resident is pinned); without
+ * heat tracking (n_experts == 0) slot 1, the reference's LRU-by-fill stand-in. */
+O_EXPORT int o_ecache_get(void *p, int eid, int *loaded) {
+    OCache *c = p;
+    if (c->heat && eid >= 0 && eid < c->n_experts) {
+        if (c->heat[eid] < 0xFFFFFFFFu) c->heat[eid]++;
+        c->last[eid] = c->clock++;
+    }
+    for (int i = 0; i < c->n; i++)
+        if (c->eid[i] == eid) { c->hits++; *loaded = 0; return i; }
+    c->misses++;
+    int v;
+    if (c->n < c->cap) v = c->n++;
+    else {
+        v = 0;
+        if (c->heat) {
+            uint64_t worst = UINT64_MAX;
+            for (int i = 0; i < c->n; i++) {
+                int e = c->eid[i];
+                if (o_is_pinned(c, e)) continue;
+                uint64_t s = o_lfru(c->heat[e], c->last[e], c->clock);
+                if (s < worst) { worst = s; v = i; }
+            }
+        } else {
+            for (int i = 1; i < c->n; i++) if (!o_is_pinned(c, c->eid[i])) { v = i; break; }
+        }
+    }
+    c->eid[v] = eid;
+    *loaded = 1;
+    return v;
+}
+
+/* moty_expert_pin: mark pinned, then always load into a fresh slot, or the
+ * first unpinned resident's, or slot 0 */
+O_EXPORT int o_ecache_pin(void *p, int eid) {
+    OCache *c = p;
+    if (c->pinned && eid >= 0 && eid < c->n_experts) c->pinned[eid] = 1;
+    int v;
+    if (c->n < c->cap) v = c->n++;
+    else {
+        v = -1;
+        for (int i = 0; i < c->n; i++) if (!o_is_pinned(c, c->eid[i])) { v = i; break; }
+        if (v < 0) v = 0;
+    }
+    c->eid[v] = eid;
+    return v;
+}
+
+O_EXPORT void o_ecache_state(void *p, int *n, int *eids, uint32_t *heat, uint32_t *last, uint32_t *clock,
+                             long long *hits, long long *misses) {
+    OCache *c = p;
+    *n = c->n;
+    memcpy(eids, c->eid, sizeof(int) * c->cap);
+    if (c->heat) { memcpy(heat, c->heat, 4 * c->n_experts); memcpy(last, c->last, 4 * c->n_experts); }
+    *clock = c->clock; *hits = c->hits; *misses = c->misses;
+}
+
+/* moty_moe_route_bias (runtime/moecache.c:91-95): logits of every filled
+ * slot's expert += bias, once per slot */
+O_EXPORT void o_ecache_route_bias(void *p, float *logits, float bias) {
+    OCache *c = p;
+    if (bias <= 0) return;
+    for (int i = 0; i < c->n; i++) if (c->eid[i] >= 0) logits[c->eid[i]] += bias;
+}

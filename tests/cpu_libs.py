@@ -62,6 +62,12 @@ _SIGS = {
     "o_gguf_dequant": (I32, [I32, P, I64, P]),
     "ref_gguf_repack_q4_0": (None, [P, P, P, I64, I64]),
     "ref_gguf_dequant": (None, [I32, P, I64, P]),
+    "o_ecache_new": (P, [I32, I32]),
+    "o_ecache_free": (None, [P]),
+    "o_ecache_get": (I32, [P, I32, P]),
+    "o_ecache_pin": (I32, [P, I32]),
+    "o_ecache_state": (None, [P, P, P, P, P, P, P, P]),
+    "o_ecache_route_bias": (None, [P, P, F32]),
     # the reference's own R4 symbols (nn/quant.c, hw/hw_q4r4.h, nn/matmul.c)
     "moty_hw_f16_to_f32": (F32, [C.c_uint16]),
     "moty_f32_to_f16": (C.c_uint16, [F32]),
@@ -357,3 +363,116 @@ def ref_gguf_repack_q4_0(r, raw, O, I):
     qs = np.empty(O * I // 32, np.float32)
     r.ref_gguf_repack_q4_0(ptr(raw), ptr(q4), ptr(qs), O, I)
     return q4, qs
+
+
+# ---- expert cache bookkeeping (runtime/moecache.c) ----
+class OCacheState:
+    def __init__(self, n, eids, heat, last, clock, hits, misses):
+        self.n, self.eids, self.heat, self.last = n, eids, heat, last
+        self.clock, self.hits, self.misses = clock, hits, misses
+
+    def key(self):
+        return (self.n, tuple(self.eids[:self.n]), tuple(self.heat), tuple(self.last), self.clock, self.hits,
+                self.misses)
+
+
+class OCache:
+    """The oracle's restatement of ExpertCache; get/pin return (slot, loaded)."""
+
+    def __init__(self, cap, n_experts):
+        self.cap, self.E = max(cap, 1), n_experts
+        self.p = oracle().o_ecache_new(cap, n_experts)
+
+    def __del__(self):
+        if getattr(self, "p", None):
+            oracle().o_ecache_free(self.p)
+
+    def get(self, eid):
+        ld = C.c_int(0)
+        s = oracle().o_ecache_get(self.p, eid, C.byref(ld))
+        return s, bool(ld.value)
+
+    def pin(self, eid):
+        return oracle().o_ecache_pin(self.p, eid), True
+
+    def route_bias(self, logits, bias):
+        logits = f32(logits).copy()
+        oracle().o_ecache_route_bias(self.p, ptr(logits), bias)
+        return logits
+
+    def state(self):
+        n = C.c_int()
+        eids = np.empty(self.cap, np.int32)
+        heat = np.zeros(max(self.E, 1), np.uint32)
+        last = np.zeros(max(self.E, 1), np.uint32)
+        clock = C.c_uint32()
+        hits, misses = C.c_longlong(), C.c_longlong()
+        oracle().o_ecache_state(self.p, C.byref(n), ptr(eids), ptr(heat), ptr(last), C.byref(clock),
+                                C.byref(hits), C.byref(misses))
+        return OCacheState(n.value, eids.tolist(), heat[:self.E].tolist(), last[:self.E].tolist(), clock.value,
+                           hits.value, misses.value)
+
+
+class _RefSlot(C.Structure):
+    _fields_ = [("eid", C.c_int), ("g", P), ("u", P), ("d", P), ("gs", P), ("us", P), ("ds", P)]
+
+
+class _RefCache(C.Structure):
+    _fields_ = [("slots", C.POINTER(_RefSlot)), ("n", C.c_int), ("cap", C.c_int), ("heat", C.POINTER(C.c_uint32)),
+                ("last", C.POINTER(C.c_uint32)), ("pinned", C.POINTER(C.c_uint8)), ("n_experts", C.c_int),
+                ("clock", C.c_uint32), ("hits", C.c_longlong), ("misses", C.c_longlong)]
+
+
+REF_LOAD_FN = C.CFUNCTYPE(None, P, I32, I32, C.POINTER(_RefSlot), I32, I32)
+
+
+class RefCache:
+    """The reference's own ExpertCache (runtime/moecache.c compiled into
+    oracle/_ref), driven with a loader that records each load."""
+
+    def __init__(self, r, cap, n_experts, inter=4, hidden=4):
+        self.r, self.E, self.I, self.D = r, n_experts, inter, hidden
+        self.c = _RefCache()
+        self.loads = []
+        self.fn = REF_LOAD_FN(lambda ctx, layer, eid, slot, i, d: self.loads.append(eid))
+        r.moty_expert_cache_init.argtypes = [C.POINTER(_RefCache), I32, I32]
+        r.moty_expert_cache_init.restype = None
+        for nm in ("moty_expert_get", "moty_expert_pin"):
+            f = getattr(r, nm)
+            f.argtypes = [C.POINTER(_RefCache), P, I32, I32, REF_LOAD_FN, I32, I32]
+            f.restype = C.POINTER(_RefSlot)
+        r.moty_moe_route_bias.argtypes = [P, C.POINTER(_RefCache), F32]
+        r.moty_moe_route_bias.restype = None
+        r.moty_expert_cache_free.argtypes = [C.POINTER(_RefCache)]
+        r.moty_expert_cache_free.restype = None
+        r.moty_expert_cache_init(C.byref(self.c), cap, n_experts)
+        self.cap = self.c.cap
+
+    def __del__(self):
+        if getattr(self, "r", None):
+            self.r.moty_expert_cache_free(C.byref(self.c))
+
+    def _slot(self, sp):
+        base = C.addressof(self.c.slots.contents)
+        return (C.addressof(sp.contents) - base) // C.sizeof(_RefSlot)
+
+    def get(self, eid):
+        n0 = len(self.loads)
+        sp = self.r.moty_expert_get(C.byref(self.c), None, 0, eid, self.fn, self.I, self.D)
+        return self._slot(sp), len(self.loads) > n0
+
+    def pin(self, eid):
+        sp = self.r.moty_expert_pin(C.byref(self.c), None, 0, eid, self.fn, self.I, self.D)
+        return self._slot(sp), True
+
+    def route_bias(self, logits, bias):
+        logits = f32(logits).copy()
+        self.r.moty_moe_route_bias(ptr(logits), C.byref(self.c), bias)
+        return logits
+
+    def state(self):
+        c = self.c
+        eids = [c.slots[i].eid for i in range(self.cap)]
+        heat = [c.heat[e] for e in range(self.E)] if self.E > 0 else []
+        last = [c.last[e] for e in range(self.E)] if self.E > 0 else []
+        return OCacheState(c.n, eids, heat, last, c.clock, c.hits, c.misses)
