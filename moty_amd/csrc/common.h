@@ -87,6 +87,27 @@ __device__ __forceinline__ float f16_to_f32(uint32_t h) {
 }
 
 // ---------------------------------------------------------------------------
+// 16 bytes per lane from global memory straight into LDS, at lds_base +
+// 16*lane (global_load_lds_dwordx4; lds_base must be wave-uniform).  Written
+// as inline asm so that the compiler's wait insertion does not see an LDS
+// write in flight -- it would wait for every outstanding load before each
+// LDS read -- callers order it themselves with vmcnt waits and barriers.
+// m0 (the LDS base register) is saved and restored around the load.
+__device__ __forceinline__ void dma16_to_lds(const void* g, uint32_t lds_base) {
+  uint32_t save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "v"(g), "s"(lds_base));
+}
+
+// s_waitcnt vmcnt(n) alone (expcnt and lgkmcnt left at their maxima)
+#define MOTY_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+
+// ---------------------------------------------------------------------------
 // wave64 reductions
 __device__ __forceinline__ int wave_sum_i32(int v) {
 #pragma unroll

@@ -143,10 +143,130 @@ __global__ __launch_bounds__(GM_NT, 2) void k_gemm_q8(const int8_t* __restrict__
   }
 }
 
+// The same GEMM for K % 128 == 0 with the operand tiles moved by DMA:
+// global_load_lds writes each 16-byte chunk straight into LDS (no register
+// staging), S - 1 K blocks ahead of the MFMAs.  A stage holds the BM
+// activation rows then the BN weight rows, 128 bytes each, dense; chunk c of
+// row r sits in 16-byte slot c ^ ((r >> 1) & 7), so the 16 lanes that one
+// ds_read_b128 cycle serves (rows r..r+15, one chunk) hit 16 distinct
+// 16-byte bank groups.  A DMA instruction fills 8 rows (1 KiB): lane l loads
+// row l/8's chunk (l%8) ^ ((row >> 1) & 7) into slot l%8.
+template <int BM, int BN, int S>
+__global__ __launch_bounds__(GM_NT) void k_gemm_q8_dma(const int8_t* __restrict__ xq, const float* __restrict__ sx,
+                                                       const int8_t* __restrict__ W, const float* __restrict__ scale,
+                                                       float* __restrict__ y, int M, int K, int O) {
+  constexpr int STAGE = (BM + BN) * GM_KB;
+  constexpr int NI = (BM + BN) / 32;  // DMA instructions per wave per stage
+  constexpr int TM = BM / 2, TN = BN / 2, FM = TM / 32, FN = TN / 32;
+  __shared__ __align__(1024) int8_t lds[S * STAGE];
+  __shared__ float s_sx[BM];
+  const int tid = threadIdx.x, lane = tid % MOTY_WAVE, wv = tid / MOTY_WAVE;
+  const int wm = wv >> 1, wn = wv & 1;
+  const int r32 = lane & 31, h = lane >> 5;
+  const int mb = blockIdx.y * BM, nb = blockIdx.x * BN;
+  const int8_t* src[NI];
+#pragma unroll
+  for (int i = 0; i < NI; i++) {
+    const int row = (i * 4 + wv) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((row >> 1) & 7);
+    if (row < BM) {
+      const int m = mb + row < M ? mb + row : M - 1;  // rows past the end: loaded, never stored
+      src[i] = xq + (int64_t)m * K + c * 16;
+    } else {
+      const int n = nb + row - BM < O ? nb + row - BM : O - 1;
+      src[i] = W + (int64_t)n * K + c * 16;
+    }
+  }
+  const int nk = K / GM_KB;
+  // K block kb into stage kb % S; blocks past the end reload the last one
+  // (their stage is never read), so every iteration issues the same count
+  auto issue = [&](int kb) {
+    const int kc = (kb < nk ? kb : nk - 1) * GM_KB;
+    const uint32_t base = (uint32_t)(uintptr_t)lds + (kb % S) * STAGE + wv * 1024;
+#pragma unroll
+    for (int i = 0; i < NI; i++) dma16_to_lds(src[i] + kc, __builtin_amdgcn_readfirstlane(base + i * 4 * 1024));
+  };
+  // epilogue scales first: their loads are the oldest, so the vmcnt waits
+  // below (which count only the DMAs after them) also cover them
+  float sxr;
+  {
+    const int m = mb + tid % BM;
+    sxr = sx[m < M ? m : M - 1];
+  }
+  float scn[FN];
+#pragma unroll
+  for (int j = 0; j < FN; j++) {
+    const int n = nb + wn * TN + j * 32 + r32;
+    scn[j] = scale[n < O ? n : O - 1];
+  }
+#pragma unroll
+  for (int s = 0; s < S - 1; s++) issue(s);
+  v16i acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; i++)
+#pragma unroll
+    for (int j = 0; j < FN; j++) acc[i][j] = v16i{};
+  for (int kb = 0; kb < nk; kb++) {
+    // this wave's DMAs of block kb have landed (the S-2 later blocks may
+    // still fly); the barrier makes every wave's share visible and retires
+    // the reads of block kb-1, whose stage the next DMA overwrites
+    MOTY_WAIT_VMCNT((S - 2) * NI);
+    __syncthreads();
+    issue(kb + S - 1);
+    const int8_t* st = lds + (kb % S) * STAGE;
+#pragma unroll
+    for (int j4 = 0; j4 < 4; j4++) {
+      // MFMA step j4 takes chunk 4h + j4 of row r32 (a k-permutation shared
+      // by both operands: exact for integer dots)
+      const int sw = ((h * 4 + j4) ^ ((r32 >> 1) & 7)) * 16;
+      v4i fa[FM], fb[FN];
+#pragma unroll
+      for (int i = 0; i < FM; i++) fa[i] = *(const v4i*)(st + (wm * TM + i * 32 + r32) * GM_KB + sw);
+#pragma unroll
+      for (int j = 0; j < FN; j++) fb[j] = *(const v4i*)(st + (BM + wn * TN + j * 32 + r32) * GM_KB + sw);
+#pragma unroll
+      for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+  }
+  // every DMA (including the reloads past the end) lands before the
+  // workgroup's LDS can be released
+  __builtin_amdgcn_s_waitcnt(0);
+  if (tid < BM) s_sx[tid] = sxr;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < FN; j++) {
+    const int n = nb + wn * TN + j * 32 + r32;
+    if (n >= O) continue;
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int ml = wm * TM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (mb + ml < M) y[(int64_t)(mb + ml) * O + n] = (scn[j] * s_sx[ml]) * (float)acc[i][j][r];
+      }
+  }
+}
+
 int launch_gemm_q8(const int8_t* xq, const float* sx, const int8_t* W, const float* scale, float* y, int M,
                    int K, int O, hipStream_t st) {
   if (K % 16) return MOTY_EUNSUP;
   if (M <= 0 || O <= 0) return MOTY_OK;
+  if (K % GM_KB == 0) {
+    // 64 x 64 tiles (several workgroups per CU hide the DMA latency); three
+    // stages for K <= 1024, four for longer rows.  Measured on MI355X, M =
+    // 512: N=10240, K=1024: 17.3 us vs 18.8 register-staged; K=2048, N=1024:
+    // 7.7 vs 9.6; K=3072: 10.0 vs 12.5.
+    const dim3 grid((O + 63) / 64, (M + 63) / 64);
+    if (K <= 1024)
+      hipLaunchKernelGGL((k_gemm_q8_dma<64, 64, 3>), grid, dim3(GM_NT), 0, st, xq, sx, W, scale, y, M, K, O);
+    else
+      hipLaunchKernelGGL((k_gemm_q8_dma<64, 64, 4>), grid, dim3(GM_NT), 0, st, xq, sx, W, scale, y, M, K, O);
+    LAUNCH_TRY("k_gemm_q8_dma");
+    return MOTY_OK;
+  }
   // Tiles and prefetch depth from a sweep on MI355X (M = 512, the C2
   // projections): 64 x 64 tiles beat 128 x 128 until the grid holds several
   // workgroups per CU (N=10240, K=1024: 17.1 us vs 18.5); long K rows keep

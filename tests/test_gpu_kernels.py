@@ -104,7 +104,9 @@ def test_pack_int4_grouped(ops, O, I, gs):
 
 Q8_CASES = [(1, 1024, 3072), (1, 3072, 1024), (2, 1024, 100), (3, 48, 24), (4, 2048, 1024),
             (1, 16384, 64), (5, 1024, 256), (8, 3072, 96), (64, 1024, 1024), (512, 1024, 2048),
-            (130, 2048, 200), (33, 16, 17), (1024, 1024, 4096), (256, 1040, 8192), (200, 3072, 1000)]
+            (130, 2048, 200), (33, 16, 17), (1024, 1024, 4096), (256, 1040, 8192), (200, 3072, 1000),
+            # K % 128 == 0 past the GEMV: the DMA-staged GEMM, one-block and ragged tiles
+            (70, 128, 33), (9, 256, 1), (130, 384, 65), (600, 4096, 100), (5, 128, 7)]
 
 
 @pytest.mark.parametrize("S,I,O", Q8_CASES)
