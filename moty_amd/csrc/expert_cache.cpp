@@ -180,9 +180,22 @@ static int ec_alloc(MotyHipExpertCache* c, int inter, int hidden) {
   return MOTY_OK;
 }
 
-// Fill device slot `s` with expert `eid` through the loader, on `st`.
+// Fill device slot `s` with expert `eid` through the loader, on `st`.  On
+// failure the slot is marked empty, so a later get reloads it instead of
+// taking stale weights for a hit.
+static int ec_load_(MotyHipExpertCache* c, void* ctx, int layer, int eid, MotyHipLoadExpertFn fn, int s,
+                    hipStream_t st);
 static int ec_load(MotyHipExpertCache* c, void* ctx, int layer, int eid, MotyHipLoadExpertFn fn, int s,
                    hipStream_t st) {
+  const int rc = ec_load_(c, ctx, layer, eid, fn, s, st);
+  if (rc) {
+    c->eid[s] = -1;
+    c->dslot[s].eid = -1;
+  }
+  return rc;
+}
+static int ec_load_(MotyHipExpertCache* c, void* ctx, int layer, int eid, MotyHipLoadExpertFn fn, int s,
+                    hipStream_t st) {
   const int k = c->next_stage;
   c->next_stage ^= 1;
   HIP_TRY(hipEventSynchronize(c->staged[k]));  // its previous copy has left the staging slot
