@@ -90,7 +90,8 @@ static int ec_get(MotyHipExpertCache* c, int eid, bool* load, int* prev) {
     for (int i = 0; i < c->n; i++) {
       const int e = c->eid[i];
       if (ec_pinned(c, e)) continue;
-      const uint64_t s = lfru_score(c->heat[e], c->last[e], c->clock);
+      // a slot left empty by a failed load scores lowest: refill it first
+      const uint64_t s = e < 0 || e >= c->n_experts ? 0 : lfru_score(c->heat[e], c->last[e], c->clock);
       if (s < worst) {
         worst = s;
         v = i;
