@@ -131,7 +131,21 @@ static int ec_pin(MotyHipExpertCache* c, int eid, int* prev) {
   return v;
 }
 
-// Device and staging storage, on the first load.
+static void ec_release(MotyHipExpertCache* c) {
+  for (void* p : {(void*)c->g, (void*)c->u, (void*)c->d, (void*)c->gs, (void*)c->us, (void*)c->ds})
+    if (p) hipFree(p);
+  c->g = c->u = c->d = nullptr;
+  c->gs = c->us = c->ds = nullptr;
+  for (int k = 0; k < 2; k++) {
+    if (c->stage_base[k].g) hipHostFree(c->stage_base[k].g);
+    if (c->staged[k]) hipEventDestroy(c->staged[k]);
+    c->stage_base[k] = c->stage[k] = MotyHipExpertSlot{};
+    c->staged[k] = nullptr;
+  }
+  c->dslot.clear();
+}
+
+// Device and staging storage, on the first load; all or nothing.
 static int ec_alloc(MotyHipExpertCache* c, int inter, int hidden) {
   if (c->g) {
     if (inter != c->I || hidden != c->D)
@@ -143,41 +157,41 @@ static int ec_alloc(MotyHipExpertCache* c, int inter, int hidden) {
   if (inter <= 0 || hidden <= 0) return set_error("expert cache: bad inter/hidden"), MOTY_EINVAL;
   HIP_TRY(hipGetDevice(&c->dev));
   const size_t ng = (size_t)inter * hidden, cap = (size_t)c->cap;
-  c->I = inter;
-  c->D = hidden;
-  void* p[6];
+  void* p[6] = {};
   const size_t sz[6] = {cap * ng, cap * ng, cap * ng, cap * inter * 4, cap * inter * 4, cap * hidden * 4};
-  for (int i = 0; i < 6; i++) {
-    hipError_t e = hipMalloc(&p[i], sz[i]);
-    if (e != hipSuccess) {
-      for (int j = 0; j < i; j++) hipFree(p[j]);
-      return check_hip(e, "expert cache hipMalloc");
-    }
-  }
+  hipError_t e = hipSuccess;
+  for (int i = 0; i < 6 && e == hipSuccess; i++) e = hipMalloc(&p[i], sz[i]);
   c->g = (int8_t*)p[0];
   c->u = (int8_t*)p[1];
   c->d = (int8_t*)p[2];
   c->gs = (float*)p[3];
   c->us = (float*)p[4];
   c->ds = (float*)p[5];
+  for (int k = 0; k < 2 && e == hipSuccess; k++) {
+    void* h = nullptr;
+    e = hipHostMalloc(&h, 3 * ng + (2 * (size_t)inter + hidden) * 4, hipHostMallocDefault);
+    if (e != hipSuccess) break;
+    char* b = (char*)h;
+    c->stage_base[k] = MotyHipExpertSlot{-1,
+                                         (int8_t*)b,
+                                         (int8_t*)(b + ng),
+                                         (int8_t*)(b + 2 * ng),
+                                         (float*)(b + 3 * ng),
+                                         (float*)(b + 3 * ng + inter * 4),
+                                         (float*)(b + 3 * ng + 2 * (size_t)inter * 4)};
+    c->stage[k] = c->stage_base[k];
+    e = hipEventCreateWithFlags(&c->staged[k], hipEventDisableTiming);
+  }
+  if (e != hipSuccess) {
+    ec_release(c);
+    return check_hip(e, "expert cache allocation");
+  }
+  c->I = inter;
+  c->D = hidden;
   c->dslot.resize(c->cap);
   for (int s = 0; s < c->cap; s++)
     c->dslot[s] = MotyHipExpertSlot{c->eid[s],         c->g + s * ng,     c->u + s * ng,     c->d + s * ng,
                                     c->gs + s * inter, c->us + s * inter, c->ds + s * hidden};
-  for (int k = 0; k < 2; k++) {
-    void* h;
-    HIP_TRY(hipHostMalloc(&h, 3 * ng + (2 * (size_t)inter + hidden) * 4, hipHostMallocDefault));
-    char* b = (char*)h;
-    c->stage[k] = MotyHipExpertSlot{-1,
-                                    (int8_t*)b,
-                                    (int8_t*)(b + ng),
-                                    (int8_t*)(b + 2 * ng),
-                                    (float*)(b + 3 * ng),
-                                    (float*)(b + 3 * ng + inter * 4),
-                                    (float*)(b + 3 * ng + 2 * (size_t)inter * 4)};
-    c->stage_base[k] = c->stage[k];
-    HIP_TRY(hipEventCreateWithFlags(&c->staged[k], hipEventDisableTiming));
-  }
   return MOTY_OK;
 }
 
@@ -276,16 +290,7 @@ int moty_hip_expert_cache_free(MotyHipExpertCache* c) {
     HIP_TRY(hipSetDevice(c->dev));
     HIP_TRY(hipDeviceSynchronize());
   }
-  hipFree(c->g);
-  hipFree(c->u);
-  hipFree(c->d);
-  hipFree(c->gs);
-  hipFree(c->us);
-  hipFree(c->ds);
-  for (int k = 0; k < 2; k++) {
-    if (c->stage_base[k].g) hipHostFree(c->stage_base[k].g);
-    if (c->staged[k]) hipEventDestroy(c->staged[k]);
-  }
+  ec_release(c);
   if (c->ptab_h) hipHostFree(c->ptab_h);
   if (c->route_h) hipHostFree(c->route_h);
   if (c->call_done) hipEventDestroy(c->call_done);
