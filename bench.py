@@ -317,6 +317,38 @@ def bench_c3(c, steps, warmup):
     return {"workload": "C3 8B-dense FFN, grouped int4 g32 (IDOT4=1), D=4096, I=12288, M=1 and M=256", **res}
 
 
+def bench_q8_gemv_sizes(c, steps, warmup):
+    """The C1 decode kernels at larger weight matrices, where the launch
+    floor no longer dominates: the Q8 GEMV (k_gemv1_q8, S = 1) on the
+    reference's own matmul_q_s benchmark shape 4096 x 4096
+    (docs/performance.md:45) and on the 8B FFN's 12288 x 4096, and the fused
+    gate/up + SiLU GEMV over the 8B gate and up matrices.  Weights rotate
+    past the Infinity Cache like C1's."""
+    torch, ops = c.torch, c.ops
+    res = {}
+    for O, I in ((4096, 4096), (12288, 4096)):
+        wbytes = O * I + O * 4
+        g = c.gen(7, O)
+        copies = [c.q8((O, I), g) for _ in range(n_copies(wbytes))]
+        x = c.randn((1, I), c.gen(7, 1))
+        y = torch.empty((1, O), device="cuda:0")
+        t, n = c.time_steps([lambda w=w: ops.matmul_q_s(x, w[0], w[1], out=y) for w in copies], steps, warmup)
+        algo = wbytes + (I + O) * 4
+        res["gemv_%dx%d" % (O, I)] = {"us": round(t * 1e6, 3), **roofline("hbm", algo / t / 1e9, HBM_PEAK_GBS, "GB/s")}
+    D, I = 4096, 12288
+    wbytes = 2 * (I * D + I * 4)
+    g = c.gen(7, 2)
+    copies = [c.q8((I, D), g) + c.q8((I, D), g) for _ in range(n_copies(wbytes))]
+    x = c.randn((1, D), c.gen(7, 3))
+    h = torch.empty((1, I), device="cuda:0")
+    t, n = c.time_steps([lambda w=w: ops.gate_up_silu_q8(x, w[0], w[1], w[2], w[3], out=h) for w in copies],
+                        steps, warmup)
+    algo = wbytes + (D + I) * 4
+    res["gate_up_silu_8B"] = {"us": round(t * 1e6, 3), **roofline("hbm", algo / t / 1e9, HBM_PEAK_GBS, "GB/s")}
+    return {"workload": "Q8 decode GEMV at larger shapes (S = 1): 4096 x 4096, 12288 x 4096, fused gate/up + SiLU "
+                        "over 2 x 12288 x 4096", **res}
+
+
 def bench_c3_r4(c, steps, warmup):
     """The C3 8B-dense FFN shapes in the Q4R4 format (nn/matmul.c:395-431:
     f16 group scales, 4-row blocks, group-32 int8 activations), gate and up
@@ -508,6 +540,8 @@ def main():
     log("C4: %.0f tokens/s, %.3f ms/layer" % (c4["tokens_per_s"], c4["ms_per_layer"]))
     extra = []
     if not args.quick:
+        log("Q8 GEMV at larger shapes")
+        extra.append(bench_q8_gemv_sizes(c, args.steps, args.warmup))
         log("C2")
         extra.append(bench_c2(c, args.steps, args.warmup))
         log("C3")
