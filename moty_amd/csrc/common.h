@@ -134,24 +134,20 @@ __device__ __forceinline__ int dot16(const int4 a, const int4 b, int c) {
 
 // 8 packed int4 bytes (16 nibbles, even element in the low nibble, value
 // n in 0..15 standing for n-8) -> 16 signed int8 (n-8) in element order.
-__device__ __forceinline__ uint32_t nib_lo_bytes(uint32_t w) {
-  // w holds 4 packed bytes b0..b3 = elements 0..7; returns elements 0..3
-  // as bytes (n-8): byte j = nibble j of the little-endian stream.
-  uint32_t b0 = w & 0xffu, b1 = (w >> 8) & 0xffu;
-  uint32_t r = (b0 & 0xfu) | ((b0 >> 4) << 8) | ((b1 & 0xfu) << 16) | ((b1 >> 4) << 24);
-  return r;
-}
-__device__ __forceinline__ uint32_t nib_signed(uint32_t t) {
-  // per byte n in 0..15 -> (n-8) as int8: n^8 then sign-extend bit 3
-  t ^= 0x08080808u;
-  return t | ((t & 0x08080808u) * 0x1Eu);
-}
+// Per input word: low and high nibbles masked out as bytes, interleaved
+// back into element order by two byte permutes, then n-8 per byte without
+// carries between bytes: n + 0x78 stays below 0x100, and flipping bit 7
+// turns it into n - 8 in two's complement.
+__device__ __forceinline__ uint32_t nib_minus8(uint32_t t) { return (t + 0x78787878u) ^ 0x80808080u; }
 __device__ __forceinline__ int4 unpack_nib16(uint2 w) {
+  const uint32_t l0 = w.x & 0x0f0f0f0fu, h0 = (w.x >> 4) & 0x0f0f0f0fu;
+  const uint32_t l1 = w.y & 0x0f0f0f0fu, h1 = (w.y >> 4) & 0x0f0f0f0fu;
+  // perm(hi, lo, sel): byte k of the result = byte sel_k of {hi:lo} (lo = bytes 0..3)
   int4 r;
-  r.x = (int)nib_signed(nib_lo_bytes(w.x));
-  r.y = (int)nib_signed(nib_lo_bytes(w.x >> 16));
-  r.z = (int)nib_signed(nib_lo_bytes(w.y));
-  r.w = (int)nib_signed(nib_lo_bytes(w.y >> 16));
+  r.x = (int)nib_minus8(__builtin_amdgcn_perm(h0, l0, 0x05010400u));  // elements 0..3
+  r.y = (int)nib_minus8(__builtin_amdgcn_perm(h0, l0, 0x07030602u));  // 4..7
+  r.z = (int)nib_minus8(__builtin_amdgcn_perm(h1, l1, 0x05010400u));  // 8..11
+  r.w = (int)nib_minus8(__builtin_amdgcn_perm(h1, l1, 0x07030602u));  // 12..15
   return r;
 }
 
