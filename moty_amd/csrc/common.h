@@ -151,6 +151,19 @@ __device__ __forceinline__ int4 unpack_nib16(uint2 w) {
   return r;
 }
 
+// The same 16 codes as unsigned bytes n (0..15), for dots whose -8*sum(x)
+// term is added separately (its accumulator starts there).
+__device__ __forceinline__ int4 unpack_nib16_u(uint2 w) {
+  const uint32_t l0 = w.x & 0x0f0f0f0fu, h0 = (w.x >> 4) & 0x0f0f0f0fu;
+  const uint32_t l1 = w.y & 0x0f0f0f0fu, h1 = (w.y >> 4) & 0x0f0f0f0fu;
+  int4 r;
+  r.x = (int)__builtin_amdgcn_perm(h0, l0, 0x05010400u);
+  r.y = (int)__builtin_amdgcn_perm(h0, l0, 0x07030602u);
+  r.z = (int)__builtin_amdgcn_perm(h1, l1, 0x05010400u);
+  r.w = (int)__builtin_amdgcn_perm(h1, l1, 0x07030602u);
+  return r;
+}
+
 // ---------------------------------------------------------------------------
 // 16-lane horizontal sum with gcc's _mm512_reduce_add_ps association:
 // v[j+8]+v[j], then [j+4]+[j], then (b0+b2)+(b1+b3).  `v` is lane c's value

@@ -130,7 +130,8 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
   const int lane = threadIdx.x % MOTY_WAVE, wv = threadIdx.x / MOTY_WAVE;
   const int ng = I / 32, rb = I / 2, ldv = ng + 2;  // ldv even: float2 rows stay 8-byte aligned
   int8_t* xq_s = lds;                                                          // [I]
-  float2* dv = (float2*)(lds + I) + (size_t)wv * (NM * RW * ldv);               // [NM*RW][ldv] (scale, dot)
+  int* xg8 = (int*)(lds + I);                                                  // [ng] -8 * group sums
+  float2* dv = (float2*)(lds + I + ng * 4) + (size_t)wv * (NM * RW * ldv);      // [NM*RW][ldv] (scale, dot)
   const int o0 = (blockIdx.x * WAVES + wv) * RW;
 
   // 1. x (one pass, kept in registers), then every nibble load of this wave
@@ -188,6 +189,14 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
     }
   }
   __syncthreads();
+  // -8 * each group's activation sum: the dots run on the unsigned codes n
+  // and start from it, giving sum (n-8)*x exactly
+  for (int g = threadIdx.x; g < ng; g += NT) {
+    const int4 a = *(const int4*)(xq_s + g * 32), b = *(const int4*)(xq_s + g * 32 + 16);
+    xg8[g] = -8 * dot16(b, int4{0x01010101, 0x01010101, 0x01010101, 0x01010101},
+                        dot16(a, int4{0x01010101, 0x01010101, 0x01010101, 0x01010101}, 0));
+  }
+  __syncthreads();
   // 3. exact group dots with their group scales into the wave's LDS slice
 #pragma unroll
   for (int c = 0; c < NGC; c++) {
@@ -195,14 +204,15 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
     if (g >= ng) break;
     const int4 x0 = *(const int4*)(xq_s + g * 32);
     const int4 x1 = *(const int4*)(xq_s + g * 32 + 16);
+    const int c8 = xg8[g];
 #pragma unroll
     for (int m = 0; m < NM; m++)
 #pragma unroll
       for (int r = 0; r < RW; r++) {
         const int4 w = wb[m][r][c];
-        const int4 w0 = unpack_nib16(uint2{(uint32_t)w.x, (uint32_t)w.y});
-        const int4 w1 = unpack_nib16(uint2{(uint32_t)w.z, (uint32_t)w.w});
-        const int d = dot16(w1, x1, dot16(w0, x0, 0));
+        const int4 w0 = unpack_nib16_u(uint2{(uint32_t)w.x, (uint32_t)w.y});
+        const int4 w1 = unpack_nib16_u(uint2{(uint32_t)w.z, (uint32_t)w.w});
+        const int d = dot16(w1, x1, dot16(w0, x0, c8));
         dv[(m * RW + r) * ldv + g] = float2{wsc[m][r][c], (float)d};
       }
   }
@@ -423,7 +433,7 @@ static int go_gemv1_i4g(const float* x, const uint8_t* q4, const float* scl, con
                         float* y, int I, int O, hipStream_t st) {
   constexpr int NM = PAIR ? 2 : 1;
   const int ng = I / 32;
-  const size_t lds = (size_t)I + (size_t)(NT / MOTY_WAVE) * NM * RW * (ng + 2) * 8;
+  const size_t lds = (size_t)I + (size_t)ng * 4 + (size_t)(NT / MOTY_WAVE) * NM * RW * (ng + 2) * 8;
   if (lds > 64 * 1024) return MOTY_EUNSUP;
   const unsigned nb = (unsigned)((O + RW * (NT / MOTY_WAVE) - 1) / (RW * (NT / MOTY_WAVE)));
   hipLaunchKernelGGL((k_gemv1_i4g<RW, NGC, PAIR, NT>), dim3(nb), dim3(NT), lds, st, x, q4, scl, q4b, sclb, y, I, O);
