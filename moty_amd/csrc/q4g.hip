@@ -143,22 +143,22 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
   }
   int4 wb[NM][RW][NGC];
   float wsc[NM][RW][NGC];  // group scales, loaded with the nibbles
+  // chunk-major issue order: chunk c of every row lands before chunk c+1, so
+  // the group dots and FMA chains of chunk c can run while later chunks are
+  // still in flight (the compiler waits only for the chunk it consumes)
 #pragma unroll
-  for (int m = 0; m < NM; m++)
+  for (int c = 0; c < NGC; c++)
 #pragma unroll
-    for (int r = 0; r < RW; r++) {
-      const int64_t o = o0 + r < O ? o0 + r : O - 1;
-      const uint8_t* base = (m ? q4b : q4) + o * rb;
-      const float* sbase = (m ? sclb : scl) + o * ng;
+    for (int m = 0; m < NM; m++)
 #pragma unroll
-      for (int c = 0; c < NGC; c++) {
+      for (int r = 0; r < RW; r++) {
+        const int64_t o = o0 + r < O ? o0 + r : O - 1;
         // clamped (unused past ng): unconditional loads keep the wave's
         // loads in one straight run, with no wait at branch joins
         const int g = c * 64 + lane < ng ? c * 64 + lane : 0;
-        wb[m][r][c] = *(const int4*)(base + g * 16);
-        wsc[m][r][c] = sbase[g];
+        wb[m][r][c] = *(const int4*)((m ? q4b : q4) + o * rb + g * 16);
+        wsc[m][r][c] = ((m ? sclb : scl) + o * ng)[g];
       }
-    }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int j = 0; j < XV; j++) xr[j] = sel4((threadIdx.x + j * NT) * 4 < I, xr[j]);
@@ -197,46 +197,50 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
                         dot16(a, int4{0x01010101, 0x01010101, 0x01010101, 0x01010101}, 0));
   }
   __syncthreads();
-  // 3. exact group dots with their group scales into the wave's LDS slice
+  // 3./4. per 64-group chunk: every lane forms its group's exact integer dot
+  // for each row and parks (scale, dot) in the wave's LDS slice; then lane
+  // j < NM*RW continues the FMA chain of its row (j % RW of matrix j / RW)
+  // over the chunk's groups in order, while later chunks may still arrive.
+  // 16-byte LDS reads carry two groups' pairs.
+  float acc = 0.f;
 #pragma unroll
   for (int c = 0; c < NGC; c++) {
     const int g = c * 64 + lane;
-    if (g >= ng) break;
-    const int4 x0 = *(const int4*)(xq_s + g * 32);
-    const int4 x1 = *(const int4*)(xq_s + g * 32 + 16);
-    const int c8 = xg8[g];
+    if (g < ng) {
+      const int4 x0 = *(const int4*)(xq_s + g * 32);
+      const int4 x1 = *(const int4*)(xq_s + g * 32 + 16);
+      const int c8 = xg8[g];
 #pragma unroll
-    for (int m = 0; m < NM; m++)
+      for (int m = 0; m < NM; m++)
 #pragma unroll
-      for (int r = 0; r < RW; r++) {
-        const int4 w = wb[m][r][c];
-        const int4 w0 = unpack_nib16_u(uint2{(uint32_t)w.x, (uint32_t)w.y});
-        const int4 w1 = unpack_nib16_u(uint2{(uint32_t)w.z, (uint32_t)w.w});
-        const int d = dot16(w1, x1, dot16(w0, x0, c8));
-        dv[(m * RW + r) * ldv + g] = float2{wsc[m][r][c], (float)d};
-      }
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  // 4. ordered FMA chains: lane j < NM*RW runs row (j % RW) of matrix j / RW;
-  //    16-byte LDS reads carry two groups' (scale, dot)
-  float acc = 0.f;
-  if (lane < NM * RW) {
-    const float4* dr = (const float4*)(dv + lane * ldv);
-    int g = 0;
-    for (; g + 16 <= ng; g += 16) {
-      float4 v[8];
-#pragma unroll
-      for (int u = 0; u < 8; u++) v[u] = dr[g / 2 + u];
-#pragma unroll
-      for (int u = 0; u < 8; u++) {
-        acc = __fmaf_rn(v[u].x, v[u].y, acc);
-        acc = __fmaf_rn(v[u].z, v[u].w, acc);
-      }
+        for (int r = 0; r < RW; r++) {
+          const int4 w = wb[m][r][c];
+          const int4 w0 = unpack_nib16_u(uint2{(uint32_t)w.x, (uint32_t)w.y});
+          const int4 w1 = unpack_nib16_u(uint2{(uint32_t)w.z, (uint32_t)w.w});
+          const int d = dot16(w1, x1, dot16(w0, x0, c8));
+          dv[(m * RW + r) * ldv + g] = float2{wsc[m][r][c], (float)d};
+        }
     }
-    const float2* d2 = dv + lane * ldv;
-    for (; g < ng; g++) acc = __fmaf_rn(d2[g].x, d2[g].y, acc);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < NM * RW) {
+      const int gend = ng < (c + 1) * 64 ? ng : (c + 1) * 64;
+      const float4* dr = (const float4*)(dv + lane * ldv);
+      int gg = c * 64;
+      for (; gg + 16 <= gend; gg += 16) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = dr[gg / 2 + u];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+          acc = __fmaf_rn(v[u].x, v[u].y, acc);
+          acc = __fmaf_rn(v[u].z, v[u].w, acc);
+        }
+      }
+      const float2* d2 = dv + lane * ldv;
+      for (; gg < gend; gg++) acc = __fmaf_rn(d2[gg].x, d2[gg].y, acc);
+    }
   }
   const float sxv = sx_s;
   if (PAIR) {
