@@ -175,9 +175,14 @@ __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, con
     }
   __syncthreads();
 
-  // 3. per chunk: the exact integer group sum, the group's scale (from the
-  // lane that loaded it: group g = lane/4 + 16k sits in lane g % 64, chunk
-  // k/4 -- Q8R4: lane/8 + 8k, chunk k/8), the chain step's operands
+  // 3./4. per chunk: the exact integer group sum, the group's scale (from
+  // the lane that loaded it: group g = lane/4 + 16k sits in lane g % 64,
+  // chunk k/4 -- Q8R4: lane/8 + 8k, chunk k/8), the chain step's operands;
+  // then lane (m*4 + r)*S_ + t continues row r's chain for token t (PAIR:
+  // m = 1 is the up row) over the chunk's groups in order, while later
+  // chunks may still be in flight.
+  constexpr int GPC = Q8 ? 8 : 16;  // groups per chunk
+  float acc = 0.f;
 #pragma unroll
   for (int k = 0; k < NCH; k++) {
     const int ci = lane + 64 * k;
@@ -203,25 +208,22 @@ __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, con
         if (ok && h == 0) op_s[((m * 4 + r) * S_ + t) * nb + g] = float2{(float)sacc, dd * xs_s[t * nb + gc]};
       }
     }
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-  // 4. lane (t*4 + r) runs row r's chain for token t over the groups in
-  // order (PAIR: lane 4 + r the up row's)
-  float acc = 0.f;
-  if (lane < 4 * NM * S_) {
-    const float2* op = op_s + lane * nb;  // lane = (m*4 + r)*S_ + t with S_ = 1 for PAIR
-    int g = 0;
-    for (; g + 8 <= nb; g += 8) {
-      float2 v[8];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < 4 * NM * S_) {
+      const float2* op = op_s + lane * nb;  // lane = (m*4 + r)*S_ + t with S_ = 1 for PAIR
+      const int g0 = k * GPC, g1 = nb < g0 + GPC ? nb : g0 + GPC;
+      if (g1 - g0 == GPC) {
+        float2 v[GPC];
 #pragma unroll
-      for (int u = 0; u < 8; u++) v[u] = op[g + u];
+        for (int u = 0; u < GPC; u++) v[u] = op[g0 + u];
 #pragma unroll
-      for (int u = 0; u < 8; u++) acc = __fmaf_rn(v[u].x, v[u].y, acc);
+        for (int u = 0; u < GPC; u++) acc = __fmaf_rn(v[u].x, v[u].y, acc);
+      } else {
+        for (int gg = g0; gg < g1; gg++) acc = __fmaf_rn(op[gg].x, op[gg].y, acc);
+      }
     }
-    for (; g < nb; g++) acc = __fmaf_rn(op[g].x, op[g].y, acc);
   }
   if (PAIR) {
     const float u = __shfl(acc, (lane + 4) & 63, 64);
