@@ -27,29 +27,51 @@
 namespace moty {
 
 // ---------------------------------------------------------------------------
-// Group-32 activation quantization: 8 lanes per group, 4 elements per lane.
+// Group-32 activation quantization: a lane pair per group, 16 elements
+// (4 float4) per lane.  Each lane reduces its half in registers; one
+// exchange with the partner lane joins amax and the code sum, so the scale's
+// two divisions run once per half group.  The arithmetic per element is the
+// reference's: s = amax/127 (at least 1e-30), q = rint(x * (1/s)).
+// Returns the group's code sum; q gets the lane's 16 codes, s the scale.
+__device__ __forceinline__ int quant_half_g32(const float4 (&v)[4], uint4& q, float& s) {
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  s = amax / 127.f;
+  if (s < 1e-30f) s = 1e-30f;
+  const float inv = 1.f / s;
+  int sum = 0;
+  uint32_t w[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int a = rne_int(v[j].x * inv), b = rne_int(v[j].y * inv), c = rne_int(v[j].z * inv),
+              d = rne_int(v[j].w * inv);
+    sum += a + b + c + d;
+    w[j] = (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+           ((uint32_t)(d & 0xff) << 24);
+  }
+  q = make_uint4(w[0], w[1], w[2], w[3]);
+  return sum + __shfl_xor(sum, 1, 64);
+}
+
+// One lane per 16 elements of a row: lanes 2i, 2i+1 share group i.
 __global__ __launch_bounds__(256) void k_quant_g32(const float* __restrict__ x, int8_t* __restrict__ xq,
                                                    float* __restrict__ xs, int32_t* __restrict__ xm, int I) {
   const int64_t row = blockIdx.y;
-  const int e = (blockIdx.x * 256 + threadIdx.x) * 4;
+  const int e = (blockIdx.x * 256 + threadIdx.x) * 16;
   const bool ok = e < I;
-  const float4 v = sel4(ok, *(const float4*)(x + row * I + (ok ? e : 0)));
-  float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-  amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
-  float s = amax / 127.f;
-  if (s < 1e-30f) s = 1e-30f;
-  const float inv = 1.f / s;
-  const int a = rne_int(v.x * inv), b = rne_int(v.y * inv), c = rne_int(v.z * inv), d = rne_int(v.w * inv);
-  int sum = a + b + c + d;
-  sum += __shfl_xor(sum, 1, 64);
-  sum += __shfl_xor(sum, 2, 64);
-  sum += __shfl_xor(sum, 4, 64);
+  const float4* src = (const float4*)(x + row * I + (ok ? e : 0));
+  float4 v[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) v[j] = sel4(ok, src[j]);
+  uint4 q;
+  float s;
+  const int sum = quant_half_g32(v, q, s);
   if (!ok) return;
-  *(uint32_t*)(xq + row * I + e) = (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) |
-                                   ((uint32_t)(c & 0xff) << 16) | ((uint32_t)(d & 0xff) << 24);
-  if ((threadIdx.x & 7) == 0) {
+  *(uint4*)(xq + row * I + e) = q;
+  if ((threadIdx.x & 1) == 0) {
     const int nb = I / 32;
     xs[row * nb + e / 32] = s;
     xm[row * nb + e / 32] = sum;
@@ -59,7 +81,7 @@ __global__ __launch_bounds__(256) void k_quant_g32(const float* __restrict__ x, 
 int launch_quant_g32(const float* x, int8_t* xq, float* xs, int32_t* xm, int S, int I, hipStream_t st) {
   if (S <= 0) return MOTY_OK;
   if (I % 32) return MOTY_EUNSUP;
-  hipLaunchKernelGGL(k_quant_g32, dim3((I + 1023) / 1024, S), dim3(256), 0, st, x, xq, xs, xm, I);
+  hipLaunchKernelGGL(k_quant_g32, dim3((I + 4095) / 4096, S), dim3(256), 0, st, x, xq, xs, xm, I);
   LAUNCH_TRY("k_quant_g32");
   return MOTY_OK;
 }
@@ -96,7 +118,7 @@ __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, con
   constexpr int NCH = IC * (Q8 ? 4 : 2);   // weight chunks per lane
   constexpr int DCH = (IC + 1) / 2;        // scale chunks (groups) per lane
   constexpr int WAVES = NT / MOTY_WAVE;
-  constexpr int XC = IC * 1024 / (NT * 4);  // activation float4 per thread per row
+  constexpr int XU = (IC * 64 + NT - 1) / NT;  // activation half groups (16 floats) per thread per row
   extern __shared__ __align__(16) int8_t lds[];
   const int nb = I / 32, O4 = (O + 3) / 4;
   const int lane = threadIdx.x % MOTY_WAVE, wv = threadIdx.x / MOTY_WAVE;
@@ -110,13 +132,15 @@ __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, con
   blk = live ? blk : O4 - 1;
 
   // 1. activation rows, then every weight and scale chunk of the block
-  float4 xr[S_][XC];
+  float4 xr[S_][XU][4];
 #pragma unroll
   for (int t = 0; t < S_; t++)
 #pragma unroll
-    for (int c = 0; c < XC; c++) {
-      const int e = (c * NT + threadIdx.x) * 4;
-      xr[t][c] = *(const float4*)(x + (size_t)(t < S ? t : 0) * I + (e < I ? e : 0));
+    for (int c = 0; c < XU; c++) {
+      const int e = (c * NT + threadIdx.x) * 16;
+      const float4* src = (const float4*)(x + (size_t)(t < S ? t : 0) * I + (e < I ? e : 0));
+#pragma unroll
+      for (int j = 0; j < 4; j++) xr[t][c][j] = src[j];
     }
   // PAIR: W is the row-fused [gate; up] matrix (moty_mat_fuse_rows), the up
   // rows' blocks start O/4 blocks after the gate rows'
@@ -148,26 +172,18 @@ __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, con
 #pragma unroll
   for (int t = 0; t < S_; t++)
 #pragma unroll
-    for (int c = 0; c < XC; c++) {
-      const int e = (c * NT + threadIdx.x) * 4;
+    for (int c = 0; c < XU; c++) {
+      const int e = (c * NT + threadIdx.x) * 16;
       const bool ok = e < I;
-      const float4 v = sel4(ok, xr[t][c]);
-      float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-      amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-      amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-      amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
-      float s = amax / 127.f;
-      if (s < 1e-30f) s = 1e-30f;
-      const float inv = 1.f / s;
-      const int a = rne_int(v.x * inv), b = rne_int(v.y * inv), cc = rne_int(v.z * inv), d = rne_int(v.w * inv);
-      int sum = a + b + cc + d;
-      sum += __shfl_xor(sum, 1, 64);
-      sum += __shfl_xor(sum, 2, 64);
-      sum += __shfl_xor(sum, 4, 64);
+      float4 v[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) v[j] = sel4(ok, xr[t][c][j]);
+      uint4 q;
+      float s;
+      const int sum = quant_half_g32(v, q, s);
       if (ok) {
-        *(uint32_t*)(xq_s + t * I + e) = (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) |
-                                         ((uint32_t)(cc & 0xff) << 16) | ((uint32_t)(d & 0xff) << 24);
-        if ((threadIdx.x & 7) == 0) {
+        *(uint4*)(xq_s + t * I + e) = q;
+        if ((threadIdx.x & 1) == 0) {
           xs_s[t * nb + e / 32] = s;
           xm_s[t * nb + e / 32] = sum;
         }
