@@ -95,11 +95,35 @@ int arena_get(Arena& a, size_t bytes, void** p) {
 }
 
 
-// Device copy of a persistent host weight buffer.
+// Fingerprint of a host buffer from 64 evenly spaced 16-byte samples (the
+// first and last bytes included): FNV-1a over the sampled bytes.  A few
+// hundred nanoseconds per call, independent of the buffer's size.
+static uint64_t host_fp(const void* host, size_t bytes) {
+  const uint8_t* p = (const uint8_t*)host;
+  uint64_t h = 1469598103934665603ull ^ bytes;
+  constexpr int NS = 64, SB = 16;
+  if (bytes <= (size_t)NS * SB) {
+    for (size_t i = 0; i < bytes; i++) h = (h ^ p[i]) * 1099511628211ull;
+    return h;
+  }
+  const size_t span = bytes - SB;
+  for (int k = 0; k < NS; k++) {
+    const uint8_t* q = p + span * k / (NS - 1);
+    for (int i = 0; i < SB; i++) h = (h ^ q[i]) * 1099511628211ull;
+  }
+  return h;
+}
+
+// Device copy of a persistent host weight buffer, keyed by its address.  A
+// hit also needs the same sampled fingerprint: a different buffer that got
+// the address of a freed one is uploaded afresh.  An in-place rewrite that
+// leaves every sampled byte alone is not detected (moty_hip_weight_forget
+// is the caller's way to announce one).
 static int weight(Dev* d, const void* host, size_t bytes, const void** dev) {
   std::lock_guard<std::mutex> lk(g_mu);
+  const uint64_t fp = host_fp(host, bytes);
   auto it = d->wcache.find(host);
-  if (it != d->wcache.end() && it->second.bytes >= bytes) {
+  if (it != d->wcache.end() && it->second.bytes == bytes && it->second.fp == fp) {
     *dev = it->second.dev;
     return MOTY_OK;
   }
@@ -116,7 +140,7 @@ static int weight(Dev* d, const void* host, size_t bytes, const void** dev) {
     hipFree(p);
     return check_hip(e, "weight upload");
   }
-  d->wcache[host] = WEntry{p, bytes};
+  d->wcache[host] = WEntry{p, bytes, fp};
   *dev = p;
   return MOTY_OK;
 }

@@ -12,6 +12,7 @@ namespace moty {
 struct WEntry {
   void* dev;
   size_t bytes;
+  uint64_t fp;  // sampled content fingerprint of the host buffer at upload
 };
 
 struct Arena {

@@ -118,7 +118,10 @@ def test_matmul_r4_host_dropin(ops, q8):
                 C.c_void_p(d.ctypes.data), S, I, O)
         assert rc == 0, lib.moty_hip_last_error()
         assert same_bits(y, o_matmul_r4(x, q, d, O, q8))
+    # both arrays are cached by address: a later array at the same address
+    # must not find these
     assert lib.moty_hip_weight_forget(C.c_void_p(q.ctypes.data)) == 0
+    assert lib.moty_hip_weight_forget(C.c_void_p(d.ctypes.data)) == 0
 
 
 def o_silu(g, u):
