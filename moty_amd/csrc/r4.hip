@@ -96,42 +96,52 @@ __device__ __forceinline__ int4 r4_hi(int4 w) {
 
 // ---------------------------------------------------------------------------
 // Decode GEMV, S_ <= 3 tokens (all in the per-token kernel's form), I <=
-// 1024*IC.  Workgroup = NT/64 waves; a wave owns one 4-row block.  Order of
-// the loads: the activation rows first, then every 16-byte chunk of the
-// wave's block (lane l takes chunks l, l+64, ...: each load instruction
-// reads 1 KiB of the contiguous block) and one 8-byte scale chunk (the 4
-// rows' f16 scales) per group -- all issued before any is consumed.  The
-// workgroup quantizes the activation rows into LDS from registers (every
-// workgroup derives the same codes).  Each lane forms the exact integer
-// group sums of its chunks (Q8R4: half a row per chunk, the halves joined
-// across the lane pair), fetches its group's scale from the lane that loaded
-// it, and parks the two operands of the chain step, (s - 8*xsum, dd*xs), in
-// the wave's LDS slice ([row][token][group]); one lane per (row, token) then
-// runs acc = fma(a, b, acc) over the groups in order.
-template <bool Q8, int S_, int IC, int NT, bool PAIR = false>
+// 1024*IC.  KS waves share one 4-row block, split along K: chunk index kk
+// (64 lanes x 16 bytes, GPC groups) belongs to part kk % KS, so a block
+// count near the SIMD count still puts several waves on every SIMD.  Order
+// of the loads: the activation rows first, then every 16-byte chunk of the
+// wave's part (each load instruction reads 1 KiB of the contiguous block)
+// with the f16 scale of the chunk's (row, group) -- all issued before any is
+// consumed.  The workgroup quantizes the activation rows into LDS from
+// registers (every workgroup derives the same codes).  Each lane forms the
+// exact integer group sums of its chunks (Q8R4: half a row per chunk, the
+// halves joined across the lane pair) and parks the two operands of the
+// chain step, (s - 8*xsum, dd*xs), in the block's LDS slice
+// ([row][token][group]); after its k-th chunk a part raises its progress
+// flag to k+1.  One lane per (row, token) of part 0 runs acc = fma(a, b,
+// acc) over the groups in order, chunk index by chunk index, each one as
+// soon as its part's flag says it is parked.  Only part 0 ever waits, on
+// flags that every other part raises unconditionally, so every wait ends.
+template <bool Q8, int S_, int IC, int NT, bool PAIR = false, int KS = 1>
 __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, const uint8_t* __restrict__ W,
                                                 const uint16_t* __restrict__ d16, float* __restrict__ y, int S,
                                                 int I, int O) {
   static_assert(!PAIR || S_ == 1, "the fused gate/up form serves one token");
   constexpr int NM = PAIR ? 2 : 1;  // matrices: gate (and up)
   constexpr int GB = Q8 ? 128 : 64;        // bytes per (block, group)
-  constexpr int NCH = IC * (Q8 ? 4 : 2);   // weight chunks per lane
-  constexpr int DCH = (IC + 1) / 2;        // scale chunks (groups) per lane
+  constexpr int NCH = IC * (Q8 ? 4 : 2);   // chunk indices per block
+  static_assert(NCH % KS == 0, "K parts of whole chunks");
+  constexpr int NCW = NCH / KS;            // chunks per lane per wave
+  constexpr int GPC = Q8 ? 8 : 16;         // groups per chunk index
   constexpr int WAVES = NT / MOTY_WAVE;
+  static_assert(WAVES % KS == 0, "whole blocks per workgroup");
+  constexpr int BPW = WAVES / KS;          // blocks per workgroup
   constexpr int XU = (IC * 64 + NT - 1) / NT;  // activation half groups (16 floats) per thread per row
   extern __shared__ __align__(16) int8_t lds[];
+  __shared__ int flag_s[BPW * KS];
   const int nb = I / 32, O4 = (O + 3) / 4;
   const int lane = threadIdx.x % MOTY_WAVE, wv = threadIdx.x / MOTY_WAVE;
-  // LDS: xq [S_][I] | xs [S_][nb] | xm [S_][nb] | per wave: operands [4][S_][nb] float2
+  const int part = wv % KS, bw = wv / KS;
+  // LDS: xq [S_][I] | xs [S_][nb] | xm [S_][nb] | per block: operands [NM*4][S_][nb] float2
   int8_t* xq_s = lds;
   float* xs_s = (float*)(lds + S_ * I);
   int* xm_s = (int*)(xs_s + S_ * nb);
-  float2* op_s = (float2*)(xm_s + S_ * nb) + (size_t)wv * (4 * NM * S_ * nb);
-  int blk = blockIdx.x * WAVES + wv;
+  float2* op_s = (float2*)(xm_s + S_ * nb) + (size_t)bw * (4 * NM * S_ * nb);
+  int blk = blockIdx.x * BPW + bw;
   const bool live = blk < O4;
   blk = live ? blk : O4 - 1;
 
-  // 1. activation rows, then every weight and scale chunk of the block
+  // 1. activation rows, then every weight chunk of the part and its scale
   float4 xr[S_][XU][4];
 #pragma unroll
   for (int t = 0; t < S_; t++)
@@ -145,28 +155,23 @@ __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, con
   // PAIR: W is the row-fused [gate; up] matrix (moty_mat_fuse_rows), the up
   // rows' blocks start O/4 blocks after the gate rows'
   const int nchunk = nb * GB / 16;
-  int4 wc[NM][NCH];
+  int4 wc[NM][NCW];
+  uint16_t dc[NM][NCW];
 #pragma unroll
   for (int m = 0; m < NM; m++) {
     const uint8_t* wb = W + (size_t)(blk + m * O4) * nb * GB;
-#pragma unroll
-    for (int k = 0; k < NCH; k++) {
-      const int ci = lane + 64 * k;
-      wc[m][k] = *(const int4*)(wb + (size_t)(ci < nchunk ? ci : 0) * 16);
-    }
-  }
-  // lane l, chunk k: the 4 rows' f16 scales of group l + 64k
-  uint2 dc[NM][DCH];
-#pragma unroll
-  for (int m = 0; m < NM; m++) {
     const uint16_t* db = d16 + (size_t)(blk + m * O4) * nb * 4;
 #pragma unroll
-    for (int k = 0; k < DCH; k++) {
-      const int g = lane + 64 * k;
-      dc[m][k] = *(const uint2*)(db + (size_t)(g < nb ? g : 0) * 4);
+    for (int k = 0; k < NCW; k++) {
+      const int ci = lane + 64 * (k * KS + part);
+      const int cc = ci < nchunk ? ci : 0;
+      wc[m][k] = *(const int4*)(wb + (size_t)cc * 16);
+      // chunk ci: group ci/4, row ci%4 (Q8R4: group ci/8, row (ci/2)%4)
+      dc[m][k] = db[Q8 ? (cc >> 3) * 4 + ((cc >> 1) & 3) : cc];
     }
   }
   __builtin_amdgcn_sched_barrier(0);
+  if (KS > 1 && threadIdx.x < BPW * KS) flag_s[threadIdx.x] = 0;
 
   // 2. group-32 quantization of the activation rows into LDS (k_quant_g32's arithmetic)
 #pragma unroll
@@ -179,37 +184,35 @@ __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, con
 #pragma unroll
       for (int j = 0; j < 4; j++) v[j] = sel4(ok, xr[t][c][j]);
       uint4 q;
-      float s;
-      const int sum = quant_half_g32(v, q, s);
+      float sc;
+      const int sum = quant_half_g32(v, q, sc);
       if (ok) {
         *(uint4*)(xq_s + t * I + e) = q;
         if ((threadIdx.x & 1) == 0) {
-          xs_s[t * nb + e / 32] = s;
+          xs_s[t * nb + e / 32] = sc;
           xm_s[t * nb + e / 32] = sum;
         }
       }
     }
   __syncthreads();
 
-  // 3./4. per chunk: the exact integer group sum, the group's scale (from
-  // the lane that loaded it: group g = lane/4 + 16k sits in lane g % 64,
-  // chunk k/4 -- Q8R4: lane/8 + 8k, chunk k/8), the chain step's operands;
-  // then lane (m*4 + r)*S_ + t continues row r's chain for token t (PAIR:
-  // m = 1 is the up row) over the chunk's groups in order, while later
-  // chunks may still be in flight.
-  constexpr int GPC = Q8 ? 8 : 16;  // groups per chunk
+  // 3./4. per chunk: the exact integer group sum and the chain step's
+  // operands; then part 0's lane (m*4 + r)*S_ + t continues row r's chain
+  // for token t (PAIR: m = 1 is the up row) over chunk indices k*KS ..
+  // k*KS + KS-1 in order, while later chunks may still be in flight.
+  const bool chain = part == 0 && lane < 4 * NM * S_;
+  const float2* opc = op_s + (lane < 4 * NM * S_ ? lane : 0) * nb;  // lane = (m*4 + r)*S_ + t
+  const bool even = (nb & 1) == 0;  // 16-byte reads of two groups' operands stay aligned
   float acc = 0.f;
 #pragma unroll
-  for (int k = 0; k < NCH; k++) {
-    const int ci = lane + 64 * k;
+  for (int k = 0; k < NCW; k++) {
+    const int ci = lane + 64 * (k * KS + part);
     const int g = Q8 ? (ci >> 3) : (ci >> 2), r = Q8 ? ((ci >> 1) & 3) : (ci & 3), h = Q8 ? (ci & 1) : 0;
     const bool ok = ci < nchunk;
     const int gc = ok ? g : 0;
 #pragma unroll
     for (int m = 0; m < NM; m++) {
-      const uint2 dsrc = dc[m][Q8 ? k / 8 : k / 4];
-      const uint32_t dx = __shfl(dsrc.x, g & 63, 64), dy = __shfl(dsrc.y, g & 63, 64);
-      const float dd = f16_to_f32(((r < 2 ? dx : dy) >> (16 * (r & 1))) & 0xffffu);
+      const float dd = f16_to_f32(dc[m][k]);
 #pragma unroll
       for (int t = 0; t < S_; t++) {
         const int8_t* xg = xq_s + t * I + gc * 32;
@@ -224,23 +227,40 @@ __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, con
         if (ok && h == 0) op_s[((m * 4 + r) * S_ + t) * nb + g] = float2{(float)sacc, dd * xs_s[t * nb + gc]};
       }
     }
+    if (KS > 1 && part != 0) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      if (lane == 0) __hip_atomic_store(&flag_s[bw * KS + part], k + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      continue;
+    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (lane < 4 * NM * S_) {
-      const float2* op = op_s + lane * nb;  // lane = (m*4 + r)*S_ + t with S_ = 1 for PAIR
-      const int g0 = k * GPC, g1 = nb < g0 + GPC ? nb : g0 + GPC;
-      if (g1 - g0 == GPC) {
-        float2 v[GPC];
+    if (chain) {
 #pragma unroll
-        for (int u = 0; u < GPC; u++) v[u] = op[g0 + u];
+      for (int p = 0; p < KS; p++) {
+        if (p > 0) {
+          while (__hip_atomic_load(&flag_s[bw * KS + p], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) <= k)
+            __builtin_amdgcn_s_sleep(1);
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        }
+        const int g0 = (k * KS + p) * GPC, g1 = nb < g0 + GPC ? nb : g0 + GPC;
+        if (g1 - g0 == GPC && even) {
+          const float4* p4 = (const float4*)(opc + g0);
+          float4 v[GPC / 2];
 #pragma unroll
-        for (int u = 0; u < GPC; u++) acc = __fmaf_rn(v[u].x, v[u].y, acc);
-      } else {
-        for (int gg = g0; gg < g1; gg++) acc = __fmaf_rn(op[gg].x, op[gg].y, acc);
+          for (int u = 0; u < GPC / 2; u++) v[u] = p4[u];
+#pragma unroll
+          for (int u = 0; u < GPC / 2; u++) {
+            acc = __fmaf_rn(v[u].x, v[u].y, acc);
+            acc = __fmaf_rn(v[u].z, v[u].w, acc);
+          }
+        } else {
+          for (int gg = g0; gg < g1; gg++) acc = __fmaf_rn(opc[gg].x, opc[gg].y, acc);
+        }
       }
     }
   }
+  if (part != 0) return;
   if (PAIR) {
     const float u = __shfl(acc, (lane + 4) & 63, 64);
     const int o = blk * 4 + lane;
@@ -253,30 +273,51 @@ __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, con
   }
 }
 
-template <int S_, int NT, bool PAIR>
+template <int S_, int NT, bool PAIR, int KS>
 static size_t r4_gemv_lds(int I) {
   const int nb = I / 32;
-  return (size_t)S_ * I + (size_t)S_ * nb * 8 + (size_t)(NT / MOTY_WAVE) * 4 * (PAIR ? 2 : 1) * S_ * nb * 8;
+  return (size_t)S_ * I + (size_t)S_ * nb * 8 + (size_t)(NT / MOTY_WAVE / KS) * 4 * (PAIR ? 2 : 1) * S_ * nb * 8;
 }
 
-template <bool Q8, int S_, int IC, int NT, bool PAIR>
+template <bool Q8, int S_, int IC, int NT, bool PAIR, int KS>
 static int go_r4_gemv(const float* x, const uint8_t* W, const uint16_t* d16, float* y, int S, int I, int O,
                       hipStream_t st) {
-  const int O4 = (O + 3) / 4, waves = NT / MOTY_WAVE;
-  const size_t lds = r4_gemv_lds<S_, NT, PAIR>(I);
-  hipLaunchKernelGGL((k_r4_gemv<Q8, S_, IC, NT, PAIR>), dim3((unsigned)((O4 + waves - 1) / waves)), dim3(NT), lds,
+  const int O4 = (O + 3) / 4, bpw = NT / MOTY_WAVE / KS;
+  const size_t lds = r4_gemv_lds<S_, NT, PAIR, KS>(I);
+  if (lds + 256 > 64 * 1024) return MOTY_EUNSUP;  // 256: the static progress flags
+  hipLaunchKernelGGL((k_r4_gemv<Q8, S_, IC, NT, PAIR, KS>), dim3((unsigned)((O4 + bpw - 1) / bpw)), dim3(NT), lds,
                      st, x, W, d16, y, S, I, O);
   LAUNCH_TRY("k_r4_gemv");
   return MOTY_OK;
 }
 
-// 4-wave workgroups when the LDS fits, else 2-wave ones
+// Waves per block: K is split until the blocks give every SIMD (1024 on the
+// chip) about four waves, within the chunks a lane holds.  Workgroups of
+// 4 * KS... waves as the LDS allows.
 template <bool Q8, int S_, int IC, bool PAIR>
 static int go_r4_gemv_nt(const float* x, const uint8_t* W, const uint16_t* d16, float* y, int S, int I, int O,
                          hipStream_t st) {
-  if (r4_gemv_lds<S_, 256, PAIR>(I) <= 64 * 1024) return go_r4_gemv<Q8, S_, IC, 256, PAIR>(x, W, d16, y, S, I, O, st);
-  if (r4_gemv_lds<S_, 128, PAIR>(I) <= 64 * 1024) return go_r4_gemv<Q8, S_, IC, 128, PAIR>(x, W, d16, y, S, I, O, st);
-  return MOTY_EUNSUP;
+  constexpr int NCH = IC * (Q8 ? 4 : 2);
+  const int O4 = (O + 3) / 4;
+  if constexpr (NCH % 4 == 0 && NCH >= 8) {
+    if (O4 <= 1024) {
+      int rc = go_r4_gemv<Q8, S_, IC, 1024, PAIR, 4>(x, W, d16, y, S, I, O, st);
+      if (rc != MOTY_EUNSUP) return rc;
+      rc = go_r4_gemv<Q8, S_, IC, 512, PAIR, 4>(x, W, d16, y, S, I, O, st);
+      if (rc != MOTY_EUNSUP) return rc;
+    }
+  }
+  if constexpr (NCH % 2 == 0 && NCH >= 4) {
+    if (O4 <= 2048) {
+      int rc = go_r4_gemv<Q8, S_, IC, 512, PAIR, 2>(x, W, d16, y, S, I, O, st);
+      if (rc != MOTY_EUNSUP) return rc;
+      rc = go_r4_gemv<Q8, S_, IC, 256, PAIR, 2>(x, W, d16, y, S, I, O, st);
+      if (rc != MOTY_EUNSUP) return rc;
+    }
+  }
+  int rc = go_r4_gemv<Q8, S_, IC, 256, PAIR, 1>(x, W, d16, y, S, I, O, st);
+  if (rc != MOTY_EUNSUP) return rc;
+  return go_r4_gemv<Q8, S_, IC, 128, PAIR, 1>(x, W, d16, y, S, I, O, st);
 }
 
 // instances: activation float4 per thread and weight chunks per lane stay
