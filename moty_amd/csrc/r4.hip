@@ -98,14 +98,14 @@ __device__ __forceinline__ int4 r4_hi(int4 w) {
 // Decode GEMV, S_ <= 3 tokens (all in the per-token kernel's form), I <=
 // 1024*IC.  KS waves share one 4-row block, split along K: chunk index kk
 // (64 lanes x 16 bytes, GPC groups) belongs to part kk % KS, so a block
-// count near the SIMD count still puts several waves on every SIMD.  Order
-// of the loads: the activation rows first, then every 16-byte chunk of the
-// wave's part (each load instruction reads 1 KiB of the contiguous block)
-// with the f16 scale of the chunk's (row, group) -- all issued before any is
-// consumed.  The workgroup quantizes the activation rows into LDS from
-// registers (every workgroup derives the same codes).  Each lane forms the
-// exact integer group sums of its chunks (Q8R4: half a row per chunk, the
-// halves joined across the lane pair) and parks the two operands of the
+// count near the SIMD count still puts several waves on every SIMD.  The
+// activation rows are loaded and land first; the weight chunks of the part
+// (each load instruction reads 1 KiB of the contiguous block) and the f16
+// scale of each chunk's (row, group) are then kept PD chunks ahead of the
+// one being consumed.  The workgroup quantizes the activation rows into LDS
+// from registers (every workgroup derives the same codes).  Each lane forms
+// the exact integer group sums of its chunks (Q8R4: half a row per chunk,
+// the halves joined across the lane pair) and parks the two operands of the
 // chain step, (s - 8*xsum, dd*xs), in the block's LDS slice
 // ([row][token][group]); after its k-th chunk a part raises its progress
 // flag to k+1.  One lane per (row, token) of part 0 runs acc = fma(a, b,
@@ -122,6 +122,8 @@ __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, con
   constexpr int NCH = IC * (Q8 ? 4 : 2);   // chunk indices per block
   static_assert(NCH % KS == 0, "K parts of whole chunks");
   constexpr int NCW = NCH / KS;            // chunks per lane per wave
+  constexpr int PD = NCW < 4 ? NCW : 4;    // chunks in flight ahead of the one consumed
+  constexpr int P0 = PD < 2 ? PD : 2;      // of them issued before the quantization
   constexpr int GPC = Q8 ? 8 : 16;         // groups per chunk index
   constexpr int WAVES = NT / MOTY_WAVE;
   static_assert(WAVES % KS == 0, "whole blocks per workgroup");
@@ -141,7 +143,7 @@ __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, con
   const bool live = blk < O4;
   blk = live ? blk : O4 - 1;
 
-  // 1. activation rows, then every weight chunk of the part and its scale
+  // 1. activation rows
   float4 xr[S_][XU][4];
 #pragma unroll
   for (int t = 0; t < S_; t++)
@@ -152,28 +154,39 @@ __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, con
 #pragma unroll
       for (int j = 0; j < 4; j++) xr[t][c][j] = src[j];
     }
+  if (KS > 1 && threadIdx.x < BPW * KS) flag_s[threadIdx.x] = 0;
+
+  // 2. weight chunks of the part and their scales, PD chunks ahead: chunk
+  // k + PD is issued just before chunk k is consumed, so the integer dots
+  // and the chain run while the stream is still arriving (a wave that
+  // issued all of its loads first would sit in the issue stall until the
+  // memory path had taken them all).  The activation rows land first (the
+  // wait and the bare barrier: queued behind the weight stream in the CU's
+  // load path and in L2 they would arrive with it), then the first P0
+  // chunks go out before the quantization, the rest of the PD after it.
   // PAIR: W is the row-fused [gate; up] matrix (moty_mat_fuse_rows), the up
   // rows' blocks start O/4 blocks after the gate rows'
   const int nchunk = nb * GB / 16;
   int4 wc[NM][NCW];
   uint16_t dc[NM][NCW];
+  auto issue = [&](int k) {
 #pragma unroll
-  for (int m = 0; m < NM; m++) {
-    const uint8_t* wb = W + (size_t)(blk + m * O4) * nb * GB;
-    const uint16_t* db = d16 + (size_t)(blk + m * O4) * nb * 4;
-#pragma unroll
-    for (int k = 0; k < NCW; k++) {
+    for (int m = 0; m < NM; m++) {
       const int ci = lane + 64 * (k * KS + part);
       const int cc = ci < nchunk ? ci : 0;
-      wc[m][k] = *(const int4*)(wb + (size_t)cc * 16);
+      wc[m][k] = *(const int4*)(W + ((size_t)(blk + m * O4) * nb * GB + (size_t)cc * 16));
       // chunk ci: group ci/4, row ci%4 (Q8R4: group ci/8, row (ci/2)%4)
-      dc[m][k] = db[Q8 ? (cc >> 3) * 4 + ((cc >> 1) & 3) : cc];
+      dc[m][k] = d16[(size_t)(blk + m * O4) * nb * 4 + (Q8 ? (cc >> 3) * 4 + ((cc >> 1) & 3) : cc)];
     }
-  }
+  };
+  MOTY_WAIT_VMCNT(0);
+  __builtin_amdgcn_s_barrier();
+#pragma unroll
+  for (int k = 0; k < P0; k++) issue(k);
   __builtin_amdgcn_sched_barrier(0);
-  if (KS > 1 && threadIdx.x < BPW * KS) flag_s[threadIdx.x] = 0;
 
-  // 2. group-32 quantization of the activation rows into LDS (k_quant_g32's arithmetic)
+  // 3. group-32 quantization of the activation rows into LDS (k_quant_g32's
+  // arithmetic)
 #pragma unroll
   for (int t = 0; t < S_; t++)
 #pragma unroll
@@ -194,18 +207,28 @@ __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, con
         }
       }
     }
+  __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+  for (int k = P0; k < PD; k++) issue(k);
+  __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
 
-  // 3./4. per chunk: the exact integer group sum and the chain step's
+  // 4. per chunk: the exact integer group sum and the chain step's
   // operands; then part 0's lane (m*4 + r)*S_ + t continues row r's chain
   // for token t (PAIR: m = 1 is the up row) over chunk indices k*KS ..
   // k*KS + KS-1 in order, while later chunks may still be in flight.
+  // part 0 carries the serial chain: its wave gets the SIMD's issue
+  // priority over the parts that only form group sums
+  if (KS > 1 && part == 0) __builtin_amdgcn_s_setprio(3);
   const bool chain = part == 0 && lane < 4 * NM * S_;
   const float2* opc = op_s + (lane < 4 * NM * S_ ? lane : 0) * nb;  // lane = (m*4 + r)*S_ + t
   const bool even = (nb & 1) == 0;  // 16-byte reads of two groups' operands stay aligned
   float acc = 0.f;
 #pragma unroll
   for (int k = 0; k < NCW; k++) {
+    if (k + PD < NCW) issue(k + PD);
+    __builtin_amdgcn_sched_barrier(0);
     const int ci = lane + 64 * (k * KS + part);
     const int g = Q8 ? (ci >> 3) : (ci >> 2), r = Q8 ? ((ci >> 1) & 3) : (ci & 3), h = Q8 ? (ci & 1) : 0;
     const bool ok = ci < nchunk;
