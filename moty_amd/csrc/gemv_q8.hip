@@ -5,7 +5,8 @@
 //     xq[s] = qrow_i8(x[s]);  y[s*O+o] = (scale[o]*sx[s]) * (float)dot(W[o], xq[s])
 //
 // MI355X design (HBM-bound, one pass over W).  S = 1 with I <= 4096 takes
-// k_gemv1_q8 (activations quantized per wave in registers); otherwise:
+// k_gemv1_q8 (activations quantized per wave in registers) or, for large
+// matrices, k_gemv1_q8_lds (quantized once per workgroup into LDS); otherwise:
 //  * a wave owns RPW weight rows; each lane streams 16 contiguous bytes per
 //    1 KiB chunk of a row (global_load_dwordx4, fully coalesced), up to four
 //    chunks per row in flight;
@@ -170,7 +171,7 @@ __global__ __launch_bounds__(GEMV_NT) void k_gemv_q8(const float* __restrict__ x
     }
 }
 
-// S = 1, I <= 4096: the activation row never touches LDS.  Lane l of every
+// S = 1, I <= 4096, small matrices: the activation row never touches LDS.  Lane l of every
 // wave loads elements [c*1024 + 16l, +16) of each 1 KiB chunk c -- exactly
 // its dot inputs -- so a wave-max gives the row's amax and each wave
 // quantizes in registers (qrow_i8 bit for bit), with no workgroup barrier.
@@ -249,6 +250,113 @@ __global__ __launch_bounds__(NW * MOTY_WAVE) void k_gemv1_q8(const float* __rest
   if (lane < RPW && o < O) y[o] = v;
 }
 
+// S = 1, I <= 4096, large matrices (the weight stream is long enough for
+// its queueing to matter).  The workgroup loads the activation row once
+// (thread t takes XE contiguous values) and waits for it before any weight
+// load is issued: queued behind the weight stream, in the CU's load path
+// and in L2, it would arrive with the weights.  Then it streams its
+// weights: wave w owns
+// RPW rows, lane l reads bytes [c*1024 + 16l, +16) of each 1 KiB chunk c,
+// with non-temporal loads (read once, kept out of the caches' way).  While
+// they fly the row is quantized (qrow_i8 bit for bit: the row's amax from a
+// wave max and an LDS exchange across the waves) into LDS, from where each
+// lane takes exactly the 16 codes per chunk its dot needs.
+template <int NC, int RPW, bool PAIR, int NW>
+__global__ __launch_bounds__(NW * MOTY_WAVE) void k_gemv1_q8_lds(const float* __restrict__ x, const int8_t* __restrict__ W,
+                                                      const float* __restrict__ scale,
+                                                      const int8_t* __restrict__ W2,
+                                                      const float* __restrict__ scale2, float* __restrict__ y,
+                                                      int I, int O) {
+  constexpr int XE = 16 * NC / NW;  // activation values per thread (a multiple of 4)
+  __shared__ __align__(16) int8_t xq_s[NC * CHUNK];
+  __shared__ float red[NW];
+  const int lane = threadIdx.x % MOTY_WAVE, wv = threadIdx.x / MOTY_WAVE;
+  const int o0 = (blockIdx.x * NW + wv) * RPW;
+  const int e0 = threadIdx.x * XE;
+  float4 xv[XE / 4];
+#pragma unroll
+  for (int j = 0; j < XE / 4; j++) {
+    const int k = e0 + 4 * j;
+    xv[j] = *(const float4*)(x + (k < I ? k : 0));
+  }
+  MOTY_WAIT_VMCNT(0);
+  __builtin_amdgcn_s_barrier();
+  int4 wq[RPW][NC], wq2[RPW][NC];
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const int o = o0 + r < O ? o0 + r : O - 1;
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+      const int k = c * CHUNK + lane * 16;
+      const int kc = k < I ? k : 0;
+      wq[r][c] = ldnt16(W + (int64_t)o * I + kc);
+      if (PAIR) wq2[r][c] = ldnt16(W2 + (int64_t)o * I + kc);
+    }
+  }
+  // lane r holds the scales of the wave's row r, loaded with the weights so
+  // the epilogue waits on no further memory latency
+  float sc = 0.f, sc2 = 0.f;
+  {
+    const int o = o0 + (lane < RPW ? lane : 0);
+    sc = scale[o < O ? o : O - 1];
+    if (PAIR) sc2 = scale2[o < O ? o : O - 1];
+  }
+  // keep the scheduler from sinking weight loads below the quantization
+  __builtin_amdgcn_sched_barrier(0);
+  // past the row end x was read from a clamped address: zero it (the
+  // weights there are multiplied by these zeros)
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < XE / 4; j++) {
+    xv[j] = sel4(e0 + 4 * j < I, xv[j]);
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(xv[j].x), fabsf(xv[j].y)), fmaxf(fabsf(xv[j].z), fabsf(xv[j].w))));
+  }
+  amax = wave_max_f32(amax);
+  if (NW > 1) {
+    if (lane == 0) red[wv] = amax;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NW; i++) amax = fmaxf(amax, red[i]);
+  }
+  float sx = amax / 127.f;
+  if (sx < 1e-12f) sx = 1e-12f;
+  const float inv = 1.f / sx;
+#pragma unroll
+  for (int j = 0; j < XE / 4; j++)
+    *(uint32_t*)(xq_s + e0 + 4 * j) =
+        (uint32_t)(rne_int(xv[j].x * inv) & 0xff) | ((uint32_t)(rne_int(xv[j].y * inv) & 0xff) << 8) |
+        ((uint32_t)(rne_int(xv[j].z * inv) & 0xff) << 16) | ((uint32_t)(rne_int(xv[j].w * inv) & 0xff) << 24);
+  __syncthreads();
+  int4 xq[NC];
+#pragma unroll
+  for (int c = 0; c < NC; c++) xq[c] = *(const int4*)(xq_s + c * CHUNK + lane * 16);
+  int acc[RPW], acc2[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    acc[r] = 0;
+    acc2[r] = 0;
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+      acc[r] = dot16(wq[r][c], xq[c], acc[r]);
+      if (PAIR) acc2[r] = dot16(wq2[r][c], xq[c], acc2[r]);
+    }
+    acc[r] = wave_sum_i32(acc[r]);
+    if (PAIR) acc2[r] = wave_sum_i32(acc2[r]);
+  }
+  // lane r finishes row o0 + r; computed on every lane (wave-wide cost is
+  // the same) so the scale loads above stay where they were issued
+  int a = acc[0], a2 = acc2[0];
+#pragma unroll
+  for (int r = 1; r < RPW; r++) {
+    a = lane == r ? acc[r] : a;
+    a2 = lane == r ? acc2[r] : a2;
+  }
+  float v = (sc * sx) * (float)a;
+  if (PAIR) v = ref_silu_mul(v, (sc2 * sx) * (float)a2);
+  const int o = o0 + lane;
+  if (lane < RPW && o < O) y[o] = v;
+}
+
 template <int NC, bool PAIR>
 static int launch_1(const float* x, const int8_t* W, const float* scale, const int8_t* W2, const float* scale2,
                     float* y, int I, int O, hipStream_t st) {
@@ -261,10 +369,18 @@ static int launch_1(const float* x, const int8_t* W, const float* scale, const i
   const int waves = (O + rpw - 1) / rpw;
   const int nw = waves > 512 ? 4 : (waves > 256 ? 2 : 1);
   const unsigned nb = (unsigned)((waves + nw - 1) / nw);
+  // a long weight stream: the shared-activation kernel (activation row
+  // first, quantized once per workgroup, fewer registers per wave); a short
+  // one: the per-wave kernel, whose activation and weight latencies overlap
+  const bool big = (int64_t)O * I * (PAIR ? 2 : 1) >= ((int64_t)16 << 20);
 #define L1(R, N)                                                                                              \
   if (rpw == R && nw == N) {                                                                                 \
-    hipLaunchKernelGGL((k_gemv1_q8<NC, R, PAIR, N>), dim3(nb), dim3(N * MOTY_WAVE), 0, st, x, W, scale, W2,   \
-                       scale2, y, I, O);                                                                     \
+    if (big)                                                                                                 \
+      hipLaunchKernelGGL((k_gemv1_q8_lds<NC, R, PAIR, N>), dim3(nb), dim3(N * MOTY_WAVE), 0, st, x, W, scale, \
+                         W2, scale2, y, I, O);                                                               \
+    else                                                                                                     \
+      hipLaunchKernelGGL((k_gemv1_q8<NC, R, PAIR, N>), dim3(nb), dim3(N * MOTY_WAVE), 0, st, x, W, scale, W2, \
+                         scale2, y, I, O);                                                                   \
     LAUNCH_TRY("k_gemv1_q8");                                                                                \
     return MOTY_OK;                                                                                          \
   }

@@ -106,7 +106,9 @@ Q8_CASES = [(1, 1024, 3072), (1, 3072, 1024), (2, 1024, 100), (3, 48, 24), (4, 2
             (1, 16384, 64), (5, 1024, 256), (8, 3072, 96), (64, 1024, 1024), (512, 1024, 2048),
             (130, 2048, 200), (33, 16, 17), (1024, 1024, 4096), (256, 1040, 8192), (200, 3072, 1000),
             # K % 128 == 0 past the GEMV: the DMA-staged GEMM, one-block and ragged tiles
-            (70, 128, 33), (9, 256, 1), (130, 384, 65), (600, 4096, 100), (5, 128, 7)]
+            (70, 128, 33), (9, 256, 1), (130, 384, 65), (600, 4096, 100), (5, 128, 7),
+            # S = 1 past 16 MiB of weights: the shared-activation GEMV, full and ragged
+            (1, 4096, 4096), (1, 3088, 5500), (1, 1040, 16200)]
 
 
 @pytest.mark.parametrize("S,I,O", Q8_CASES)
