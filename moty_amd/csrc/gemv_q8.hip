@@ -267,7 +267,8 @@ __global__ __launch_bounds__(NW * MOTY_WAVE) void k_gemv1_q8_lds(const float* __
                                                       const int8_t* __restrict__ W2,
                                                       const float* __restrict__ scale2, float* __restrict__ y,
                                                       int I, int O) {
-  constexpr int XE = 16 * NC / NW;  // activation values per thread (a multiple of 4)
+  constexpr int XE = 16 * NC / NW;  // activation values per thread
+  static_assert(XE % 4 == 0 && XE > 0, "whole float4 of the activation row per thread");
   __shared__ __align__(16) int8_t xq_s[NC * CHUNK];
   __shared__ float red[NW];
   const int lane = threadIdx.x % MOTY_WAVE, wv = threadIdx.x / MOTY_WAVE;
@@ -370,17 +371,28 @@ static int launch_1(const float* x, const int8_t* W, const float* scale, const i
   const int nw = waves > 512 ? 4 : (waves > 256 ? 2 : 1);
   const unsigned nb = (unsigned)((waves + nw - 1) / nw);
   // a long weight stream: the shared-activation kernel (activation row
-  // first, quantized once per workgroup, fewer registers per wave); a short
-  // one: the per-wave kernel, whose activation and weight latencies overlap
-  const bool big = (int64_t)O * I * (PAIR ? 2 : 1) >= ((int64_t)16 << 20);
+  // first, quantized once per workgroup, fewer registers per wave) in
+  // 8-wave workgroups, one row per wave (two past 8192 rows: plain matrices
+  // only) -- the best of a rows/wave x waves/workgroup sweep on MI355X over
+  // 4096x4096, 12288x4096 and the fused 2 x 12288x4096; a short one: the
+  // per-wave kernel, whose activation and weight latencies overlap
+  if ((int64_t)O * I * (PAIR ? 2 : 1) >= ((int64_t)16 << 20)) {
+    constexpr int NWL = (4 * NC) % 8 == 0 ? 8 : 4;  // whole float4 of the row per thread
+    const int r = (!PAIR && O > 8192) ? 2 : 1;
+    const unsigned nbl = (unsigned)(((O + r - 1) / r + NWL - 1) / NWL);
+    if (r == 2)
+      hipLaunchKernelGGL((k_gemv1_q8_lds<NC, 2, PAIR, NWL>), dim3(nbl), dim3(NWL * MOTY_WAVE), 0, st, x, W, scale,
+                         W2, scale2, y, I, O);
+    else
+      hipLaunchKernelGGL((k_gemv1_q8_lds<NC, 1, PAIR, NWL>), dim3(nbl), dim3(NWL * MOTY_WAVE), 0, st, x, W, scale,
+                         W2, scale2, y, I, O);
+    LAUNCH_TRY("k_gemv1_q8_lds");
+    return MOTY_OK;
+  }
 #define L1(R, N)                                                                                              \
   if (rpw == R && nw == N) {                                                                                 \
-    if (big)                                                                                                 \
-      hipLaunchKernelGGL((k_gemv1_q8_lds<NC, R, PAIR, N>), dim3(nb), dim3(N * MOTY_WAVE), 0, st, x, W, scale, \
-                         W2, scale2, y, I, O);                                                               \
-    else                                                                                                     \
-      hipLaunchKernelGGL((k_gemv1_q8<NC, R, PAIR, N>), dim3(nb), dim3(N * MOTY_WAVE), 0, st, x, W, scale, W2, \
-                         scale2, y, I, O);                                                                   \
+    hipLaunchKernelGGL((k_gemv1_q8<NC, R, PAIR, N>), dim3(nb), dim3(N * MOTY_WAVE), 0, st, x, W, scale, W2,   \
+                       scale2, y, I, O);                                                                     \
     LAUNCH_TRY("k_gemv1_q8");                                                                                \
     return MOTY_OK;                                                                                          \
   }
