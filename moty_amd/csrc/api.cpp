@@ -135,7 +135,10 @@ static int weight(Dev* d, const void* host, size_t bytes, const void** dev) {
   void* p = nullptr;
   hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
   if (e != hipSuccess) return check_hip(e, "weight hipMalloc");
-  e = hipMemcpy(p, host, bytes, hipMemcpyHostToDevice);
+  // on the library's stream, ahead of every kernel that reads the copy: a
+  // plain hipMemcpy from pageable memory may return before its DMA lands,
+  // and the library's (non-blocking) stream does not wait for the null stream
+  e = hipMemcpyAsync(p, host, bytes, hipMemcpyHostToDevice, d->stream);
   if (e != hipSuccess) {
     hipFree(p);
     return check_hip(e, "weight upload");

@@ -5,7 +5,6 @@ through the C-ABI, and the weight cache behind them: keyed by host address,
 re-uploaded when a different buffer takes a freed address or after
 moty_hip_weight_forget."""
 import ctypes as C
-import os
 
 import numpy as np
 import pytest
@@ -49,10 +48,32 @@ def test_matmul_q_s_host(lib, S, I, O):
         forget(lib, q, s)
 
 
+@pytest.fixture(scope="module")
+def idot4_env(lib):
+    """The library reads IDOT4 from the process environment at its first
+    host-pointer grouped-int4 call (as nn/matmul.c:171 does).  The C
+    environment, not os.environ, is what it sees -- the compiled reference's
+    ref_init sets IDOT4 with setenv when test modules are collected -- so
+    read it there and make that first call now, latching the same value."""
+    libc = C.CDLL(None)
+    libc.getenv.restype, libc.getenv.argtypes = C.c_char_p, [C.c_char_p]
+    libc.atoi.restype, libc.atoi.argtypes = C.c_int, [C.c_char_p]
+    v = libc.getenv(b"IDOT4")
+    on = v is not None and libc.atoi(v) != 0
+    x = np.zeros((1, 64), np.float32)
+    q4 = np.zeros((1, 32), np.uint8)
+    s = np.ones((1, 2), np.float32)
+    y = np.empty((1, 1), np.float32)
+    try:
+        assert lib.moty_hip_matmul_i4_grouped_s(P(y), P(x), P(q4), P(s), 1, 64, 1, 32) == 0
+    finally:
+        forget(lib, q4, s)
+    return on
+
+
 @pytest.mark.parametrize("S,I,O", [(1, 1024, 512), (3, 256, 70), (17, 2048, 96), (1, 4096, 64)])
-def test_matmul_i4_grouped_s_host(lib, S, I, O):
-    # IDOT4 is read from the environment once per process (nn/matmul.c:171)
-    idot4 = os.environ.get("IDOT4", "0") not in ("", "0") and I % 64 == 0 and I <= 16384
+def test_matmul_i4_grouped_s_host(lib, idot4_env, S, I, O):
+    idot4 = idot4_env and I % 64 == 0 and I <= 16384
     say("dropin i4g", S, I, O, idot4)
     q4, s = o_pack_int4_grouped(randn(3 + I, (O, I), 0.02), 32)
     x = randn(4 + S, (S, I))
