@@ -39,6 +39,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on each CPU baseline sample")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only launch the dominant kernel on distinct weights and a 64 MiB copy (for rocprofv3 --pmc)")
+    ap.add_argument("--only", choices=["c2", "c3", "c3r4", "c4", "q8gemv"],
+                    help="run one config alone and print its JSON object (for rocprofv3 runs of a single config)")
     return ap.parse_args()
 
 
@@ -528,6 +530,16 @@ def main():
     c = Ctx(torch, ops)
     if args.pmc_probe:
         pmc_probe(c)
+        return
+    if args.only:
+        one = {"c2": lambda: bench_c2(c, args.steps, args.warmup),
+               "c3": lambda: bench_c3(c, args.steps, args.warmup),
+               "c3r4": lambda: bench_c3_r4(c, args.steps, args.warmup),
+               "q8gemv": lambda: bench_q8_gemv_sizes(c, args.steps, args.warmup),
+               "c4": lambda: {k2: v for k2, v in bench_moe(
+                   c, 3, 256, 64, 8, 1024, 2048, 0, moty_amd.ORDER_TOPK, args.steps, args.warmup,
+                   label="C4 OLMoE MoE layer Q8, T=256").items() if k2 not in ("x", "Wr", "layer0")}}[args.only]()
+        print(json.dumps(one), flush=True)
         return
 
     log("C1 decode FFN")
