@@ -368,7 +368,7 @@ static int launch_1(const float* x, const int8_t* W, const float* scale, const i
   int rpw = 4;
   while (rpw > 1 && (O + rpw - 1) / rpw < 256) rpw >>= 1;
   const int waves = (O + rpw - 1) / rpw;
-  const int nw = waves > 512 ? 4 : (waves > 256 ? 2 : 1);
+  const int nw = waves > 768 ? 4 : (waves + 255) / 256;  // one workgroup per CU, up to 4 waves each
   const unsigned nb = (unsigned)((waves + nw - 1) / nw);
   // a long weight stream: the shared-activation kernel (activation row
   // first, quantized once per workgroup, fewer registers per wave) in
@@ -396,7 +396,7 @@ static int launch_1(const float* x, const int8_t* W, const float* scale, const i
     LAUNCH_TRY("k_gemv1_q8");                                                                                \
     return MOTY_OK;                                                                                          \
   }
-  L1(4, 4) L1(4, 2) L1(4, 1) L1(2, 2) L1(2, 1) L1(1, 2) L1(1, 1)
+  L1(4, 4) L1(4, 3) L1(4, 2) L1(4, 1) L1(2, 2) L1(2, 1) L1(1, 2) L1(1, 1)
 #undef L1
   return MOTY_EUNSUP;
 }
