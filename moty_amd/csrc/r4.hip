@@ -391,7 +391,7 @@ constexpr int R4M_NT = 256;
 constexpr int R4M_KG = 4;                 // groups per K block
 constexpr int R4M_AS = R4M_KG * 32 + 16;  // A row stride (bytes)
 
-template <bool Q8>
+template <bool Q8, bool TILE = false>
 __global__ __launch_bounds__(R4M_NT, 2) void k_r4_gemm(const int8_t* __restrict__ xq, const float* __restrict__ xs,
                                                        const int32_t* __restrict__ xm,
                                                        const uint8_t* __restrict__ W,
@@ -530,7 +530,8 @@ __global__ __launch_bounds__(R4M_NT, 2) void k_r4_gemm(const int8_t* __restrict_
         for (int q = 0; q < 4; q++) {
           const int tb = wm * 32 + 8 * q + 4 * hk;
           const float4 xv = *(const float4*)(sX + gg * 64 + tb);
-          const int4 mv = *(const int4*)(sM + gg * 64 + tb);
+          // every token in the tile kernel's form (S % 4 == 0): m8 is 0 throughout
+          const int4 mv = TILE ? int4{0, 0, 0, 0} : *(const int4*)(sM + gg * 64 + tb);
           const float4 cv = *(const float4*)(sC + gg * 64 + tb);
           accf[4 * q + 0] = __fmaf_rn(-dd, cv.x, __fmaf_rn((float)(dsum[4 * q + 0] + mv.x), dd * xv.x, accf[4 * q + 0]));
           accf[4 * q + 1] = __fmaf_rn(-dd, cv.y, __fmaf_rn((float)(dsum[4 * q + 1] + mv.y), dd * xv.y, accf[4 * q + 1]));
@@ -574,6 +575,8 @@ int launch_r4_matmul(bool q8, const float* x, const uint8_t* W, const uint16_t* 
   dim3 grid((O + 63) / 64, (S + 63) / 64);
   if (q8)
     hipLaunchKernelGGL(k_r4_gemm<true>, grid, dim3(R4M_NT), 0, st, xq, xs, xm, W, d16, y, S, I, O);
+  else if (S % 4 == 0)  // every token in the tile kernel's form
+    hipLaunchKernelGGL((k_r4_gemm<false, true>), grid, dim3(R4M_NT), 0, st, xq, xs, xm, W, d16, y, S, I, O);
   else
     hipLaunchKernelGGL(k_r4_gemm<false>, grid, dim3(R4M_NT), 0, st, xq, xs, xm, W, d16, y, S, I, O);
   LAUNCH_TRY("k_r4_gemm");
