@@ -104,12 +104,14 @@ class Ctx:
         return e0.elapsed_time(e1) / 1e3 / n, n
 
 
-def pmc_traffic(name):
+def pmc_traffic(name, key=None):
     """HBM bytes per launch of a kernel from its committed rocprofv3 PMC
-    summary (profiles/<name>.md, line `traffic_bytes_per_launch: N`)."""
+    summary (profiles/<name>.md, line `traffic_bytes_per_launch: N`, or
+    `traffic_bytes_per_launch[key]: N` for one of several kernels)."""
+    tag = "traffic_bytes_per_launch%s:" % ("[%s]" % key if key else "")
     try:
         for line in open(os.path.join(ROOT, "profiles", name + ".md")):
-            if line.startswith("traffic_bytes_per_launch:"):
+            if line.startswith(tag):
                 return int(line.split(":")[1])
     except OSError:
         pass
@@ -336,7 +338,9 @@ def bench_q8_gemv_sizes(c, steps, warmup):
         y = torch.empty((1, O), device="cuda:0")
         t, n = c.time_steps([lambda w=w: ops.matmul_q_s(x, w[0], w[1], out=y) for w in copies], steps, warmup)
         algo = wbytes + (I + O) * 4
-        res["gemv_%dx%d" % (O, I)] = {"us": round(t * 1e6, 3), **roofline("hbm", algo / t / 1e9, HBM_PEAK_GBS, "GB/s")}
+        key = "gemv_%dx%d" % (O, I)
+        res[key] = {"us": round(t * 1e6, 3),
+                    **roofline("hbm", algo / t / 1e9, HBM_PEAK_GBS, "GB/s", pmc_traffic("q8_gemv_large_pmc", key))}
     D, I = 4096, 12288
     wbytes = 2 * (I * D + I * 4)
     g = c.gen(7, 2)
@@ -346,7 +350,9 @@ def bench_q8_gemv_sizes(c, steps, warmup):
     t, n = c.time_steps([lambda w=w: ops.gate_up_silu_q8(x, w[0], w[1], w[2], w[3], out=h) for w in copies],
                         steps, warmup)
     algo = wbytes + (D + I) * 4
-    res["gate_up_silu_8B"] = {"us": round(t * 1e6, 3), **roofline("hbm", algo / t / 1e9, HBM_PEAK_GBS, "GB/s")}
+    res["gate_up_silu_8B"] = {"us": round(t * 1e6, 3),
+                              **roofline("hbm", algo / t / 1e9, HBM_PEAK_GBS, "GB/s",
+                                         pmc_traffic("q8_gemv_large_pmc", "gate_up_silu_8B"))}
     return {"workload": "Q8 decode GEMV at larger shapes (S = 1): 4096 x 4096, 12288 x 4096, fused gate/up + SiLU "
                         "over 2 x 12288 x 4096", **res}
 
