@@ -39,7 +39,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on each CPU baseline sample")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only launch the dominant kernel on distinct weights and a 64 MiB copy (for rocprofv3 --pmc)")
-    ap.add_argument("--only", choices=["c2", "c3", "c3r4", "c4", "q8gemv"],
+    ap.add_argument("--only", choices=["c2", "c3", "c3r4", "c4", "c5", "q8gemv"],
                     help="run one config alone and print its JSON object (for rocprofv3 runs of a single config)")
     return ap.parse_args()
 
@@ -544,7 +544,11 @@ def main():
                "q8gemv": lambda: bench_q8_gemv_sizes(c, args.steps, args.warmup),
                "c4": lambda: {k2: v for k2, v in bench_moe(
                    c, 3, 256, 64, 8, 1024, 2048, 0, moty_amd.ORDER_TOPK, args.steps, args.warmup,
-                   label="C4 OLMoE MoE layer Q8, T=256").items() if k2 not in ("x", "Wr", "layer0")}}[args.only]()
+                   label="C4 OLMoE MoE layer Q8, T=256").items() if k2 not in ("x", "Wr", "layer0")},
+               "c5": lambda: {k2: v for k2, v in bench_moe(
+                   c, 4, 1072, 128, 8, 768, 2048, 1, moty_amd.ORDER_EXPERT, args.steps, args.warmup,
+                   label="C5 Qwen3-30B-A3B MoE layer Q8, T=1072, uniform").items()
+                   if k2 not in ("x", "Wr", "layer0")}}[args.only]()
         print(json.dumps(one), flush=True)
         return
 
