@@ -279,12 +279,30 @@ def bench_c2(c, steps, warmup):
         return f
     t, n = c.time_steps([step(w) for w in copies], max(16, steps // 8), max(4, warmup // 8))
     ops_int = 2 * M * sum(O * I for _, O, I in shapes)
+
+    # the three GEMMs alone, and the platform library's int8 GEMM
+    # (torch._int_mm: hipBLASLt, int32 out, no scale epilogue) on the same
+    # operands, timed alike: a yardstick for the MFMA fraction above
+    def gemms(ws):
+        return lambda: [ops.matmul_q8_preq(xq[I], sx[I], q, s, out=ys[I]) for I, (q, s) in zip((1024, 2048, 3072), ws)]
+
+    def lib_gemms(ws):
+        return lambda: [torch._int_mm(xq[I], q.t()) for I, (q, _) in zip((1024, 2048, 3072), ws)]
+    nt, nw = max(16, steps // 8), max(4, warmup // 8)
+    tg, _ = c.time_steps([gemms(w) for w in copies], nt, nw)
+    try:
+        tl, _ = c.time_steps([lib_gemms(w) for w in copies], nt, nw)
+        lib_ref = {"ms_per_step": tl * 1e3, "tops": round(ops_int / tl / 1e12, 1)}
+    except Exception as e:  # the library may not take a shape
+        lib_ref = {"error": str(e)[:160]}
     algo = wbytes + M * (1024 + 2048 + 3072) * 4 + sum(M * O * 4 for _, O, _ in shapes)
     return {"workload": "C2 Qwen3-0.6B layer, 7 Q8 projections as prefill GEMMs, M=512 "
                         "(q/k/v/gate/up fused by rows: one GEMM N=10240, K=1024; o; down)",
             "ms_per_step": t * 1e3, "steps": n,
             "roofline": roofline("mfma", ops_int / t / 1e12, INT8_PEAK_TOPS, "TOP/s"),
-            "hbm_gbs": round(algo / t / 1e9, 1)}
+            "hbm_gbs": round(algo / t / 1e9, 1),
+            "gemms_only": {"ms_per_step": tg * 1e3, "tops": round(ops_int / tg / 1e12, 1)},
+            "library_int_mm": lib_ref}
 
 
 def bench_c3(c, steps, warmup):
