@@ -3,6 +3,7 @@ declares (no compute without a GPU), and the host-side error behaviour."""
 import os
 import re
 import subprocess
+import sys
 
 import pytest
 
@@ -48,3 +49,11 @@ def test_no_device_reports_error_not_abort():
     rc = moty_amd.lib().moty_hip_init(0)
     assert rc != 0
     assert moty_amd.lib().moty_hip_last_error()
+
+
+def test_bench_refuses_several_gpus():
+    # one GPU per box: --gpus N > 1 exits with a message before touching a device
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=60)
+    assert r.returncode == 2
+    assert "measures one GPU" in r.stderr and not r.stdout
