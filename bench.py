@@ -75,10 +75,17 @@ class Ctx:
         return self.ops.pack_int4_grouped(w, 32)
 
     def time_steps(self, fns, steps, warmup):
-        """Capture one step per callable into a HIP graph, replay it; returns
-        (seconds per step, steps timed).  Events sit on the stream the library
-        launches on (torch's current stream)."""
+        """Time exactly `steps` steps: step k runs fns[k % len(fns)] (the
+        weight copies rotate), captured into one HIP graph; `warmup` steps
+        from a second graph run just before it on
+        the same stream, so the timed graph is queued while the GPU is still
+        busy and no launch gap enters the timed region.  Events sit on the
+        stream the library launches on (torch's current stream).  Returns
+        (seconds per step, steps timed)."""
         torch = self.torch
+        n = len(fns)
+        steps = max(1, int(steps))
+        warmup = max(1, int(warmup))
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
@@ -86,22 +93,29 @@ class Ctx:
                 f()
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for f in fns:
-                f()
-        reps = max(1, -(-steps // len(fns)))
-        for _ in range(max(1, -(-warmup // len(fns)))):
-            g.replay()
+
+        def capture(first, count):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for k in range(count):
+                    fns[(first + k) % n]()
+            return g
+        timed = capture(0, steps)
+        # the warm-up steps run the copies that precede copy 0 in cyclic
+        # order, ending with copy n-1: every timed copy is then either
+        # untouched by the warm-up or was touched at its start, with the
+        # rest of the rotation (more than the 256 MB Infinity Cache) after it
+        warm = capture((-warmup) % n, warmup)
+        warm.replay()  # first replay of each graph uploads it
+        timed.replay()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        warm.replay()
         e0.record()
-        for _ in range(reps):
-            g.replay()
+        timed.replay()
         e1.record()
         torch.cuda.synchronize()
-        n = reps * len(fns)
-        return e0.elapsed_time(e1) / 1e3 / n, n
+        return e0.elapsed_time(e1) / 1e3 / steps, steps
 
 
 def pmc_traffic(name, key=None):

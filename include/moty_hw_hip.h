@@ -12,11 +12,16 @@
  *     stream) and returns without synchronising.
  *
  * Every function returns MOTY_HIP_OK (0) or an error code, and never aborts;
- * moty_hip_last_error() describes the last failure.  A caller that keeps a
- * CPU path (as engines/glm.c:798-810 does for its CUDA matmul) falls back
- * on a nonzero return.  Calls share library-owned scratch per device and are
- * not re-entrant, like the reference's process-static activation buffers
- * (nn/matmul.c:55-58).
+ * moty_hip_last_error() describes the failure of this thread's last call
+ * (empty after a call that succeeded).  A caller that keeps a CPU path (as
+ * engines/glm.c:798-810 does for its CUDA matmul) falls back on a nonzero
+ * return.  Calls share library-owned scratch per device and are not
+ * re-entrant from several host threads at once, like the reference's
+ * process-static activation buffers (nn/matmul.c:55-58).  Sequential _dev
+ * calls may use different streams: a call whose stream differs from the
+ * previous scratch user's is ordered behind that stream's queued work.
+ * Under HIP graph capture that ordering is not added: capture the calls of
+ * one device on one stream.
  *
  * Numerics match the reference's x86-64 AVX512-VNNI build: int8 activations
  * and int32 accumulators bit-exact, float steps in the reference's order
@@ -165,7 +170,9 @@ int moty_hip_gguf_repack_q4_0(const uint8_t *blocks, uint8_t *q4, float *qs, int
 int moty_hip_weight_forget(const void *host_ptr);
 
 /* HwBackend.matmul_i8 slot (hw/hw_backend.h:57-58), which returns void:
- * on failure y is left untouched and moty_hip_last_error() says why. */
+ * on failure every y[S*O] is set to a quiet NaN and moty_hip_last_error()
+ * says why (it is "" after a call that succeeded).  A caller that keeps the
+ * CPU path calls moty_hip_matmul_q_s instead and falls back on nonzero. */
 void moty_hip_hw_matmul_i8(float *y, const float *x, const int8_t *q, const float *scale, int S, int I, int O);
 
 /* ---------------- device-pointer entry points ---------------- */

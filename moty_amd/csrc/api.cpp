@@ -60,6 +60,7 @@ static int dev_init(int d) {
 }
 
 int cur(Dev** out) {
+  g_err[0] = 0;  // an entry point that succeeds leaves no stale message
   if (t_dev < 0) {
     int rc = dev_init(0);
     if (rc) return rc;
@@ -94,6 +95,29 @@ int arena_get(Arena& a, size_t bytes, void** p) {
   return MOTY_OK;
 }
 
+static bool capturing(hipStream_t st) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
+int scratch_get(Dev* d, size_t bytes, hipStream_t st, void** p) {
+  if (d->scr_used && d->scr_stream != st && !capturing(st) && !capturing(d->scr_stream)) {
+    if (!d->scr_ev) HIP_TRY(hipEventCreateWithFlags(&d->scr_ev, hipEventDisableTiming));
+    // every call queues its work before returning, so recording on the
+    // previous stream now marks the end of the work that used the arena
+    if (hipEventRecord(d->scr_ev, d->scr_stream) == hipSuccess) {
+      HIP_TRY(hipStreamWaitEvent(st, d->scr_ev, 0));
+    } else {
+      (void)hipGetLastError();  // the previous stream is gone: wait for everything instead
+      HIP_TRY(hipDeviceSynchronize());
+    }
+  }
+  int rc = arena_get(d->scratch, bytes, p);
+  if (rc) return rc;
+  d->scr_stream = st;
+  d->scr_used = true;
+  return MOTY_OK;
+}
 
 // Fingerprint of a host buffer from 64 evenly spaced 16-byte samples (the
 // first and last bytes included): FNV-1a over the sampled bytes.  A few
@@ -194,6 +218,10 @@ int moty_hip_shutdown(void) {
     d.io = Arena();
     hipStreamDestroy(d.stream);
     d.stream = nullptr;
+    if (d.scr_ev) hipEventDestroy(d.scr_ev);
+    d.scr_ev = nullptr;
+    d.scr_used = false;
+    d.scr_stream = nullptr;
     d.ready = false;
   }
   t_dev = -1;
@@ -248,7 +276,7 @@ int moty_hip_matmul_q_s_dev(float* y, const float* x, const int8_t* q, const flo
   if (S <= GEMV_MAX_S) return launch_gemv_q8(x, q, scale, nullptr, nullptr, y, S, I, O, st);
   void* sp;
   const size_t xb = al256((size_t)S * I);
-  int rc = arena_get(d->scratch, xb + al256((size_t)S * 4), &sp);
+  int rc = scratch_get(d, xb + al256((size_t)S * 4), st, &sp);
   if (rc) return rc;
   int8_t* xq = (int8_t*)sp;
   float* sx = (float*)((char*)sp + xb);
@@ -268,7 +296,7 @@ int moty_hip_matmul_i4_grouped_s_dev(float* y, const float* x, const uint8_t* q4
     if (S <= 4) return launch_gemv_i4g(x, q4, scale, nullptr, nullptr, y, S, I, O, st);
     void* sp;
     const size_t xb = al256((size_t)S * I);
-    int rc = arena_get(d->scratch, xb + al256((size_t)S * 4), &sp);
+    int rc = scratch_get(d, xb + al256((size_t)S * 4), st, &sp);
     if (rc) return rc;
     int8_t* xq = (int8_t*)sp;
     float* sx = (float*)((char*)sp + xb);
@@ -341,7 +369,7 @@ int moty_hip_dense_ffn_q8_dev(float* out, const float* x, int S, const int8_t* g
   hipStream_t st = STREAM(stream);
   void* sp;
   if (S <= GEMV_MAX_S) {
-    int rc = arena_get(d->scratch, al256((size_t)S * I * 4), &sp);
+    int rc = scratch_get(d, al256((size_t)S * I * 4), st, &sp);
     if (rc) return rc;
     float* h = (float*)sp;
     rc = launch_gemv_q8(x, gate, gs, up, us, h, S, D, I, st);
@@ -350,7 +378,7 @@ int moty_hip_dense_ffn_q8_dev(float* out, const float* x, int S, const int8_t* g
   }
   const size_t b_xq = al256((size_t)S * (D > I ? D : I)), b_sx = al256((size_t)S * 4);
   const size_t b_g = al256((size_t)S * I * 4);
-  int rc = arena_get(d->scratch, b_xq + b_sx + 2 * b_g, &sp);
+  int rc = scratch_get(d, b_xq + b_sx + 2 * b_g, st, &sp);
   if (rc) return rc;
   int8_t* xq = (int8_t*)sp;
   float* sx = (float*)((char*)sp + b_xq);
@@ -377,7 +405,7 @@ int moty_hip_moe_topk_dev(const MotyHipMoe* m, const float* x, int S, float* out
   size_t offs[MOE_NBUF];
   const size_t need = moe_scratch_size(S, m->D, m->E, m->K, m->I, offs);
   void* sp;
-  int rc = arena_get(d->scratch, need, &sp);
+  int rc = scratch_get(d, need, STREAM(stream), &sp);
   if (rc) return rc;
   MoeArgs a;
   a.x = x;
@@ -450,7 +478,7 @@ static int r4_dev(bool q8, const char* what, float* y, const float* x, const uin
   {  // activation scratch for the GEMM path (also taken by S <= 3 when the
      // decode GEMV does not serve the shape)
     const size_t bq = al256((size_t)S * I), bs = al256((size_t)S * (I / 32) * 4);
-    if ((rc = arena_get(d->scratch, bq + 2 * bs, &sp))) return rc;
+    if ((rc = scratch_get(d, bq + 2 * bs, STREAM(stream), &sp))) return rc;
     xq = (int8_t*)sp;
     xs = (float*)((char*)sp + bq);
     xm = (int32_t*)((char*)sp + bq + bs);
@@ -529,7 +557,7 @@ static int r4_ffn(bool q8, const char* what, float* out, const float* x, int S, 
   const size_t bh = al256((size_t)S * I * 4), bgu = al256((size_t)S * 2 * I * 4);
   const size_t bq = al256((size_t)S * W), bs = al256((size_t)S * (W / 32) * 4);
   void* sp;
-  int rc = arena_get(d->scratch, bh + bgu + bq + 2 * bs, &sp);
+  int rc = scratch_get(d, bh + bgu + bq + 2 * bs, st, &sp);
   if (rc) return rc;
   float* h = (float*)sp;
   float* g2 = (float*)((char*)sp + bh);
@@ -638,8 +666,14 @@ int moty_hip_gguf_repack_q4_0(const uint8_t* blocks, uint8_t* q4, float* qs, int
   return finish_io(d, qs, ds, (size_t)nblk * 4);
 }
 
+// The slot returns void: a failed call must not leave y looking valid, so
+// every output becomes a quiet NaN (and the message stays for
+// moty_hip_last_error()).
 void moty_hip_hw_matmul_i8(float* y, const float* x, const int8_t* q, const float* scale, int S, int I, int O) {
-  (void)moty_hip_matmul_q_s(y, x, q, scale, S, I, O);
+  if (moty_hip_matmul_q_s(y, x, q, scale, S, I, O) != MOTY_OK && y && S > 0 && O > 0) {
+    const float nan = __builtin_nanf("");
+    for (int64_t i = 0; i < (int64_t)S * O; i++) y[i] = nan;
+  }
 }
 
 int moty_hip_matmul_i4_grouped_s(float* y, const float* x, const uint8_t* q4, const float* scale, int S, int I,

@@ -25,6 +25,11 @@ struct Dev {
   int cus = 0;  // compute units
   hipStream_t stream = nullptr;
   Arena scratch, io;
+  // the stream whose queued work last used `scratch`, and an event used to
+  // order a later call on another stream behind that work
+  hipStream_t scr_stream = nullptr;
+  bool scr_used = false;
+  hipEvent_t scr_ev = nullptr;
   std::unordered_map<const void*, WEntry> wcache;
 };
 
@@ -32,6 +37,11 @@ struct Dev {
 int cur(Dev** out);
 // Grow an arena to at least `bytes`; waits for queued work before freeing.
 int arena_get(Arena& a, size_t bytes, void** p);
+// The device's scratch arena for work about to be queued on `st`: when the
+// previous user queued on another stream, `st` first waits for that work
+// (calls on one device share the arena, so two streams must not overlap in
+// it).  Streams under graph capture are left unordered.
+int scratch_get(Dev* d, size_t bytes, hipStream_t st, void** p);
 // Stage host x into the transfer arena (device x and y returned), and copy
 // y back and synchronise.
 int stage_io(Dev* d, const void* x, size_t xbytes, size_t ybytes, void** dx, void** dy);

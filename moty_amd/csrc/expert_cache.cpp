@@ -255,6 +255,8 @@ static int ec_fetch(bool pin, MotyHipExpertCache* c, void* ctx, int layer, int e
   int prev;
   const int s = pin ? ec_pin(c, eid, &prev) : ec_get(c, eid, &load, &prev);
   if (load) {
+    // a cached MoE call queued on a caller's stream may still read the slot
+    if (c->call_done) HIP_TRY(hipEventSynchronize(c->call_done));
     // work queued earlier on the library stream may still read the slot
     if ((rc = ec_load(c, ctx, layer, eid, fn, s, dv->stream))) return rc;
     HIP_TRY(hipStreamSynchronize(dv->stream));
@@ -354,7 +356,7 @@ int moty_hip_moe_topk_cached_dev(const MotyHipMoe* m, MotyHipExpertCache* c, voi
   size_t offs[MOE_NBUF];
   const size_t need = al256(moe_scratch_size(S, D, E, K, I, offs));
   void* sp;
-  if ((rc = arena_get(dv->scratch, need + max_pass * E * 4, &sp))) return rc;
+  if ((rc = scratch_get(dv, need + max_pass * E * 4, st, &sp))) return rc;
   int* ptab_d = (int*)((char*)sp + need);
   if (c->ptab_rows < max_pass) {
     if (c->ptab_h) HIP_TRY(hipHostFree(c->ptab_h));

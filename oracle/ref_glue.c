@@ -86,6 +86,24 @@ R_EXPORT void ref_moe_batch(float *out, const float *x, int S, const float *Wr,
     moty_expert_cache_free(&ec);
 }
 
+/* moty_nn_moe_topk_d1 (nn/moe.c:33-153, S = 1): route_topk (always
+ * normalised, nn/moe.c:27-30), then the serial top-k-order combine */
+R_EXPORT void ref_moe_d1(float *out, const float *x, const float *Wr,
+                         const int8_t *G, const float *GS, const int8_t *U, const float *US,
+                         const int8_t *Dn, const float *DS, int E, int K, int I, int D) {
+    Mat router; memset(&router, 0, sizeof router);
+    router.fmt = WF_F32; router.f = (float *)Wr; router.O = E; router.I = D;
+    ExpertCache ec; moty_expert_cache_init(&ec, E, E);
+    Stack st = { G, U, Dn, GS, US, DS };
+    Scratch scr; memset(&scr, 0, sizeof scr);
+    MotyMoeView v; memset(&v, 0, sizeof v);
+    v.router = &router; v.ec = &ec; v.load_expert = stack_load; v.ectx = &st;
+    v.E = E; v.K = K; v.I = I; v.D = D; v.ebits = 8; v.scr = &scr;
+    moty_nn_moe_topk_d1(&v, x, out);
+    moty_scr_free(&scr);
+    moty_expert_cache_free(&ec);
+}
+
 /* engines/olmoe.c:219-244 replayed over the reference's public functions */
 R_EXPORT void ref_moe_olmoe(float *out, const float *x, int S, const float *Wr,
                             const int8_t *G, const float *GS, const int8_t *U, const float *US,

@@ -92,6 +92,7 @@ _SIGS = {
     "ref_expf": (F32, [F32]),
     "ref_topk": (None, [P, I32, I32, P, P, I32]),
     "ref_moe_batch": (None, [P, P, I32, P, P, P, P, P, P, P, I32, I32, I32, I32]),
+    "ref_moe_d1": (None, [P, P, P, P, P, P, P, P, P, I32, I32, I32, I32]),
     "ref_moe_olmoe": (None, [P, P, I32, P, P, P, P, P, P, P, I32, I32, I32, I32, I32, P]),
 }
 
@@ -476,3 +477,37 @@ class RefCache:
         heat = [c.heat[e] for e in range(self.E)] if self.E > 0 else []
         last = [c.last[e] for e in range(self.E)] if self.E > 0 else []
         return OCacheState(c.n, eids, heat, last, c.clock, c.hits, c.misses)
+
+
+def fast_q8(seed, shape):
+    """Int8 codes over the full range and positive f32 row scales, drawn
+    directly (no f32 weights to quantize): workload-sized expert stacks in
+    seconds.  Codes include -128, which weights may hold (the dot_i8i8
+    contract restricts activations only, hw/hw.h)."""
+    g = rng(seed)
+    n = int(np.prod(shape))
+    q = np.frombuffer(g.bytes(n), dtype=np.int8).reshape(shape).copy()
+    s = g.uniform(1e-4, 3e-4, size=shape[:-1]).astype(np.float32)
+    return q, s
+
+
+def fast_moe_weights(E, I, D, seed=10):
+    ex = {}
+    ex["G"], ex["GS"] = fast_q8(seed, (E, I, D))
+    ex["U"], ex["US"] = fast_q8(seed + 1, (E, I, D))
+    ex["Dn"], ex["DS"] = fast_q8(seed + 2, (E, D, I))
+    return ex
+
+
+def skew_inputs(x, Wr, hot, lift=2.0):
+    """The skewed continuous batch through the plain router: feature 0 of
+    every token is 1 and the hot experts' router weight on it is `lift`, so
+    their logits rise by `lift` (up to one rounding) -- the +2.0 logit bias
+    of the skewed C5 variant, expressed in inputs every MoE entry point
+    (the reference's moe_batch included) takes."""
+    x = f32(x).copy()
+    Wr = f32(Wr).copy()
+    x[:, 0] = 1.0
+    Wr[:, 0] = 0.0
+    Wr[hot, 0] = lift
+    return x, Wr

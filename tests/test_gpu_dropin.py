@@ -172,3 +172,51 @@ def test_dropin_bad_arguments(lib):
     # empty problems succeed without touching anything
     assert lib.moty_hip_matmul_q_s(P(y), P(x), P(q), P(s), 0, 4, 1) == 0
     assert lib.moty_hip_matmul_q_s(P(y), P(x), P(q), P(s), 1, 4, 0) == 0
+
+
+def test_hw_slot_failure_poisons_y_and_errors_clear(lib):
+    # the void HwBackend.matmul_i8 slot cannot return a code: an unsupported
+    # shape (I % 16 != 0) leaves every y a NaN and a message; the next call
+    # that succeeds clears the message
+    S, I, O = 2, 40, 8
+    q, s = o_quantize_rows(randn(30, (O, I), 0.02))
+    x = randn(31, (S, I))
+    y = np.zeros((S, O), np.float32)
+    try:
+        lib.moty_hip_hw_matmul_i8(P(y), P(x), P(q), P(s), S, I, O)
+        assert np.isnan(y).all()
+        assert lib.moty_hip_last_error()
+        I2 = 64
+        q2, s2 = o_quantize_rows(randn(32, (O, I2), 0.02))
+        x2 = randn(33, (S, I2))
+        y2 = np.empty((S, O), np.float32)
+        lib.moty_hip_hw_matmul_i8(P(y2), P(x2), P(q2), P(s2), S, I2, O)
+        assert lib.moty_hip_last_error() == b""
+        assert same_bits(y2, o_matmul_q_s(x2, q2, s2))
+    finally:
+        forget(lib, q, s)
+
+
+def test_scratch_shared_across_streams(lib):
+    # sequential _dev calls on two streams share the device scratch: the
+    # second call is ordered behind the first (a long GEMM on stream A, then
+    # a different GEMM on stream B that reuses the same activation scratch)
+    import torch
+    from moty_amd import ops
+    from gpu_util import to_dev, to_np
+    a, b = torch.cuda.Stream(), torch.cuda.Stream()
+    S, I, O = 512, 4096, 8192
+    q, s = o_quantize_rows(randn(40, (O, I), 0.02))
+    x1 = randn(41, (S, I))
+    x2 = randn(42, (S, I)) * 3
+    qd, sd, x1d, x2d = to_dev(q), to_dev(s), to_dev(x1), to_dev(x2)
+    r1, r2 = o_matmul_q_s(x1, q, s), o_matmul_q_s(x2, q, s)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        with torch.cuda.stream(a):
+            y1 = ops.matmul_q_s(x1d, qd, sd)
+        with torch.cuda.stream(b):
+            y2 = ops.matmul_q_s(x2d, qd, sd)
+        torch.cuda.synchronize()
+        assert same_bits(to_np(y1), r1)
+        assert same_bits(to_np(y2), r2)

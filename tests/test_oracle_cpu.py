@@ -324,3 +324,43 @@ def test_route_bias_moves_argmax():
     bias[5] = 100.0
     idx, _, _ = o_route(x, Wr, 2, 1, bias)
     assert (idx[:, 0] == 5).all()
+
+
+@needs_ref
+@pytest.mark.parametrize("E,K,I,D", [(16, 4, 128, 256), (64, 8, 1024, 2048), (128, 8, 768, 2048), (8, 8, 32, 64)])
+def test_moe_d1_matches_ref(E, K, I, D):
+    # moty_nn_moe_topk_d1 (nn/moe.c:33-153) is the olmoe order with the
+    # routing always normalised: the oracle's olmoe layer at norm = 1
+    from cpu_libs import fast_moe_weights
+    ex = fast_moe_weights(E, I, D, seed=E + I)
+    Wr = randn(E + 1, (E, D), 0.02)
+    for seed in (3, 4):
+        x = randn(seed, (1, D))
+        out, idx, w = o_moe(x, Wr, ex, K, "olmoe", norm=1)
+        o2 = np.empty_like(out)
+        ref(True).ref_moe_d1(ptr(o2), ptr(x), ptr(Wr), *[ptr(ex[k]) for k in ("G", "GS", "U", "US", "Dn", "DS")],
+                             E, K, I, D)
+        assert (bits(out) == bits(o2)).all()
+
+
+@needs_ref
+@pytest.mark.parametrize("skewed", [False, True])
+def test_moe_batch_matches_ref_at_c5(skewed):
+    # the C5 workload (Qwen3-30B-A3B MoE: T = 1072, E = 128, top-8, I = 768,
+    # D = 2048) through moe_batch_core (nn/moe.c:159-205): every output row
+    from cpu_libs import fast_moe_weights, skew_inputs
+    E, K, I, D, T = 128, 8, 768, 2048, 1072
+    ex = fast_moe_weights(E, I, D, seed=50)
+    Wr = randn(51, (E, D), 0.02)
+    x = randn(52, (T, D))
+    hot = np.arange(0, 128, 16)
+    if skewed:
+        x, Wr = skew_inputs(x, Wr, hot)
+    out, idx, w = o_moe(x, Wr, ex, K, "batch")
+    o2 = np.empty_like(out)
+    ref(True).ref_moe_batch(ptr(o2), ptr(x), T, ptr(Wr), *[ptr(ex[k]) for k in ("G", "GS", "U", "US", "Dn", "DS")],
+                            E, K, I, D)
+    assert (bits(out) == bits(o2)).all()
+    cnt = np.bincount(idx.ravel(), minlength=E)
+    if skewed:
+        assert cnt[hot].sum() > 0.5 * cnt.sum()
