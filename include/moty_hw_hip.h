@@ -257,6 +257,16 @@ int moty_hip_gguf_repack_q4_0_dev(const uint8_t *blocks, uint8_t *q4, float *qs,
                                   void *stream);
 /* the MoE layer, all pointers in m and x/out on the device */
 int moty_hip_moe_topk_dev(const MotyHipMoe *m, const float *x, int S, float *out, void *stream);
+/* No counterpart in the reference: for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The MoE layer of moty_hip_moe_topk_dev, bit for bit, with its
+ * scratch in a fixed 64 MiB device array the library holds per GPU until
+ * the process ends (taken at moty_hip_init or the first call on a device);
+ * it calls no hipMalloc/hipFree.  Shapes whose scratch exceeds 64 MiB
+ * return MOTY_HIP_EINVAL (the OLMoE layer fits up to T = 256 tokens: about
+ * 27 MiB).  Every call on one GPU shares that array: calls that overlap on
+ * one GPU (several streams or host threads at once) race. */
+int moty_hip_moe_topk_noalloc_dev(const MotyHipMoe *m, const float *x, int S, float *out, void *stream);
 /* the cached layer with m's router/bias/outputs and x/out on the device;
  * synchronises `stream` once (the routing read-back) */
 int moty_hip_moe_topk_cached_dev(const MotyHipMoe *m, MotyHipExpertCache *lc, void *ctx, int layer,

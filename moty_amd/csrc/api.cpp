@@ -36,6 +36,13 @@ int check_hip(hipError_t e, const char* what) {
 
 constexpr int MAX_DEV = 16;
 static Dev g_dev[MAX_DEV];
+
+// Fixed scratch of the no-allocation entry point: a file-scope device array,
+// one copy per GPU the library runs on, held until the process ends.  Host
+// code never uses its name as an address (that is a host-side stand-in);
+// each device's address comes from hipGetSymbolAddress at set-up.
+constexpr size_t FIXED_SCRATCH_BYTES = (size_t)64 << 20;
+static __device__ __align__(256) char scratch[FIXED_SCRATCH_BYTES];
 static std::mutex g_mu;  // guards g_dev[*] set-up and the weight caches
 static thread_local int t_dev = -1;
 
@@ -52,6 +59,9 @@ static int dev_init(int d) {
     hipDeviceProp_t prop;
     HIP_TRY(hipGetDeviceProperties(&prop, d));
     g_dev[d].cus = prop.multiProcessorCount;
+    void* fp = nullptr;
+    HIP_TRY(hipGetSymbolAddress(&fp, HIP_SYMBOL(scratch)));
+    g_dev[d].fixed_scratch = fp;
     HIP_TRY(hipStreamCreateWithFlags(&g_dev[d].stream, hipStreamNonBlocking));
     g_dev[d].ready = true;
   }
@@ -392,21 +402,18 @@ int moty_hip_dense_ffn_q8_dev(float* out, const float* x, int S, const int8_t* g
   return launch_gemm_q8(xq, sx, down, ds, out, S, I, D, st);
 }
 
-int moty_hip_moe_topk_dev(const MotyHipMoe* m, const float* x, int S, float* out, void* stream) {
-  CUR(d);
-  if (!m || !x || !out || S < 0) return set_error("moe_topk: bad arguments"), MOTY_EINVAL;
+static int moe_check(const MotyHipMoe* m, const float* x, float* out, int S, const char* what) {
+  if (!m || !x || !out || S < 0) return set_error("%s: bad arguments", what), MOTY_EINVAL;
   if (m->E <= 0 || m->K <= 0 || m->K > m->E || m->K > 64 || m->I <= 0 || m->D <= 0)
-    return set_error("moe_topk: bad shape E=%d K=%d I=%d D=%d", m->E, m->K, m->I, m->D), MOTY_EINVAL;
-  if (S == 0) return MOTY_OK;
-  if ((m->D % 32) || (m->I % 32) || m->E > 256 || (size_t)(m->D + m->E) * 4 > 64 * 1024) {
-    set_error("moe_topk: D=%d I=%d E=%d unsupported (D, I multiples of 32, E <= 256)", m->D, m->I, m->E);
+    return set_error("%s: bad shape E=%d K=%d I=%d D=%d", what, m->E, m->K, m->I, m->D), MOTY_EINVAL;
+  if (S > 0 && ((m->D % 32) || (m->I % 32) || m->E > 256 || (size_t)(m->D + m->E) * 4 > 64 * 1024)) {
+    set_error("%s: D=%d I=%d E=%d unsupported (D, I multiples of 32, E <= 256)", what, m->D, m->I, m->E);
     return MOTY_EUNSUP;
   }
-  size_t offs[MOE_NBUF];
-  const size_t need = moe_scratch_size(S, m->D, m->E, m->K, m->I, offs);
-  void* sp;
-  int rc = scratch_get(d, need, STREAM(stream), &sp);
-  if (rc) return rc;
+  return MOTY_OK;
+}
+
+static MoeArgs moe_args(const MotyHipMoe* m, const float* x, int S, float* out) {
   MoeArgs a;
   a.x = x;
   a.Wr = m->router;
@@ -429,8 +436,38 @@ int moty_hip_moe_topk_dev(const MotyHipMoe* m, const float* x, int S, float* out
   a.w_out = m->w_out;
   a.counts_out = m->counts_out;
   a.probs_out = nullptr;
-  rc = launch_moe(a, sp, STREAM(stream));
+  return a;
+}
+
+int moty_hip_moe_topk_dev(const MotyHipMoe* m, const float* x, int S, float* out, void* stream) {
+  CUR(d);
+  int rc = moe_check(m, x, out, S, "moe_topk");
+  if (rc || S == 0) return rc;
+  size_t offs[MOE_NBUF];
+  const size_t need = moe_scratch_size(S, m->D, m->E, m->K, m->I, offs);
+  void* sp;
+  if ((rc = scratch_get(d, need, STREAM(stream), &sp))) return rc;
+  rc = launch_moe(moe_args(m, x, S, out), sp, STREAM(stream));
   if (rc == MOTY_EUNSUP) set_error("moe_topk: unsupported shape");
+  return rc;
+}
+
+// The MoE layer of moty_hip_moe_topk_dev on the fixed device scratch array:
+// no allocation of any kind, for callers that cannot allocate.
+int moty_hip_moe_topk_noalloc_dev(const MotyHipMoe* m, const float* x, int S, float* out, void* stream) {
+  CUR(d);
+  int rc = moe_check(m, x, out, S, "moe_topk_noalloc");
+  if (rc || S == 0) return rc;
+  size_t offs[MOE_NBUF];
+  const size_t need = moe_scratch_size(S, m->D, m->E, m->K, m->I, offs);
+  if (need > FIXED_SCRATCH_BYTES) {
+    set_error("moe_topk_noalloc: S=%d E=%d K=%d I=%d D=%d needs %zu bytes of scratch, above the fixed %zu", S,
+              m->E, m->K, m->I, m->D, need, FIXED_SCRATCH_BYTES);
+    return MOTY_EINVAL;
+  }
+  if (!d->fixed_scratch) return set_error("moe_topk_noalloc: fixed scratch has no device address"), MOTY_EHIP;
+  rc = launch_moe(moe_args(m, x, S, out), d->fixed_scratch, STREAM(stream));
+  if (rc == MOTY_EUNSUP) set_error("moe_topk_noalloc: unsupported shape");
   return rc;
 }
 

@@ -30,6 +30,9 @@ struct Dev {
   hipStream_t scr_stream = nullptr;
   bool scr_used = false;
   hipEvent_t scr_ev = nullptr;
+  // device address of this device's copy of the fixed no-allocation
+  // scratch array (api.cpp), taken once at set-up
+  void* fixed_scratch = nullptr;
   std::unordered_map<const void*, WEntry> wcache;
 };
 
