@@ -330,20 +330,12 @@ def bench_c3(c, steps, warmup):
     res = {}
     for M in (1, 256):
         x = c.randn((M, D), c.gen(2, 2))
-        gy = torch.empty((M, I), device="cuda:0")
-        uy = torch.empty((M, I), device="cuda:0")
         y = torch.empty((M, D), device="cuda:0")
 
         def step(w):
-            def f():
-                if M == 1:  # decode: fused gate+up+SiLU GEMV, then down
-                    ops.gate_up_silu_i4g(x, w[0][0], w[0][1], w[1][0], w[1][1], out=gy)
-                else:
-                    ops.matmul_i4_grouped_s(x, w[0][0], w[0][1], out=gy)
-                    ops.matmul_i4_grouped_s(x, w[1][0], w[1][1], out=uy)
-                    ops.silu_mul(gy, uy)
-                ops.matmul_i4_grouped_s(gy, w[2][0], w[2][1], out=y)
-            return f
+            # moty_nn_dense_ffn over WF_I4G Mats: gate + up + SiLU in one
+            # pass (a GEMV at M = 1, the f16-MFMA GEMM at M = 256), then down
+            return lambda: ops.dense_ffn_i4g(x, w[0][0], w[0][1], w[1][0], w[1][1], w[2][0], w[2][1], out=y)
         t, n = c.time_steps([step(w) for w in copies], max(8, steps // (8 if M == 1 else 64)), 8)
         ops_int = 2 * M * 3 * I * D
         algo = wbytes + M * (D + I + I + D) * 4

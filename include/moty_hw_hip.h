@@ -218,6 +218,14 @@ int moty_hip_gate_up_silu_q8_dev(float *h, const float *x, int S, const int8_t *
  * activations): h [I] = silu(x.gate^T) * (x.up^T), one token, D % 64 == 0. */
 int moty_hip_gate_up_silu_i4g_dev(float *h, const float *x, const uint8_t *gate, const float *gs,
                                   const uint8_t *up, const float *us, int D, int I, void *stream);
+/* moty_nn_dense_ffn (nn/ffn.c:26-55) over grouped-int4 Mats (WF_I4G, gs =
+ * 32): gate, up [I][D/2] nibbles + f32 scales [I][D/32], down [D][I/2] +
+ * [D][I/32]; x [S][D] -> out [S][D].  idot4 = 1: int8 activations
+ * (nn/matmul.c:164-197; gate and up in one pass with the SiLU epilogue);
+ * 0: the exact f32 path.  D, I multiples of 32. */
+int moty_hip_dense_ffn_i4g_dev(float *out, const float *x, int S, const uint8_t *gate, const float *gs,
+                               const uint8_t *up, const float *us, const uint8_t *down, const float *ds, int D,
+                               int I, int idot4, void *stream);
 /* moty_matmul_q4r4_s / moty_matmul_q8r4_s on device pointers: S <= 3 runs
  * the decode GEMV with fused activation quantization (the reference's
  * per-token form), larger S quantizes then runs the MFMA GEMM (tokens below

@@ -84,6 +84,7 @@ SIGNATURES = {
     "moty_hip_gate_up_silu_q8_dev": (I32, [P, P, I32, P, P, P, P, I32, I32, P]),
     "moty_hip_gate_up_silu_i4g_dev": (I32, [P, P, P, P, P, P, I32, I32, P]),
     "moty_hip_dense_ffn_q8_dev": (I32, [P, P, I32, P, P, P, P, P, P, I32, I32, P]),
+    "moty_hip_dense_ffn_i4g_dev": (I32, [P, P, I32, P, P, P, P, P, P, I32, I32, I32, P]),
     "moty_hip_moe_topk_dev": (I32, [C.POINTER(MotyHipMoe), P, I32, P, P]),
     "moty_hip_moe_topk_noalloc_dev": (I32, [C.POINTER(MotyHipMoe), P, I32, P, P]),
 }

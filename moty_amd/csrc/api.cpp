@@ -305,6 +305,16 @@ int moty_hip_matmul_i4_grouped_s_dev(float* y, const float* x, const uint8_t* q4
   if (idot4 && gs == 32 && (I % 64) == 0 && I <= 16384) {
     if (S <= 4) return launch_gemv_i4g(x, q4, scale, nullptr, nullptr, y, S, I, O, st);
     void* sp;
+    if ((I % 128) == 0 && !(((uintptr_t)x | (uintptr_t)q4 | (uintptr_t)scale) & 15)) {
+      // f16 codes + f16 MFMA: one FMA per output and group in the epilogue
+      const size_t hb = al256((size_t)S * I * 2);
+      int rc = scratch_get(d, hb + al256((size_t)S * 4), st, &sp);
+      if (rc) return rc;
+      uint16_t* xh = (uint16_t*)sp;
+      float* sx = (float*)((char*)sp + hb);
+      if ((rc = launch_qrow_f16p(x, xh, sx, S, I, st))) return rc;
+      return launch_gemm_i4g_h(xh, sx, q4, scale, nullptr, nullptr, y, S, I, O, st);
+    }
     const size_t xb = al256((size_t)S * I);
     int rc = scratch_get(d, xb + al256((size_t)S * 4), st, &sp);
     if (rc) return rc;
@@ -437,6 +447,60 @@ static MoeArgs moe_args(const MotyHipMoe* m, const float* x, int S, float* out) 
   a.counts_out = m->counts_out;
   a.probs_out = nullptr;
   return a;
+}
+
+// moty_nn_dense_ffn (nn/ffn.c:26-55) over grouped-int4 gate/up/down Mats
+// (WF_I4G, gs = 32): gate and up in one pass with the SiLU epilogue, then
+// down.  idot4 selects the int8-activation path (nn/matmul.c:171), else the
+// exact f32 path.
+int moty_hip_dense_ffn_i4g_dev(float* out, const float* x, int S, const uint8_t* gate, const float* gs,
+                               const uint8_t* up, const float* us, const uint8_t* down, const float* ds, int D,
+                               int I, int idot4, void* stream) {
+  CUR(d);
+  if (S < 0 || D <= 0 || I <= 0 || !out || !x || !gate || !gs || !up || !us || !down || !ds)
+    return set_error("dense_ffn_i4g: bad arguments"), MOTY_EINVAL;
+  if (S == 0) return MOTY_OK;
+  if ((D % 32) || (I % 32)) return set_error("dense_ffn_i4g: D=%d I=%d must be multiples of 32", D, I), MOTY_EUNSUP;
+  hipStream_t st = STREAM(stream);
+  const bool vec = idot4 && (D % 64) == 0 && (I % 64) == 0 && D <= 16384 && I <= 16384;  // both matrices
+  const bool h16 = vec && S > 4 && (D % 128) == 0 && (I % 128) == 0 &&
+                   !(((uintptr_t)x | (uintptr_t)gate | (uintptr_t)gs | (uintptr_t)up | (uintptr_t)us |
+                      (uintptr_t)down | (uintptr_t)ds) & 15);
+  const int W = D > I ? D : I;
+  // scratch: h [S][I] f32 | u [S][I] f32 (paths without the fused pass) |
+  // activation codes [S][W] (f16 or int8) | row scales [S]
+  const size_t bh = al256((size_t)S * I * 4), bq = al256((size_t)S * W * 2), bs = al256((size_t)S * 4);
+  void* sp;
+  int rc = scratch_get(d, 2 * bh + bq + bs, st, &sp);
+  if (rc) return rc;
+  float* h = (float*)sp;
+  float* u = (float*)((char*)sp + bh);
+  void* xq = (char*)sp + 2 * bh;
+  float* sx = (float*)((char*)sp + 2 * bh + bq);
+  if (h16) {
+    if ((rc = launch_qrow_f16p(x, (uint16_t*)xq, sx, S, D, st))) return rc;
+    if ((rc = launch_gemm_i4g_h((const uint16_t*)xq, sx, gate, gs, up, us, h, S, D, I, st))) return rc;
+    if ((rc = launch_qrow_f16p(h, (uint16_t*)xq, sx, S, I, st))) return rc;
+    return launch_gemm_i4g_h((const uint16_t*)xq, sx, down, ds, nullptr, nullptr, out, S, I, D, st);
+  }
+  if (vec && S == 1) {
+    if ((rc = launch_gemv_i4g(x, gate, gs, up, us, h, 1, D, I, st))) return rc;
+    return launch_gemv_i4g(h, down, ds, nullptr, nullptr, out, 1, I, D, st);
+  }
+  // one matmul_i4_grouped_s each, the path chosen per matrix as the
+  // reference does (IDOT4 needs the row length a multiple of 64, <= 16384)
+  auto mm = [&](const float* a, const uint8_t* w, const float* ws, float* o, int K, int N) -> int {
+    if (idot4 && (K % 64) == 0 && K <= 16384) {
+      if (S <= 4) return launch_gemv_i4g(a, w, ws, nullptr, nullptr, o, S, K, N, st);
+      int r = launch_qrow_i8(a, (int8_t*)xq, sx, nullptr, S, K, K, K, st);
+      return r ? r : launch_gemm_i4g((const int8_t*)xq, sx, w, ws, o, S, K, N, st);
+    }
+    return launch_i4g_f32(a, w, ws, o, S, K, N, st);
+  };
+  if ((rc = mm(x, gate, gs, h, D, I))) return rc;
+  if ((rc = mm(x, up, us, u, D, I))) return rc;
+  if ((rc = launch_silu_mul(h, u, (int64_t)S * I, st))) return rc;
+  return mm(h, down, ds, out, I, D);
 }
 
 int moty_hip_moe_topk_dev(const MotyHipMoe* m, const float* x, int S, float* out, void* stream) {

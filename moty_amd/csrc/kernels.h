@@ -14,6 +14,9 @@ constexpr int MOE_NBUF = 15;   // MoE scratch sub-buffers
 
 int launch_qrow_i8(const float* x, int8_t* q, float* sx, int32_t* xg, int S, int I, int64_t ldx, int64_t ldq,
                    hipStream_t st);
+// qrow_i8 with f16 codes in the k-permuted run order of the f16-MFMA
+// grouped-int4 GEMM; I % 8 == 0, I <= 16384, x and xh 16-byte aligned
+int launch_qrow_f16p(const float* x, uint16_t* xh, float* sx, int S, int I, hipStream_t st);
 int launch_quantize_rows(const float* w, int8_t* q, float* scale, int O, int I, int bits, hipStream_t st);
 int launch_pack_i4g(const float* w, uint8_t* q4, float* scale, int O, int I, int gs, hipStream_t st);
 
@@ -27,6 +30,11 @@ int launch_gemv_i4g(const float* x, const uint8_t* q4, const float* scl, const u
                     float* y, int S, int I, int O, hipStream_t st);
 int launch_gemm_i4g(const int8_t* xq, const float* sx, const uint8_t* q4, const float* scl, float* y, int M, int I,
                     int O, hipStream_t st);
+// the same GEMM on f16 MFMA over activations from launch_qrow_f16p;
+// q4b/sclb non-null: PAIR, y = silu(x.q4^T) * (x.q4b^T).  MOTY_EUNSUP when
+// I % 128 != 0 or a pointer is not 16-byte aligned
+int launch_gemm_i4g_h(const uint16_t* xh, const float* sx, const uint8_t* q4, const float* scl, const uint8_t* q4b,
+                      const float* sclb, float* y, int M, int I, int O, hipStream_t st);
 int launch_i4g_f32(const float* x, const uint8_t* q4, const float* scl, float* y, int S, int I, int O,
                    hipStream_t st);
 

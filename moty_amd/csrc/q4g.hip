@@ -14,6 +14,7 @@
 // so each output's chain runs in ascending group order in one lane.
 #include "common.h"
 #include "kernels.h"
+#include <stdlib.h>
 
 namespace moty {
 
@@ -388,6 +389,294 @@ __global__ __launch_bounds__(Q4M_NT, 2) void k_gemm_i4g(const int8_t* __restrict
     const int rl = wm * 32 + 8 * (r >> 2) + 4 * hk + (r & 3);
     if (mb + rl < M) y[(int64_t)(mb + rl) * O + col] = s_sx[rl] * accf[r];
   }
+}
+
+// ---------------------------------------------------------------------------
+// IDOT4 GEMM on f16 MFMA (v_mfma_f32_32x32x16_f16, two per group).  The
+// reference's per-group step is acc = fma(scl[o][g], (float)d_g, acc) in group
+// order, d_g = sum over the group of (n - 8) * xq: an exact integer.  With f16
+// operands -- activation codes in [-127, 127] and weight codes n - 8 in
+// [-8, 7] are exact halves, every partial sum is an integer below 2^24 -- the
+// MFMA returns d_g already as an exact float, so the epilogue is one FMA per
+// output per group instead of a conversion and an FMA.
+//
+// Weight nibbles become halves with two integer ops and a packed f16 add per
+// pair: (w >> 4i) & 0x000f000f | 0x64006400 is the half pair (1024 + n_a,
+// 1024 + n_b), minus 1032 gives (n_a - 8, n_b - 8).  One nibble dword (8
+// codes, elements e0..e7) unpacks to the order [e0,e4,e1,e5,e2,e6,e3,e7];
+// the activations arrive from k_qrow_f16p in the same order.
+//
+// Block tile BM tokens x BN weight rows, 4 waves as 2 x 2, each wave FM x FN
+// 32 x 32 tiles.  K blocks of 4 groups (128 elements) move global -> LDS by
+// DMA, S - 1 blocks ahead: per stage BM activation rows of 256 B (16-byte
+// chunk c of row r in slot c ^ (r & 15): a ds_read_b128 cycle's 16 rows hit
+// 16 distinct bank groups), BN nibble rows of 64 B (chunk c in slot
+// c ^ ((r >> 2) & 3)) and BN scale rows of 16 B (the block's 4 group scales).
+// Lane l takes, for group j, half h = l / 32 of its rows' group: elements
+// [16h, 16h + 16) -- the first 8 for MFMA 0, the next 8 for MFMA 1.
+constexpr int Q4H_NT = 256;
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// 8 nibble codes (one dword) -> 8 halves n - 8, order [e0,e4,e1,e5,e2,e6,e3,e7].
+// m = 0x000f000f and o = 0x64006400 arrive in VGPRs so that each pair is one
+// v_and_or_b32 (VOP3 takes no literal here) and one v_pk_add_f16.
+__device__ __forceinline__ v8h nib8_to_h(uint32_t w, uint32_t m, uint32_t o) {
+  const h2v bias = h2v{(_Float16)-1032.f, (_Float16)-1032.f};
+  const h2v p0 = __builtin_bit_cast(h2v, (w & m) | o) + bias;
+  const h2v p1 = __builtin_bit_cast(h2v, ((w >> 4) & m) | o) + bias;
+  const h2v p2 = __builtin_bit_cast(h2v, ((w >> 8) & m) | o) + bias;
+  const h2v p3 = __builtin_bit_cast(h2v, ((w >> 12) & m) | o) + bias;
+  return v8h{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+}
+
+// Buffer resource over `bytes` bytes at p (raw, stride 0): loads past the
+// end return zeros instead of faulting.
+__device__ __forceinline__ v4i buf_rsrc(const void* p, uint32_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)p;
+  return v4i{__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+             __builtin_amdgcn_readfirstlane((int)(uint32_t)((a >> 32) & 0xffffu)),
+             __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
+}
+
+// 16 bytes per lane from buffer offset voff + soff straight into LDS at
+// lds_base + 16*lane (buffer_load_dwordx4 ... lds); as dma16_to_lds, the
+// caller orders it with vmcnt waits and barriers.
+__device__ __forceinline__ void bdma16_to_lds(v4i rsrc, uint32_t voff, uint32_t soff, uint32_t lds_base) {
+  uint32_t save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "buffer_load_dwordx4 %1, %2, %4 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "v"(voff), "s"(rsrc), "s"(lds_base), "s"(soff));
+}
+
+// PAIR: gate and up rows of the same block tile in one pass (the activation
+// fragments serve both), epilogue y = silu(sx*gate) * (sx*up) -- the
+// gate_up + silu_rows of nn/ffn.c:28-37.
+template <int BM, int BN, int S, int WGM, int NW, bool PAIR>
+__global__ __launch_bounds__(NW * 64, 8 / NW) void k_gemm_i4g_h(const uint16_t* __restrict__ xh,
+                                                                const float* __restrict__ sx,
+                                                                const uint8_t* __restrict__ q4,
+                                                                const float* __restrict__ scl,
+                                                                const uint8_t* __restrict__ q4b,
+                                                                const float* __restrict__ sclb,
+                                                                float* __restrict__ y, int M, int I, int O) {
+  constexpr int NP = PAIR ? 2 : 1;  // weight matrices
+  // stage: BM activation rows x 256 B | NP x BN nibble rows x 64 B | NP x BN scale rows x 16 B
+  constexpr int SA = BM * 256, SB = BN * 64, SS = BN * 16, STAGE = SA + NP * (SB + SS);
+  // 1 KiB DMA instructions per stage: A 4 rows each, B 16 rows, scales 64
+  // rows; wave wv takes instruction j * NW + wv of each region (the last
+  // repeats when a region's count is not a multiple of NW)
+  constexpr int JA = BM / 4, JB = NP * BN / 16, JS = NP * BN / 64;
+  constexpr int NA = (JA + NW - 1) / NW, NB = (JB + NW - 1) / NW, NS = (JS + NW - 1) / NW;
+  constexpr int NI = NA + NB + NS;
+  constexpr int WGN = NW / WGM;  // waves along the tokens x along the rows
+  constexpr int TM = BM / WGM, TN = BN / WGN, FM = TM / 32, FN = TN / 32;
+  static_assert(BN % 64 == 0 && BM % 64 == 0 && FM >= 1 && FN >= 1, "whole 1 KiB DMA rows");
+  __shared__ __align__(1024) uint8_t lds[S * STAGE];
+  __shared__ float s_sx[BM];
+  const int tid = threadIdx.x, lane = tid % MOTY_WAVE;
+  const int wv = __builtin_amdgcn_readfirstlane(tid / MOTY_WAVE);
+  const int wm = wv / WGN, wn = wv % WGN;
+  const int r32 = lane & 31, h = lane >> 5;
+  const int mb = blockIdx.y * BM, nb = blockIdx.x * BN;
+  const int ng = I / 32;
+  const v4i rA = buf_rsrc(xh, (uint32_t)M * I * 2);
+  const v4i rB0 = buf_rsrc(q4, (uint32_t)O * (I / 2)), rS0 = buf_rsrc(scl, (uint32_t)O * ng * 4);
+  const v4i rB1 = PAIR ? buf_rsrc(q4b, (uint32_t)O * (I / 2)) : rB0;
+  const v4i rS1 = PAIR ? buf_rsrc(sclb, (uint32_t)O * ng * 4) : rS0;
+  // per-lane source offsets of this wave's DMAs: A chunk c of row r goes to
+  // slot c ^ (r & 15), B chunk c of row r to slot c ^ ((r >> 2) & 3); B and
+  // scale instructions past the first matrix's count serve the second
+  uint32_t voA[NA], voB[NB], voS[NS];
+  int jA[NA], jB[NB], jS[NS];
+#pragma unroll
+  for (int j = 0; j < NA; j++) {
+    jA[j] = j * NW + wv < JA ? j * NW + wv : JA - 1;
+    const int row = jA[j] * 4 + (lane >> 4);
+    const int c = (lane & 15) ^ (row & 15);
+    const int m = mb + row < M ? mb + row : M - 1;
+    voA[j] = (uint32_t)m * (uint32_t)I * 2u + (uint32_t)c * 16u;
+  }
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    jB[j] = j * NW + wv < JB ? j * NW + wv : JB - 1;
+    const int row = (jB[j] % (BN / 16)) * 16 + (lane >> 2);
+    const int c = (lane & 3) ^ ((row >> 2) & 3);
+    const int n = nb + row < O ? nb + row : O - 1;
+    voB[j] = (uint32_t)n * (uint32_t)(I / 2) + (uint32_t)c * 16u;
+  }
+#pragma unroll
+  for (int j = 0; j < NS; j++) {
+    jS[j] = j * NW + wv < JS ? j * NW + wv : JS - 1;
+    const int row = (jS[j] % (BN / 64)) * 64 + lane;
+    const int n = nb + row < O ? nb + row : O - 1;
+    voS[j] = (uint32_t)n * (uint32_t)ng * 4u;
+  }
+  const int nk = I / 128;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
+  auto issue = [&](int kb) {
+    const uint32_t st0 = lds0 + (uint32_t)(kb % S) * STAGE;
+#pragma unroll
+    for (int j = 0; j < NA; j++) bdma16_to_lds(rA, voA[j], (uint32_t)kb * 256u, st0 + jA[j] * 1024);
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+      bdma16_to_lds(jB[j] < BN / 16 ? rB0 : rB1, voB[j], (uint32_t)kb * 64u, st0 + SA + jB[j] * 1024);
+#pragma unroll
+    for (int j = 0; j < NS; j++)
+      bdma16_to_lds(jS[j] < BN / 64 ? rS0 : rS1, voS[j], (uint32_t)kb * 16u, st0 + SA + NP * SB + jS[j] * 1024);
+  };
+  // the tile's activation scales: the oldest load, covered by the waits below
+  float sxr;
+  {
+    const int m = mb + tid % BM;
+    sxr = sx[m < M ? m : M - 1];
+  }
+  uint32_t km, ko;
+  asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(km));
+  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(ko));
+  float acc[NP][FM][FN][16];
+#pragma unroll
+  for (int p = 0; p < NP; p++)
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int j = 0; j < FN; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[p][i][j][r] = 0.f;
+  // A K block's operands in registers: the activation fragments, the raw
+  // nibble pairs and the scales of its 4 groups.  The next block's are read
+  // from LDS while this one is unpacked and multiplied.
+  struct Frags {
+    v8h a[4][FM][2];
+    uint2 b[4][NP][FN];
+    float4 s[NP][FN];
+  };
+  auto read = [&](int kb, Frags& f) {
+    const uint8_t* st = lds + (kb % S) * STAGE;
+#pragma unroll
+    for (int p = 0; p < NP; p++)
+#pragma unroll
+      for (int j = 0; j < FN; j++)
+        f.s[p][j] = *(const float4*)(st + SA + NP * SB + p * SS + (wn * TN + j * 32 + r32) * 16);
+#pragma unroll
+    for (int gl = 0; gl < 4; gl++) {
+#pragma unroll
+      for (int i = 0; i < FM; i++) {
+        const int row = wm * TM + i * 32 + r32;
+#pragma unroll
+        for (int m = 0; m < 2; m++) {
+          const int c = 4 * gl + 2 * h + m;
+          f.a[gl][i][m] = *(const v8h*)(st + row * 256 + ((c ^ (row & 15)) * 16));
+        }
+      }
+#pragma unroll
+      for (int p = 0; p < NP; p++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+          const int row = wn * TN + j * 32 + r32;
+          f.b[gl][p][j] = *(const uint2*)(st + SA + p * SB + row * 64 + ((gl ^ ((row >> 2) & 3)) * 16) + 8 * h);
+        }
+    }
+  };
+  auto compute = [&](const Frags& f) {
+#pragma unroll
+    for (int gl = 0; gl < 4; gl++) {
+#pragma unroll
+      for (int p = 0; p < NP; p++) {
+        v8h fb[FN][2];
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+          fb[j][0] = nib8_to_h(f.b[gl][p][j].x, km, ko);
+          fb[j][1] = nib8_to_h(f.b[gl][p][j].y, km, ko);
+        }
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+          for (int j = 0; j < FN; j++) {
+            v16f d = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[gl][i][0], fb[j][0], v16f{}, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[gl][i][1], fb[j][1], d, 0, 0, 0);
+            const float4 sv = f.s[p][j];
+            const float s = gl == 0 ? sv.x : gl == 1 ? sv.y : gl == 2 ? sv.z : sv.w;
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[p][i][j][r] = __fmaf_rn(s, d[r], acc[p][i][j][r]);
+          }
+      }
+    }
+  };
+  // every stage of the ring in flight, then block 0's operands to registers
+#pragma unroll
+  for (int s = 0; s < S; s++) issue(s);
+  MOTY_WAIT_VMCNT((S - 1) * NI);
+  __syncthreads();
+  Frags f0, f1;
+  read(0, f0);
+  for (int kb = 0; kb < nk; kb += 2) {
+    // block kb + 1 has landed (the S - 2 later ones may still fly); the
+    // barrier also retires every wave's reads of block kb's stage, which the
+    // next DMA overwrites.  Blocks past the end read zeros, never consumed.
+    MOTY_WAIT_VMCNT((S - 2) * NI);
+    __syncthreads();
+    issue(kb + S);
+    read(kb + 1, f1);
+    compute(f0);
+    if (kb + 1 >= nk) break;
+    MOTY_WAIT_VMCNT((S - 2) * NI);
+    __syncthreads();
+    issue(kb + 1 + S);
+    read(kb + 2, f0);
+    compute(f1);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  if (tid < BM) s_sx[tid] = sxr;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < FN; j++) {
+    const int n = nb + wn * TN + j * 32 + r32;
+    if (n >= O) continue;
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int ml = wm * TM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (mb + ml >= M) continue;
+        const float sv = s_sx[ml];
+        y[(int64_t)(mb + ml) * O + n] =
+            PAIR ? ref_silu_mul(sv * acc[0][i][j][r], sv * acc[NP - 1][i][j][r]) : sv * acc[0][i][j][r];
+      }
+  }
+}
+
+// The f16-MFMA GEMM (q4b/sclb non-null: PAIR, y = silu(x.q4^T) * (x.q4b^T)).
+// Tiles from a sweep on MI355X at M = 256 (K = 4096, N = 12288: 57 us; K =
+// 12288, N = 4096: 79 us): 128 x 128 block tiles of 8 waves, two stages,
+// when they give at least 160 workgroups; 64 x 64 tiles of 4 waves, three
+// stages, otherwise.
+int launch_gemm_i4g_h(const uint16_t* xh, const float* sx, const uint8_t* q4, const float* scl, const uint8_t* q4b,
+                      const float* sclb, float* y, int M, int I, int O, hipStream_t st) {
+  if ((I % 128) || ((((uintptr_t)xh) | ((uintptr_t)q4) | ((uintptr_t)scl) | ((uintptr_t)q4b) | ((uintptr_t)sclb)) & 15))
+    return MOTY_EUNSUP;
+  if ((int64_t)M * I * 2 >= ((int64_t)1 << 32) || (int64_t)O * I / 2 >= ((int64_t)1 << 32)) return MOTY_EUNSUP;
+  if (M <= 0 || O <= 0) return MOTY_OK;
+  const bool big = (int64_t)((M + 127) / 128) * ((O + 127) / 128) >= 160;
+#define Q4H(BM, BN, S, WGM, NW, P)                                                                              \
+  hipLaunchKernelGGL((k_gemm_i4g_h<BM, BN, S, WGM, NW, P>), dim3((O + BN - 1) / BN, (M + BM - 1) / BM),        \
+                     dim3(NW * 64), 0, st, xh, sx, q4, scl, q4b, sclb, y, M, I, O)
+  if (q4b) {
+    if (big) Q4H(128, 128, 2, 2, 8, true);
+    else Q4H(64, 64, 3, 2, 4, true);
+  } else {
+    if (big) Q4H(128, 128, 2, 2, 8, false);
+    else Q4H(64, 64, 3, 2, 4, false);
+  }
+#undef Q4H
+  LAUNCH_TRY("k_gemm_i4g_h");
+  return MOTY_OK;
 }
 
 // ---------------------------------------------------------------------------

@@ -204,6 +204,67 @@ int launch_qrow_i8(const float* x, int8_t* q, float* sx, int32_t* xg, int S, int
   return MOTY_OK;
 }
 
+// qrow_i8 (hw/hw_quant.h:9-16) with the codes written as f16 -- exact, they
+// are integers in [-127, 127] -- for the f16-MFMA grouped-int4 GEMM.  Every
+// run of 8 codes is stored in the order [0,4,1,5,2,6,3,7], the order in
+// which that GEMM unpacks 8 weight nibbles (a k-permutation shared by both
+// operands, exact for the integer-valued dots).  One workgroup per row, the
+// row held in registers: NR runs of 8 per thread (run t + NT*j).
+template <int NT, int NR>
+__global__ __launch_bounds__(NT) void k_qrow_f16p(const float* __restrict__ x, uint16_t* __restrict__ xh,
+                                                  float* __restrict__ sx, int I) {
+  __shared__ float red[NT / MOTY_WAVE];
+  const int64_t row = blockIdx.x;
+  const float* xr = x + row * I;
+  const int nrun = I / 8;
+  float4 v[NR][2];
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < NR; j++) {
+    const int r = threadIdx.x + NT * j;
+    const int rc = r < nrun ? r : 0;
+    v[j][0] = sel4(r < nrun, *(const float4*)(xr + 8 * rc));
+    v[j][1] = sel4(r < nrun, *(const float4*)(xr + 8 * rc + 4));
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j][0].x), fabsf(v[j][0].y)), fmaxf(fabsf(v[j][0].z), fabsf(v[j][0].w))));
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j][1].x), fabsf(v[j][1].y)), fmaxf(fabsf(v[j][1].z), fabsf(v[j][1].w))));
+  }
+  amax = block_max<NT>(amax, red);
+  float s = amax / 127.f;
+  if (s < 1e-12f) s = 1e-12f;
+  const float inv = 1.f / s;
+  if (threadIdx.x == 0) sx[row] = s;
+#pragma unroll
+  for (int j = 0; j < NR; j++) {
+    const int r = threadIdx.x + NT * j;
+    if (r >= nrun) break;
+    const float e[8] = {v[j][0].x, v[j][0].y, v[j][0].z, v[j][0].w, v[j][1].x, v[j][1].y, v[j][1].z, v[j][1].w};
+    uint32_t h[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const _Float16 c = (_Float16)(float)rne_int(e[k] * inv);
+      h[k] = (uint32_t)__builtin_bit_cast(uint16_t, c);
+    }
+    const uint4 o = uint4{h[0] | (h[4] << 16), h[1] | (h[5] << 16), h[2] | (h[6] << 16), h[3] | (h[7] << 16)};
+    *(uint4*)(xh + row * I + 8 * r) = o;
+  }
+}
+
+int launch_qrow_f16p(const float* x, uint16_t* xh, float* sx, int S, int I, hipStream_t st) {
+  if (S <= 0) return MOTY_OK;
+  if ((I % 8) || (((uintptr_t)x) & 15) || (((uintptr_t)xh) & 15)) return MOTY_EUNSUP;
+  const int runs = (I / 8 + 255) / 256;
+  if (runs <= 2)
+    hipLaunchKernelGGL((k_qrow_f16p<256, 2>), dim3(S), dim3(256), 0, st, x, xh, sx, I);
+  else if (runs <= 4)
+    hipLaunchKernelGGL((k_qrow_f16p<256, 4>), dim3(S), dim3(256), 0, st, x, xh, sx, I);
+  else if (runs <= 8)
+    hipLaunchKernelGGL((k_qrow_f16p<256, 8>), dim3(S), dim3(256), 0, st, x, xh, sx, I);
+  else
+    return MOTY_EUNSUP;
+  LAUNCH_TRY("k_qrow_f16p");
+  return MOTY_OK;
+}
+
 int launch_quantize_rows(const float* w, int8_t* q, float* scale, int O, int I, int bits, hipStream_t st) {
   if (O <= 0) return MOTY_OK;
   hipLaunchKernelGGL(k_quantize_rows<256>, dim3(O), dim3(256), 0, st, w, q, scale, I, bits);

@@ -217,6 +217,17 @@ def dense_ffn_q8(x, gate, gs, up, us, down, ds, out=None):
     return y
 
 
+def dense_ffn_i4g(x, gate, gs, up, us, down, ds, idot4=True, out=None):
+    """nn/ffn.c:26-55 over grouped-int4 weights (gs = 32)."""
+    _dev(x, gate, gs, up, us, down, ds)
+    S, D = x.shape
+    I = gate.shape[0]
+    y = out if out is not None else torch.empty((S, D), dtype=torch.float32, device=x.device)
+    check(lib().moty_hip_dense_ffn_i4g_dev(_p(y), _p(x), S, _p(gate), _p(gs), _p(up), _p(us), _p(down), _p(ds),
+                                           D, I, int(bool(idot4)), _stream()), "dense_ffn_i4g")
+    return y
+
+
 def gate_up_silu_q8(x, gate, gs, up, us, out=None):
     """nn/ffn.c:28-37 for decode: h = silu(x.gate^T) * (x.up^T), one pass."""
     _dev(x, gate, gs, up, us)

@@ -200,3 +200,25 @@ def test_silu_and_softmax(ops):
         for r in range(4):
             oracle().o_softmax(ptr(x2[r]), E)
         assert same_bits(to_np(xd), x2)
+
+
+@pytest.mark.parametrize("idot4", [True, False])
+@pytest.mark.parametrize("S,D,I", [(37, 256, 384), (5, 128, 128), (4, 256, 128), (1, 128, 64), (130, 1024, 640),
+                                   (70, 192, 320), (3, 4096, 96), (300, 512, 1280)])
+def test_dense_ffn_i4g(ops, idot4, S, D, I):
+    # nn/ffn.c:26-55 over grouped-int4 Mats: the fused gate/up f16 pass
+    # (S > 4, D and I multiples of 128), the int8 GEMM fallback (other
+    # multiples of 64), the GEMVs (S <= 4) and the exact f32 path
+    say("dense_ffn_i4g", idot4, S, D, I)
+    gq, gs = o_pack_int4_grouped(randn(S + D, (I, D), 0.02))
+    uq, us = o_pack_int4_grouped(randn(S + D + 1, (I, D), 0.02))
+    dq, ds = o_pack_int4_grouped(randn(S + I, (D, I), 0.02))
+    x = randn(S + 3, (S, D))
+    y = to_np(ops.dense_ffn_i4g(to_dev(x), to_dev(gq), to_dev(gs), to_dev(uq), to_dev(us), to_dev(dq), to_dev(ds),
+                                idot4))
+    # the reference picks the IDOT4 path per matrix: row length % 64 == 0
+    g = o_matmul_i4g(x, gq, gs, idot4 and D % 64 == 0)
+    u = o_matmul_i4g(x, uq, us, idot4 and D % 64 == 0)
+    oracle().o_silu_mul(ptr(g), ptr(u), g.size)
+    y2 = o_matmul_i4g(g, dq, ds, idot4 and I % 64 == 0)
+    assert same_bits(y, y2), mismatch(y, y2)

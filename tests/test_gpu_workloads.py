@@ -197,3 +197,16 @@ def test_c3_r4_ffn(ops, c3_r4_weights, M):
     h = o_silu(y[:, :I], y[:, I:])
     ref = o_matmul_r4(h, q2, d2, D)
     assert same_bits(out, ref), mismatch(out, ref)
+
+
+@pytest.mark.parametrize("M", [256, 1])
+def test_c3_i4g_dense_ffn(ops, c3_weights, M):
+    # moty_hip_dense_ffn_i4g_dev (bench.py C3): gate and up in one pass with
+    # the SiLU epilogue, then down
+    D, I, (gq, gs), (uq, us), (dq, ds) = c3_weights
+    say("C3 i4g dense ffn M=%d" % M)
+    x = randn(85 + M, (M, D))
+    y = to_np(ops.dense_ffn_i4g(to_dev(x), to_dev(gq), to_dev(gs), to_dev(uq), to_dev(us), to_dev(dq), to_dev(ds)))
+    h = o_silu(o_matmul_i4g(x, gq, gs, True), o_matmul_i4g(x, uq, us, True))
+    y2 = o_matmul_i4g(h, dq, ds, True)
+    assert same_bits(y, y2), mismatch(y, y2)
