@@ -175,6 +175,15 @@ int moty_hip_weight_forget(const void *host_ptr);
  * CPU path calls moty_hip_matmul_q_s instead and falls back on nonzero. */
 void moty_hip_hw_matmul_i8(float *y, const float *x, const int8_t *q, const float *scale, int S, int I, int O);
 
+/* moty_matmul_i4_s (nn/nn_matmul.h:66, nn/matmul.c:75-145), per-row int4
+ * weights (WF_I4): q4 [O][(I+1)/2] nibbles (even element low) + f32 scale
+ * [O].  IDOT4 read from the environment once, as nn/matmul.c:76-77.
+ * Served for I % 16 == 0. */
+int moty_hip_matmul_i4_s(float *y, const float *x, const uint8_t *q4, const float *scale, int S, int I, int O);
+/* HwBackend.matmul_i4 slot (hw/hw_backend.h:59-60), void: on failure every
+ * y[S*O] is a quiet NaN and moty_hip_last_error() says why. */
+void moty_hip_hw_matmul_i4(float *y, const float *x, const uint8_t *q4, const float *scale, int S, int I, int O);
+
 /* ---------------- device-pointer entry points ---------------- */
 /* qrow_i8 over S rows (hw/hw_quant.h:9-16): q [S][I], sx [S]; xg [S][I/32]
  * group sums when non-NULL (I % 32 == 0). */
@@ -184,6 +193,11 @@ int moty_hip_quantize_rows_dev(const float *w, int8_t *q, float *scale, int O, i
 /* moty_pack_int4_grouped (nn/quant.c:57-83); gs % 16 == 0 as the reference requires */
 int moty_hip_pack_int4_grouped_dev(const float *w, uint8_t *q4, float *scale, int O, int I, int gs,
                                    void *stream);
+/* moty_pack_int4 (nn/quant.c:34-55): per-row int4 q4 [O][(I+1)/2], scale [O] */
+int moty_hip_pack_int4_dev(const float *w, uint8_t *q4, float *scale, int O, int I, void *stream);
+/* moty_matmul_i4_s; idot4 selects the int8-activation path explicitly */
+int moty_hip_matmul_i4_s_dev(float *y, const float *x, const uint8_t *q4, const float *scale, int S, int I, int O,
+                             int idot4, void *stream);
 /* moty_matmul_q_s: S <= 4 runs the decode GEMV with fused activation
  * quantization, larger S quantizes then runs the int8 MFMA GEMM. */
 int moty_hip_matmul_q_s_dev(float *y, const float *x, const int8_t *q, const float *scale, int S, int I, int O,

@@ -71,6 +71,10 @@ SIGNATURES = {
     "moty_hip_moe_topk": (I32, [C.POINTER(MotyHipMoe), P, I32, P]),
     "moty_hip_weight_forget": (I32, [P]),
     "moty_hip_hw_matmul_i8": (None, [P, P, P, P, I32, I32, I32]),
+    "moty_hip_matmul_i4_s": (I32, [P, P, P, P, I32, I32, I32]),
+    "moty_hip_hw_matmul_i4": (None, [P, P, P, P, I32, I32, I32]),
+    "moty_hip_pack_int4_dev": (I32, [P, P, P, I32, I32, P]),
+    "moty_hip_matmul_i4_s_dev": (I32, [P, P, P, P, I32, I32, I32, I32, P]),
     "moty_hip_qrow_i8_dev": (I32, [P, P, P, P, I32, I32, P]),
     "moty_hip_quantize_rows_dev": (I32, [P, P, P, I32, I32, I32, P]),
     "moty_hip_pack_int4_grouped_dev": (I32, [P, P, P, I32, I32, I32, P]),

@@ -329,6 +329,38 @@ int moty_hip_matmul_i4_grouped_s_dev(float* y, const float* x, const uint8_t* q4
   return MOTY_EUNSUP;
 }
 
+int moty_hip_pack_int4_dev(const float* w, uint8_t* q4, float* scale, int O, int I, void* stream) {
+  CUR(d);
+  if (O < 0 || I <= 0 || !w || !q4 || !scale) return set_error("pack_int4: bad arguments"), MOTY_EINVAL;
+  return launch_pack_i4row(w, q4, scale, O, I, STREAM(stream));
+}
+
+// moty_matmul_i4_s (nn/matmul.c:75-145), per-row int4 weights.  IDOT4: the
+// nibbles expand to int8 codes n - 8 in scratch and the Q8 kernels run the
+// integer dot with the same (scale*sx)*acc epilogue; otherwise the exact
+// f32 path.  I % 16 == 0 (the AVX2 step of the f32 path; other widths stay
+// on the CPU).
+int moty_hip_matmul_i4_s_dev(float* y, const float* x, const uint8_t* q4, const float* scale, int S, int I, int O,
+                             int idot4, void* stream) {
+  CUR(d);
+  if (S < 0 || I <= 0 || O < 0 || !y || !x || !q4 || !scale) return set_error("matmul_i4_s: bad arguments"), MOTY_EINVAL;
+  if (S == 0 || O == 0) return MOTY_OK;
+  if (I % 16) return set_error("matmul_i4_s: I=%d unsupported (I %% 16 == 0)", I), MOTY_EUNSUP;
+  hipStream_t st = STREAM(stream);
+  if (!idot4 || I > 16384) return launch_i4row_f32(x, q4, scale, y, S, I, O, st);
+  const size_t bw = al256((size_t)O * I), bx = al256((size_t)S * I);
+  void* sp;
+  int rc = scratch_get(d, bw + bx + al256((size_t)S * 4), st, &sp);
+  if (rc) return rc;
+  int8_t* w8 = (int8_t*)sp;
+  if ((rc = launch_i4row_to_i8(q4, w8, (int64_t)O * I, st))) return rc;
+  if (S <= GEMV_MAX_S) return launch_gemv_q8(x, w8, scale, nullptr, nullptr, y, S, I, O, st);
+  int8_t* xq = (int8_t*)sp + bw;
+  float* sx = (float*)((char*)sp + bw + bx);
+  if ((rc = launch_qrow_i8(x, xq, sx, nullptr, S, I, I, I, st))) return rc;
+  return launch_gemm_q8(xq, sx, w8, scale, y, S, I, O, st);
+}
+
 int moty_hip_matmul_dev(float* y, const float* x, const float* W, int S, int I, int O, void* stream) {
   CUR(d);
   if (S < 0 || I <= 0 || O < 0 || !y || !x || !W) return set_error("matmul: bad arguments"), MOTY_EINVAL;
@@ -795,6 +827,35 @@ int moty_hip_matmul_i4_grouped_s(float* y, const float* x, const uint8_t* q4, co
                                              I, O, gs, idot4, d->stream)))
     return rc;
   return finish_io(d, y, dy, (size_t)S * O * 4);
+}
+
+// moty_matmul_i4_s on host pointers; IDOT4 read from the environment once
+// (nn/matmul.c:76-77)
+int moty_hip_matmul_i4_s(float* y, const float* x, const uint8_t* q4, const float* scale, int S, int I, int O) {
+  CUR(d);
+  if (S < 0 || I <= 0 || O < 0 || !y || !x || !q4 || !scale) return set_error("matmul_i4_s: bad arguments"), MOTY_EINVAL;
+  static const int idot4 = env_int("IDOT4", 0);
+  if (S == 0 || O == 0) return MOTY_OK;
+  if (I % 16) return set_error("matmul_i4_s: I=%d unsupported (I %% 16 == 0)", I), MOTY_EUNSUP;
+  const void *dq, *ds;
+  int rc;
+  if ((rc = weight(d, q4, (size_t)O * ((I + 1) / 2), &dq))) return rc;
+  if ((rc = weight(d, scale, (size_t)O * 4, &ds))) return rc;
+  void *dx, *dy;
+  if ((rc = stage_io(d, x, (size_t)S * I * 4, (size_t)S * O * 4, &dx, &dy))) return rc;
+  if ((rc = moty_hip_matmul_i4_s_dev((float*)dy, (const float*)dx, (const uint8_t*)dq, (const float*)ds, S, I, O,
+                                     idot4, d->stream)))
+    return rc;
+  return finish_io(d, y, dy, (size_t)S * O * 4);
+}
+
+// HwBackend.matmul_i4 (hw/hw_backend.h:59-60), void like matmul_i8: a
+// failed call leaves every y a quiet NaN and its message.
+void moty_hip_hw_matmul_i4(float* y, const float* x, const uint8_t* q4, const float* scale, int S, int I, int O) {
+  if (moty_hip_matmul_i4_s(y, x, q4, scale, S, I, O) != MOTY_OK && y && S > 0 && O > 0) {
+    const float nan = __builtin_nanf("");
+    for (int64_t i = 0; i < (int64_t)S * O; i++) y[i] = nan;
+  }
 }
 
 int moty_hip_matmul(float* y, const float* x, const float* W, int S, int I, int O) {

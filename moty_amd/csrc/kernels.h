@@ -17,6 +17,13 @@ int launch_qrow_i8(const float* x, int8_t* q, float* sx, int32_t* xg, int S, int
 // qrow_i8 with f16 codes in the k-permuted run order of the f16-MFMA
 // grouped-int4 GEMM; I % 8 == 0, I <= 16384, x and xh 16-byte aligned
 int launch_qrow_f16p(const float* x, uint16_t* xh, float* sx, int S, int I, hipStream_t st);
+// per-row int4 weights (WF_I4, nn/quant.c:34-55) and their expansion to
+// int8 codes n - 8 (I % 16 == 0; n = O * I codes)
+int launch_pack_i4row(const float* w, uint8_t* q4, float* scale, int O, int I, hipStream_t st);
+int launch_i4row_to_i8(const uint8_t* q4, int8_t* q8, int64_t n, hipStream_t st);
+// the exact f32 path of moty_matmul_i4_s (I % 16 == 0)
+int launch_i4row_f32(const float* x, const uint8_t* q4, const float* scale, float* y, int S, int I, int O,
+                     hipStream_t st);
 int launch_quantize_rows(const float* w, int8_t* q, float* scale, int O, int I, int bits, hipStream_t st);
 int launch_pack_i4g(const float* w, uint8_t* q4, float* scale, int O, int I, int gs, hipStream_t st);
 

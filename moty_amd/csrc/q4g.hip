@@ -719,6 +719,51 @@ __global__ __launch_bounds__(Q4F_NT) void k_i4g_f32(const float* __restrict__ x,
   y[(int64_t)s * O + o] = a;
 }
 
+// ---------------------------------------------------------------------------
+// Per-row int4 (WF_I4), exact f32 path of moty_matmul_i4_s
+// (nn/matmul.c:102-145) in the x86-64 AVX2 order: eight accumulator lanes,
+// lane j takes elements i+j then i+8+j of each 16-element step (an FMA each),
+// then simd_hsum256_f32's tree (hw/hw_avx2.h:16-20), y = a * scale.  Lane
+// per (row, token), I % 16 == 0.
+__global__ __launch_bounds__(256) void k_i4row_f32(const float* __restrict__ x, const uint8_t* __restrict__ q4,
+                                                   const float* __restrict__ scale, float* __restrict__ y, int S,
+                                                   int I, int O) {
+  const int s = blockIdx.y;
+  const int o = blockIdx.x * 256 + threadIdx.x;
+  if (o >= O) return;
+  const float* xs = x + (int64_t)s * I;
+  const uint8_t* w = q4 + (int64_t)o * (I / 2);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < I; i += 16) {
+    const uint2 wb = *(const uint2*)(w + i / 2);
+    const uint32_t wd[2] = {wb.x, wb.y};
+    float xv[16];
+#pragma unroll
+    for (int q = 0; q < 4; q++) *(float4*)(xv + 4 * q) = *(const float4*)(xs + i + 4 * q);
+#pragma unroll
+    for (int half = 0; half < 2; half++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int e = 8 * half + j;  // element i + e: byte e / 2, low nibble when even
+        const uint32_t byte = (wd[e >> 3] >> (8 * ((e >> 1) & 3))) & 0xffu;
+        const int n = (e & 1) ? (int)(byte >> 4) : (int)(byte & 15u);
+        acc[j] = __fmaf_rn(xv[e], (float)(n - 8), acc[j]);
+      }
+  }
+  const float a0 = acc[0] + acc[4], a1 = acc[1] + acc[5], a2 = acc[2] + acc[6], a3 = acc[3] + acc[7];
+  const float b0 = a0 + a2, b1 = a1 + a3;
+  y[(int64_t)s * O + o] = (b0 + b1) * scale[o];
+}
+
+int launch_i4row_f32(const float* x, const uint8_t* q4, const float* scale, float* y, int S, int I, int O,
+                     hipStream_t st) {
+  if (I % 16) return MOTY_EUNSUP;
+  if (S <= 0 || O <= 0) return MOTY_OK;
+  hipLaunchKernelGGL(k_i4row_f32, dim3((O + 255) / 256, S), dim3(256), 0, st, x, q4, scale, y, S, I, O);
+  LAUNCH_TRY("k_i4row_f32");
+  return MOTY_OK;
+}
+
 // NT = 256 or 512 threads: wider workgroups amortize the activation row
 // (read once per workgroup) over more weight rows when I is large
 template <int RW, int NGC, bool PAIR, int NT>

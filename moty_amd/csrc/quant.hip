@@ -265,6 +265,72 @@ int launch_qrow_f16p(const float* x, uint16_t* xh, float* sx, int S, int I, hipS
   return MOTY_OK;
 }
 
+// Per-row int4 weights (nn/quant.c:34-55): s = amax/7 clamped at 1e-8,
+// v = clip(rint(w/s), -8, 7), even element in the low nibble.  One
+// workgroup per row.
+template <int NT>
+__global__ __launch_bounds__(NT) void k_pack_i4row(const float* __restrict__ w, uint8_t* __restrict__ q4,
+                                                   float* __restrict__ scale, int I) {
+  __shared__ float red[NT / MOTY_WAVE];
+  const int64_t row = blockIdx.x;
+  const float* wr = w + row * (int64_t)I;
+  uint8_t* qr = q4 + row * (int64_t)((I + 1) / 2);
+  float amax = 0.f;
+  for (int i = threadIdx.x; i < I; i += NT) amax = fmaxf(amax, fabsf(wr[i]));
+  amax = block_max<NT>(amax, red);
+  float s = amax / 7.f;
+  if (s < 1e-8f) s = 1e-8f;
+  if (threadIdx.x == 0) scale[row] = s;
+  for (int i = 2 * threadIdx.x; i < I; i += 2 * NT) {
+    int v0 = rne_int(wr[i] / s);
+    v0 = v0 > 7 ? 7 : (v0 < -8 ? -8 : v0);
+    int v1 = 0;
+    if (i + 1 < I) {
+      v1 = rne_int(wr[i + 1] / s);
+      v1 = v1 > 7 ? 7 : (v1 < -8 ? -8 : v1);
+    }
+    qr[i >> 1] = (uint8_t)((v0 + 8) | ((v1 + 8) << 4));
+  }
+}
+
+int launch_pack_i4row(const float* w, uint8_t* q4, float* scale, int O, int I, hipStream_t st) {
+  if (O <= 0) return MOTY_OK;
+  hipLaunchKernelGGL(k_pack_i4row<256>, dim3(O), dim3(256), 0, st, w, q4, scale, I);
+  LAUNCH_TRY("k_pack_i4row");
+  return MOTY_OK;
+}
+
+// Per-row int4 rows -> int8 rows n - 8 (the codes dot_i4i8 multiplies,
+// hw/hw_scalar.h:14-22), so the Q8 kernels run the integer dot.  I % 16 == 0;
+// thread per 8 input bytes.
+__global__ __launch_bounds__(256) void k_i4row_to_i8(const uint8_t* __restrict__ q4, int8_t* __restrict__ q8,
+                                                     int64_t n8) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n8) return;
+  const uint2 w = *(const uint2*)(q4 + 8 * i);
+  const uint32_t wd[2] = {w.x, w.y};
+  uint32_t o[4];
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    // bytes b0..b3 of wd[k] hold elements 2j (low) and 2j+1 (high)
+    const uint32_t lo = wd[k] & 0x0f0f0f0fu, hi = (wd[k] >> 4) & 0x0f0f0f0fu;
+    const uint32_t e01 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);  // lo0 hi0 lo1 hi1
+    const uint32_t e23 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // lo2 hi2 lo3 hi3
+    // n - 8 per byte without carries: (n + 0x78) ^ 0x80
+    o[2 * k] = (e01 + 0x78787878u) ^ 0x80808080u;
+    o[2 * k + 1] = (e23 + 0x78787878u) ^ 0x80808080u;
+  }
+  *(uint4*)(q8 + 16 * i) = uint4{o[0], o[1], o[2], o[3]};
+}
+
+int launch_i4row_to_i8(const uint8_t* q4, int8_t* q8, int64_t n, hipStream_t st) {
+  const int64_t n8 = n / 16;  // 8 input bytes (16 codes) per thread
+  if (n8 <= 0) return MOTY_OK;
+  hipLaunchKernelGGL(k_i4row_to_i8, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st, q4, q8, n8);
+  LAUNCH_TRY("k_i4row_to_i8");
+  return MOTY_OK;
+}
+
 int launch_quantize_rows(const float* w, int8_t* q, float* scale, int O, int I, int bits, hipStream_t st) {
   if (O <= 0) return MOTY_OK;
   hipLaunchKernelGGL(k_quantize_rows<256>, dim3(O), dim3(256), 0, st, w, q, scale, I, bits);

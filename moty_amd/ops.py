@@ -75,6 +75,27 @@ def matmul_q8_preq(xq, sx, q, scale, out=None):
     return y
 
 
+def pack_int4(w):
+    """nn/quant.c:34-55: per-row int4 (q4 uint8 [O,(I+1)/2], scale [O])."""
+    _dev(w)
+    O, I = w.shape
+    q4 = torch.empty((O, (I + 1) // 2), dtype=torch.uint8, device=w.device)
+    s = torch.empty(O, dtype=torch.float32, device=w.device)
+    check(lib().moty_hip_pack_int4_dev(_p(w), _p(q4), _p(s), O, I, _stream()), "pack_int4")
+    return q4, s
+
+
+def matmul_i4_s(x, q4, scale, idot4=True, out=None):
+    """nn/matmul.c:75-145, per-row int4 weights."""
+    _dev(x, q4, scale)
+    S, I = x.shape
+    O = q4.shape[0]
+    y = out if out is not None else torch.empty((S, O), dtype=torch.float32, device=x.device)
+    check(lib().moty_hip_matmul_i4_s_dev(_p(y), _p(x), _p(q4), _p(scale), S, I, O, int(bool(idot4)), _stream()),
+          "matmul_i4_s")
+    return y
+
+
 def matmul_i4_grouped_s(x, q4, scale, gs=32, idot4=True, out=None):
     """nn/matmul.c:164-197 (idot4 picks the IDOT4=1 branch)."""
     _dev(x, q4, scale)

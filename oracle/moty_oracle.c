@@ -11,12 +11,14 @@
  * this file is compiled with -ffp-contract=off, so every FMA below is explicit.
  *
  * Pinning (what checks each function beyond retyping it):
- *   o_qrow_i8, o_quantize_rows, o_pack_int4_grouped  -> compiled reference
+ *   o_qrow_i8, o_quantize_rows, o_pack_int4_grouped, o_pack_int4 -> compiled reference
  *       (oracle/_ref), reconstruction bound |x - s*q| <= s/2, golden fixtures
  *   o_dot_i8i8, o_matmul_q_s   -> brute-force int64 sums, _ref, fixtures,
  *       batch invariance (S rows == S single calls)
  *   o_dot_i4g8p, o_matmul_i4g_idot4, o_matmul_i4g_f32 -> _ref, and a double
  *       dequant reference within the reference's own tolerance
+ *   o_matmul_i4_idot4 (per-row int4) -> _ref, brute-force int64 sums
+ *   o_matmul_i4_f32 -> _ref bit-exact at I % 16 == 0, double dequant sum
  *   o_dot_f32 (AVX512 lane order), o_matmul_f32  -> _ref bit-exact, double sum
  *   o_expf     -> exhaustive over all 2^32 inputs against libm expf
  *   o_softmax, o_silu_mul, o_topk -> _ref, naive greedy top-k
@@ -85,6 +87,91 @@ O_EXPORT void o_quantize_rows(const float *w, int8_t *q, float *scale, int O, in
 /* a6: grouped int4 packing, f32 scale amax/7 per group, nibble = v+8,
  * even element in the low nibble.  nn/quant.c:57-83 (gs % 16 == 0 is
  * checked by the caller, quant.c:80). */
+/* Per-row int4 weights (WF_I4): nn/quant.c:34-55 (pack_int4_part, bits 4):
+ * s = amax/7.f clamped at 1e-8, v = clip(lrintf(w/s), -8, 7), byte =
+ * (v0+8) | (v1+8) << 4 with the even element in the low nibble. */
+O_EXPORT void o_pack_int4(const float *w, uint8_t *q4, float *scale, int O, int I) {
+    int rb = (I + 1) / 2;
+    for (int o = 0; o < O; o++) {
+        const float *wr = w + (int64_t)o * I;
+        float amax = 0.f;
+        for (int i = 0; i < I; i++) { float a = fabsf(wr[i]); if (a > amax) amax = a; }
+        float s = amax / 7.f;
+        if (s < 1e-8f) s = 1e-8f;
+        scale[o] = s;
+        uint8_t *qr = q4 + (int64_t)o * rb;
+        for (int i = 0; i < I; i += 2) {
+            int v0 = (int)lrintf(wr[i] / s);
+            if (v0 > 7) v0 = 7;
+            if (v0 < -8) v0 = -8;
+            int v1 = 0;
+            if (i + 1 < I) {
+                v1 = (int)lrintf(wr[i + 1] / s);
+                if (v1 > 7) v1 = 7;
+                if (v1 < -8) v1 = -8;
+            }
+            qr[i >> 1] = (uint8_t)((v0 + 8) | ((v1 + 8) << 4));
+        }
+    }
+}
+
+/* moty_matmul_i4_s (nn/matmul.c:75-100), IDOT4 = 1 and I <= 16384: x
+ * quantized per row (qrow_i8), dot_i4i8 (hw/hw_scalar.h:14-22: sum of
+ * (n-8)*x, exact), y = (scale[o]*sx[s]) * (float)dot. */
+O_EXPORT void o_matmul_i4_idot4(float *y, const float *x, const uint8_t *q4, const float *scale,
+                                int S, int I, int O) {
+    int8_t *xi = malloc((size_t)S * I);
+    float *sx = malloc(sizeof(float) * (size_t)S);
+    for (int s = 0; s < S; s++) sx[s] = o_qrow_i8(x + (int64_t)s * I, xi + (int64_t)s * I, I);
+    int rb = (I + 1) / 2;
+    #pragma omp parallel for schedule(static)
+    for (int o = 0; o < O; o++) {
+        const uint8_t *w4 = q4 + (int64_t)o * rb;
+        for (int s = 0; s < S; s++) {
+            const int8_t *xs = xi + (int64_t)s * I;
+            int64_t d = 0;
+            for (int i = 0; i < I; i++) {
+                int n = (i & 1) ? (w4[i >> 1] >> 4) : (w4[i >> 1] & 15);
+                d += (int64_t)(n - 8) * xs[i];
+            }
+            y[(int64_t)s * O + o] = (scale[o] * sx[s]) * (float)(int32_t)d;
+        }
+    }
+    free(xi); free(sx);
+}
+
+/* moty_matmul_i4_s, exact f32 path (i4_f32_rows, nn/matmul.c:102-145) as
+ * the x86-64 AVX2 branch evaluates it for I % 16 == 0: eight accumulator
+ * lanes, lane j takes elements i+j (first FMA) and i+8+j (second) of each
+ * 16-element step, acc = fma(x, (float)(n-8), acc); then simd_hsum256_f32
+ * (hw/hw_avx2.h:16-20): (l0+l4, l1+l5, l2+l6, l3+l7), then (a0+a2, a1+a3),
+ * then their sum; y = a * scale[o]. */
+O_EXPORT void o_matmul_i4_f32(float *y, const float *x, const uint8_t *q4, const float *scale,
+                              int S, int I, int O) {
+    int rb = (I + 1) / 2;
+    #pragma omp parallel for schedule(static)
+    for (int o = 0; o < O; o++) {
+        const uint8_t *w = q4 + (int64_t)o * rb;
+        for (int s = 0; s < S; s++) {
+            const float *xs = x + (int64_t)s * I;
+            float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            for (int i = 0; i + 16 <= I; i += 16) {
+                for (int j = 0; j < 8; j++) {
+                    int e = i + j, n = (e & 1) ? (w[e >> 1] >> 4) : (w[e >> 1] & 15);
+                    acc[j] = fmaf(xs[e], (float)(n - 8), acc[j]);
+                }
+                for (int j = 0; j < 8; j++) {
+                    int e = i + 8 + j, n = (e & 1) ? (w[e >> 1] >> 4) : (w[e >> 1] & 15);
+                    acc[j] = fmaf(xs[e], (float)(n - 8), acc[j]);
+                }
+            }
+            float a0 = acc[0] + acc[4], a1 = acc[1] + acc[5], a2 = acc[2] + acc[6], a3 = acc[3] + acc[7];
+            float b0 = a0 + a2, b1 = a1 + a3;
+            y[(int64_t)s * O + o] = (b0 + b1) * scale[o];
+        }
+    }
+}
+
 O_EXPORT void o_pack_int4_grouped(const float *w, uint8_t *q4, float *scale, int O, int I, int gs) {
     int rb = (I + 1) / 2, ng = (I + gs - 1) / gs;
     for (int o = 0; o < O; o++) {

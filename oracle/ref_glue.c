@@ -18,7 +18,8 @@
 
 #define R_EXPORT __attribute__((visibility("default")))
 
-/* IDOT4 is read once per process by nn/matmul.c:171; call before anything. */
+/* IDOT4 is read once per process by nn/matmul.c:171 (and :76-77 for the
+ * per-row int4 path); call before anything. */
 R_EXPORT void ref_init(int idot4) {
     unsetenv("IDOT");
     if (idot4) setenv("IDOT4", "1", 1); else unsetenv("IDOT4");
@@ -27,6 +28,7 @@ R_EXPORT void ref_init(int idot4) {
     static int8_t q[64]; static uint8_t q4[32];
     moty_matmul_q_s(y, x, q, s, 1, 64, 1);
     moty_matmul_i4_grouped_s(y, x, q4, s, 1, 64, 1, 32);
+    moty_matmul_i4_s(y, x, q4, s, 1, 64, 1);  /* its own latch (nn/matmul.c:76-77) */
 }
 R_EXPORT const char *ref_tier(void) { return HW_IDOT_KERNEL "/" HW_F32_KERNEL; }
 R_EXPORT float ref_qrow_i8(const float *x, int8_t *q, int n) { return moty_hw_qrow_i8(x, q, n); }

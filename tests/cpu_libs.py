@@ -36,6 +36,11 @@ _SIGS = {
     "o_matmul_q_s": (None, [P, P, P, P, I32, I32, I32]),
     "o_matmul_q8_preq": (None, [P, P, P, P, P, P, I32, I32, I32]),
     "o_dot_i4g8p": (F32, [P, P, P, P, I32]),
+    "o_pack_int4": (None, [P, P, P, I32, I32]),
+    "o_matmul_i4_idot4": (None, [P, P, P, P, I32, I32, I32]),
+    "o_matmul_i4_f32": (None, [P, P, P, P, I32, I32, I32]),
+    "moty_pack_int4": (None, [P, P, P, I32, I32]),
+    "moty_matmul_i4_s": (None, [P, P, P, P, I32, I32, I32]),
     "o_matmul_i4g_idot4": (None, [P, P, P, P, I32, I32, I32]),
     "o_matmul_i4g_f32": (None, [P, P, P, P, I32, I32, I32]),
     "o_dot_f32": (F32, [P, P, I32]),
@@ -199,6 +204,23 @@ def o_matmul_i4g(x, q4, scale, idot4=True):
     y = np.empty((S, O), np.float32)
     fn = oracle().o_matmul_i4g_idot4 if idot4 else oracle().o_matmul_i4g_f32
     fn(ptr(y), ptr(x), ptr(q4), ptr(scale), S, I, O)
+    return y
+
+
+def o_pack_int4(w):
+    O, I = w.shape
+    q4 = np.empty((O, (I + 1) // 2), np.uint8)
+    s = np.empty(O, np.float32)
+    oracle().o_pack_int4(ptr(f32(w)), ptr(q4), ptr(s), O, I)
+    return q4, s
+
+
+def o_matmul_i4(x, q4, scale, idot4=True):
+    x = f32(x)
+    S, I = x.shape
+    O = q4.shape[0]
+    y = np.empty((S, O), np.float32)
+    (oracle().o_matmul_i4_idot4 if idot4 else oracle().o_matmul_i4_f32)(ptr(y), ptr(x), ptr(q4), ptr(scale), S, I, O)
     return y
 
 

@@ -220,3 +220,27 @@ def test_scratch_shared_across_streams(lib):
         torch.cuda.synchronize()
         assert same_bits(to_np(y1), r1)
         assert same_bits(to_np(y2), r2)
+
+
+def test_hw_matmul_i4_slot(lib, idot4_env):
+    # HwBackend.matmul_i4 (hw/hw_backend.h:59-60): moty_matmul_i4_s with the
+    # process's IDOT4, through the host-pointer path; an unsupported width
+    # (I % 16 != 0) leaves NaNs and a message
+    from cpu_libs import o_matmul_i4, o_pack_int4
+    S, I, O = 3, 256, 40
+    q4, s = o_pack_int4(randn(50, (O, I), 0.02))
+    x = randn(51, (S, I))
+    y = np.full((S, O), np.nan, np.float32)
+    try:
+        assert lib.moty_hip_matmul_i4_s(P(y), P(x), P(q4), P(s), S, I, O) == 0, lib.moty_hip_last_error()
+        y2 = o_matmul_i4(x, q4, s, bool(idot4_env))
+        assert same_bits(y, y2), mismatch(y, y2)
+        y3 = np.zeros((S, O), np.float32)
+        lib.moty_hip_hw_matmul_i4(P(y3), P(x), P(q4), P(s), S, I, O)
+        assert same_bits(y3, y2)
+        q5, s5 = o_pack_int4(randn(52, (O, 40), 0.02))
+        y4 = np.zeros((S, O), np.float32)
+        lib.moty_hip_hw_matmul_i4(P(y4), P(randn(53, (S, 40))), P(q5), P(s5), S, 40, O)
+        assert np.isnan(y4).all() and lib.moty_hip_last_error()
+    finally:
+        forget(lib, q4, s)

@@ -222,3 +222,30 @@ def test_dense_ffn_i4g(ops, idot4, S, D, I):
     oracle().o_silu_mul(ptr(g), ptr(u), g.size)
     y2 = o_matmul_i4g(g, dq, ds, idot4 and I % 64 == 0)
     assert same_bits(y, y2), mismatch(y, y2)
+
+
+@pytest.mark.parametrize("O,I", [(37, 64), (5, 33), (300, 4096), (9, 1)])
+def test_pack_int4(ops, O, I):
+    # per-row int4 (WF_I4), nn/quant.c:34-55
+    from cpu_libs import o_pack_int4
+    say("pack_int4", O, I)
+    w = randn(O + I, (O, I), 0.02)
+    w[0] = 0.0
+    q4, s = ops.pack_int4(to_dev(w))
+    q2, s2 = o_pack_int4(w)
+    assert same_bits(to_np(q4), q2) and same_bits(to_np(s), s2)
+
+
+@pytest.mark.parametrize("idot4", [True, False])
+@pytest.mark.parametrize("S,I,O", [(1, 4096, 256), (3, 1024, 100), (4, 96, 17), (37, 2048, 300), (512, 1024, 1024),
+                                   (9, 16, 5)])
+def test_matmul_i4_s(ops, idot4, S, I, O):
+    # moty_matmul_i4_s (nn/matmul.c:75-145): int8 GEMV/GEMM over the
+    # expanded codes (IDOT4) or the AVX2-order exact f32 path
+    from cpu_libs import o_matmul_i4, o_pack_int4
+    say("matmul_i4_s", idot4, S, I, O)
+    q4, s = o_pack_int4(randn(O + 2 * I, (O, I), 0.02))
+    x = randn(S + I, (S, I))
+    y = to_np(ops.matmul_i4_s(to_dev(x), to_dev(q4), to_dev(s), idot4))
+    y2 = o_matmul_i4(x, q4, s, idot4)
+    assert same_bits(y, y2), mismatch(y, y2)

@@ -364,3 +364,51 @@ def test_moe_batch_matches_ref_at_c5(skewed):
     cnt = np.bincount(idx.ravel(), minlength=E)
     if skewed:
         assert cnt[hot].sum() > 0.5 * cnt.sum()
+
+
+# ---- per-row int4 (WF_I4): the HwBackend.matmul_i4 slot ----
+@needs_ref
+@pytest.mark.parametrize("O,I", [(37, 64), (5, 33), (64, 4096), (9, 1)])
+def test_pack_int4_matches_ref(O, I):
+    from cpu_libs import o_pack_int4
+    w = randn(O + I, (O, I), 0.02)
+    w[0] = 0.0  # the 1e-8 clamp
+    q4, s = o_pack_int4(w)
+    q2 = np.empty_like(q4)
+    s2 = np.empty_like(s)
+    ref(True).moty_pack_int4(ptr(w), ptr(q2), ptr(s2), O, I)
+    assert (q4 == q2).all() and (bits(s) == bits(s2)).all()
+
+
+@needs_ref
+@pytest.mark.parametrize("S,I,O", [(1, 4096, 64), (5, 1024, 33), (3, 96, 17), (2, 64, 8)])
+@pytest.mark.parametrize("idot4", [True, False])
+def test_matmul_i4_matches_ref(S, I, O, idot4):
+    # the reference latches IDOT4 per process: _ref (IDOT4=1) and _ref_f32
+    from cpu_libs import o_matmul_i4, o_pack_int4
+    q4, s = o_pack_int4(randn(O + 2 * I, (O, I), 0.02))
+    x = randn(S + I, (S, I))
+    y = o_matmul_i4(x, q4, s, idot4)
+    y2 = np.empty_like(y)
+    ref(idot4).moty_matmul_i4_s(ptr(y2), ptr(x), ptr(q4), ptr(s), S, I, O)
+    assert (bits(y) == bits(y2)).all()
+
+
+def test_matmul_i4_idot4_brute_force():
+    # the integer dot against an int64 brute force, and the f32 path against
+    # a double-precision dequantized sum
+    from cpu_libs import o_matmul_i4, o_pack_int4, o_qrow
+    S, I, O = 3, 320, 11
+    q4, s = o_pack_int4(randn(5, (O, I), 0.02))
+    x = randn(6, (S, I))
+    n = np.empty((O, I), np.int64)
+    n[:, 0::2] = (q4 & 15).astype(np.int64) - 8
+    n[:, 1::2] = (q4 >> 4).astype(np.int64) - 8
+    xq, sx = o_qrow(x)
+    d = xq.astype(np.int64) @ n.T
+    y = o_matmul_i4(x, q4, s, True)
+    y2 = (s[None, :] * sx[:, None]).astype(np.float32) * d.astype(np.float32)
+    assert (bits(y) == bits(y2.astype(np.float32))).all()
+    yf = o_matmul_i4(x, q4, s, False)
+    yd = (x.astype(np.float64) @ n.T.astype(np.float64)) * s.astype(np.float64)[None, :]
+    assert np.allclose(yf, yd, rtol=1e-5, atol=1e-5 * np.abs(yd).max())
