@@ -27,6 +27,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA
 METRIC = "Q8 GEMV HBM GB/s (% peak); MoE layer tokens/s at T=256 (1 GPU)"
+HIDDEN = ("x", "Wr", "layer0", "_cpu", "w0")  # inputs kept for the CPU baseline, never printed
 
 
 def parse():
@@ -36,7 +37,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=128)
     ap.add_argument("--quick", action="store_true", help="C1 and C4 only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU reference baseline")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on each CPU baseline sample")
+    ap.add_argument("--cpu-seconds", type=float, default=6.0, help="bound on each CPU baseline sample")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only launch the dominant kernel on distinct weights and a 64 MiB copy (for rocprofv3 --pmc)")
     ap.add_argument("--only", choices=["c2", "c3", "c3r4", "c4", "c5", "q8gemv"],
@@ -316,7 +317,8 @@ def bench_c2(c, steps, warmup):
             "roofline": roofline("mfma", ops_int / t / 1e12, INT8_PEAK_TOPS, "TOP/s"),
             "hbm_gbs": round(algo / t / 1e9, 1),
             "gemms_only": {"ms_per_step": tg * 1e3, "tops": round(ops_int / tg / 1e12, 1)},
-            "library_int_mm": lib_ref}
+            "library_int_mm": lib_ref,
+            "_cpu": {"x": xs, "w": copies[0], "ops_int": ops_int}}
 
 
 def bench_c3(c, steps, warmup):
@@ -327,9 +329,10 @@ def bench_c3(c, steps, warmup):
     ncopy = n_copies(wbytes)
     g = c.gen(2, 1)
     copies = [(c.q4((I, D), g), c.q4((I, D), g), c.q4((D, I), g)) for _ in range(ncopy)]
-    res = {}
+    res = {"_cpu": {"w": copies[0], "x": {}}}
     for M in (1, 256):
         x = c.randn((M, D), c.gen(2, 2))
+        res["_cpu"]["x"][M] = x
         y = torch.empty((M, D), device="cuda:0")
 
         def step(w):
@@ -353,12 +356,13 @@ def bench_q8_gemv_sizes(c, steps, warmup):
     gate/up + SiLU GEMV over the 8B gate and up matrices.  Weights rotate
     past the Infinity Cache like C1's."""
     torch, ops = c.torch, c.ops
-    res = {}
+    res = {"_cpu": {}}
     for O, I in ((4096, 4096), (12288, 4096)):
         wbytes = O * I + O * 4
         g = c.gen(7, O)
         copies = [c.q8((O, I), g) for _ in range(n_copies(wbytes))]
         x = c.randn((1, I), c.gen(7, 1))
+        res["_cpu"]["gemv_%dx%d" % (O, I)] = (x, copies[0], wbytes + (I + O) * 4)
         y = torch.empty((1, O), device="cuda:0")
         t, n = c.time_steps([lambda w=w: ops.matmul_q_s(x, w[0], w[1], out=y) for w in copies], steps, warmup)
         algo = wbytes + (I + O) * 4
@@ -393,9 +397,10 @@ def bench_c3_r4(c, steps, warmup):
     g = c.gen(2, 5)
     copies = [ops.pack_r4(c.randn((2 * I, D), g, 0.02)) + ops.pack_r4(c.randn((D, I), g, 0.02))
               for _ in range(ncopy)]
-    res = {}
+    res = {"_cpu": {"w": copies[0], "x": {}, "I": I}}
     for M in (1, 256):
         x = c.randn((M, D), c.gen(2, 6))
+        res["_cpu"]["x"][M] = x
         y = torch.empty((M, D), device="cuda:0")
         t, n = c.time_steps([lambda w=w: ops.dense_ffn_r4(x, w[0], w[1], w[2], w[3], I, out=y) for w in copies],
                             max(8, steps // (8 if M == 1 else 64)), 8)
@@ -428,6 +433,7 @@ def bench_gguf(c, steps, warmup):
                 for _ in range(n_copies(nb + n * 4, lo=3))]
 
     rs = raws(5)
+    res["_cpu"] = {"O": O, "I": I, "raw": {"repack_Q4_0": (5, rs[0])}}
     q4 = [torch.empty((O, I // 2), dtype=torch.uint8, device="cuda:0") for _ in range(2)]
     qs = [torch.empty((O, I // 32), device="cuda:0") for _ in range(2)]
     lib, P = ops.lib(), ops._p  # raw entry points: no output allocation per call
@@ -449,6 +455,7 @@ def bench_gguf(c, steps, warmup):
         algo = n // E * B + n * 4
         res["dequant_" + names[dt]] = {"us": round(t * 1e6, 2), "algo_bytes": algo,
                                        **roofline("hbm", algo / t / 1e9, HBM_PEAK_GBS, "GB/s")}
+        res["_cpu"]["raw"]["dequant_" + names[dt]] = (dt, rs[0])
         del rs
     return {"workload": "GGUF -> device layouts on a 12288 x 4096 matrix (Q4_0 repack to grouped int4; "
                         "Q8_0/Q4_0/Q4_K/Q5_K/Q6_K dequant to f32)", **res}
@@ -478,68 +485,261 @@ def pmc_probe(c):
 
 
 # --------------------------------------------------------------------------
-def cpu_baseline(c1, c4, budget):
-    """The reference's own CPU kernels (oracle/_ref, kind 'reference'), or the
-    oracle restatement ('port') when the reference build is absent."""
+def cpu_med(fn, budget, nmin=20, warm=3):
+    """Median wall time of fn over at least nmin runs after `warm` warm-ups
+    (CLOCK_MONOTONIC around the call, as c/tests/bench.c), stopping early
+    only past `budget` seconds with 3 runs done; returns (seconds, runs)."""
     import numpy as np
-    sys.path.insert(0, os.path.join(ROOT, "tests"))
-    import cpu_libs as cl
-    r = cl.ref(True)
-    kind = "reference" if r is not None else "port"
-    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    for _ in range(warm):
+        fn()
+    ts = []
+    t0 = time.perf_counter()
+    while len(ts) < nmin:
+        a = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - a)
+        if time.perf_counter() - t0 > budget and len(ts) >= 3:
+            break
+    return float(np.median(ts)), len(ts)
+
+
+class CpuRef:
+    """The reference's own kernels (oracle/_ref, built from the reference's
+    sources, kind 'reference': the int8-activation library and the exact
+    IDOT4=0 one), or the oracle restatement ('port') where that build is
+    absent, timed on the host cores with moty's OpenMP tuning."""
+
+    def __init__(self):
+        import numpy as np
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
+        import cpu_libs as cl
+        self.np, self.cl = np, cl
+        self.r = cl.ref(True)
+        self.r32 = cl.ref(False)
+        self.kind = "reference" if self.r is not None else "port"
+        self.cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+
+    def out(self, value, unit, sample, runs, cores=None):
+        return {"value": value, "unit": unit, "cores": cores or self.cores, "kind": self.kind,
+                "sample": "%s; median of %d runs after 3 warm-ups" % (sample, runs)}
+
+    def q_s(self, y, x, q, s):
+        S, I = x.shape
+        O = q.shape[0]
+        if self.r is not None:
+            self.r.ref_matmul_q_s(self.cl.ptr(y), self.cl.ptr(x), self.cl.ptr(q), self.cl.ptr(s), S, I, O)
+        else:
+            y[...] = self.cl.o_matmul_q_s(x, q, s)
+
+    def i4g(self, y, x, q4, s, idot4):
+        S, I = x.shape
+        O = q4.shape[0]
+        r = self.r if idot4 else self.r32
+        if r is not None:
+            r.ref_matmul_i4_grouped_s(self.cl.ptr(y), self.cl.ptr(x), self.cl.ptr(q4), self.cl.ptr(s), S, I, O, 32)
+        else:
+            y[...] = self.cl.o_matmul_i4g(x, q4, s, idot4)
+
+    def silu(self, g, u):
+        if self.r is not None:
+            self.r.ref_silu_mul(self.cl.ptr(g), self.cl.ptr(u), g.size)
+        else:
+            self.cl.oracle().o_silu_mul(self.cl.ptr(g), self.cl.ptr(u), g.size)
+
+    def moe(self, out, x, Wr, ws, E, K, I, D, order, norm, cap=0):
+        cl, T = self.cl, x.shape[0]
+        if self.r is not None:
+            if order == "batch":
+                self.r.ref_moe_batch_cap(cl.ptr(out), cl.ptr(x), T, cl.ptr(Wr), *[cl.ptr(a) for a in ws], E, K, I,
+                                         D, cap or E)
+            else:
+                i2 = self.np.empty((T, K), self.np.int32)
+                self.r.ref_moe_olmoe(cl.ptr(out), cl.ptr(x), T, cl.ptr(Wr), *[cl.ptr(a) for a in ws], E, K, I, D,
+                                     norm, cl.ptr(i2))
+        else:
+            out[...] = cl.o_moe(x, Wr, dict(zip(("G", "GS", "U", "US", "Dn", "DS"), ws)), K, order, norm=norm)[0]
+
+
+def cpu_c1(cr, c1, budget):
+    np = cr.np
     x = c1["x"].cpu().numpy()
     G, GS, U, US, Dn, DS = [t.cpu().numpy() for t in c1["w0"]]
     D, I = 1024, 3072
+    g, u, y = np.empty((1, I), np.float32), np.empty((1, I), np.float32), np.empty((1, D), np.float32)
 
     def ffn():
-        if r is not None:
-            g = np.empty((1, I), np.float32)
-            u = np.empty((1, I), np.float32)
-            y = np.empty((1, D), np.float32)
-            r.ref_matmul_q_s(cl.ptr(g), cl.ptr(x), cl.ptr(G), cl.ptr(GS), 1, D, I)
-            r.ref_matmul_q_s(cl.ptr(u), cl.ptr(x), cl.ptr(U), cl.ptr(US), 1, D, I)
-            r.ref_silu_mul(cl.ptr(g), cl.ptr(u), I)
-            r.ref_matmul_q_s(cl.ptr(y), cl.ptr(g), cl.ptr(Dn), cl.ptr(DS), 1, I, D)
-        else:
-            cl.o_dense_ffn_q8(x, G, GS, U, US, Dn, DS)
+        cr.q_s(g, x, G, GS)
+        cr.q_s(u, x, U, US)
+        cr.silu(g, u)
+        cr.q_s(y, g, Dn, DS)
+    t, n = cpu_med(ffn, budget)
+    return cr.out(round(c1["algo_bytes"] / t / 1e9, 2), "GB/s", "C1 decode FFN (3 matmul_q_s + silu_mul)", n)
 
-    def med(fn, seconds, warm=3, nmin=20):
-        for _ in range(warm):
-            fn()
-        ts = []
-        t0 = time.perf_counter()
-        while len(ts) < nmin or time.perf_counter() - t0 < seconds:
-            a = time.perf_counter()
-            fn()
-            ts.append(time.perf_counter() - a)
-            if time.perf_counter() - t0 > seconds and len(ts) >= 3:
-                break
-        return float(np.median(ts)), len(ts)
 
-    t1, n1 = med(ffn, min(3.0, budget))
-    out = {"value": round(c1["algo_bytes"] / t1 / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": kind,
-           "sample": "C1 decode FFN (3 matmul_q_s + silu_mul), median of %d runs after 3 warm-ups" % n1}
-    if c4 is not None:
-        lay = c4["layer0"]
-        xs = c4["x"].cpu().numpy()
-        Wr = c4["Wr"].cpu().numpy()
-        ws = [t.cpu().numpy() for t in lay.keep[1:7]]
-        T, D4 = xs.shape
-        E, I4, K = lay.E, lay.I, lay.K
-        Tb = 64  # bounded sample: the first 64 tokens of the T=256 batch
+def cpu_moe(cr, r, T_sample, order, norm, budget, nmin=20, skew=None, cap=0):
+    """r: a bench_moe result (its first weight copy and inputs); skew: hot
+    expert ids whose logits the inputs lift by +2.0 (the reference's batch
+    layer takes no logit bias: cpu_libs.skew_inputs expresses it in x and
+    the router); cap: expert-cache slots (0: every expert resident)."""
+    np = cr.np
+    lay = r["layer0"]
+    xs = np.ascontiguousarray(r["x"].cpu().numpy()[:T_sample])
+    Wr = r["Wr"].cpu().numpy()
+    if skew is not None:
+        xs, Wr = cr.cl.skew_inputs(xs, Wr, skew)
+    ws = [t.cpu().numpy() for t in lay.keep[1:7]]
+    out = np.empty((T_sample, lay.D), np.float32)
+    t, n = cpu_med(lambda: cr.moe(out, xs, Wr, ws, lay.E, lay.K, lay.I, lay.D, order, norm, cap), budget,
+                   nmin=nmin, warm=1)
+    return T_sample / t, n
 
-        def moe():
-            o = np.empty((Tb, D4), np.float32)
-            if r is not None:
-                i2 = np.empty((Tb, K), np.int32)
-                r.ref_moe_olmoe(cl.ptr(o), cl.ptr(xs[:Tb]), Tb, cl.ptr(Wr), *[cl.ptr(a) for a in ws], E, K, I4, D4,
-                                0, cl.ptr(i2))
+
+def cpu_c2(cr, c2, budget):
+    np = cr.np
+    d = c2["_cpu"]
+    xs = {I: d["x"][I].cpu().numpy() for I in d["x"]}
+    ws = [(q.cpu().numpy(), s.cpu().numpy()) for q, s in d["w"]]
+    ys = [np.empty((x.shape[0], q.shape[0]), np.float32) for x, (q, _) in zip(xs.values(), ws)]
+
+    def step():  # the same three calls (fused q/k/v/gate/up rows, o, down)
+        for (I, x), (q, s), y in zip(xs.items(), ws, ys):
+            cr.q_s(y, x, q, s)
+    t, n = cpu_med(step, budget)
+    return cr.out(round(d["ops_int"] / t / 1e12, 4), "TOP/s", "C2 seven projections at M=512 (3 matmul_q_s calls)", n)
+
+
+def cpu_c3(cr, c3, budget):
+    np = cr.np
+    d = c3["_cpu"]
+    (gq, gs), (uq, us), (dq, ds) = [(q.cpu().numpy(), s.cpu().numpy()) for q, s in d["w"]]
+    res = {}
+    for M, xt in d["x"].items():
+        x = xt.cpu().numpy()
+        D, I = x.shape[1], gq.shape[0]
+        g, u, y = np.empty((M, I), np.float32), np.empty((M, I), np.float32), np.empty((M, D), np.float32)
+        for idot4 in (True, False):
+            def ffn():
+                cr.i4g(g, x, gq, gs, idot4)
+                cr.i4g(u, x, uq, us, idot4)
+                cr.silu(g, u)
+                cr.i4g(y, g, dq, ds, idot4)
+            t, n = cpu_med(ffn, budget / 4)
+            res["M%d_%s" % (M, "idot4" if idot4 else "exact_f32")] = cr.out(
+                round(t * 1e3, 3), "ms/step", "C3 FFN M=%d (matmul_i4_grouped_s x3 + silu_mul, IDOT4=%d)" % (
+                    M, int(idot4)), n)
+    return res
+
+
+def cpu_q8_sizes(cr, r, budget):
+    np = cr.np
+    res = {}
+    for key, (x, (q, s), algo) in r["_cpu"].items():
+        xh, qh, sh = x.cpu().numpy(), q.cpu().numpy(), s.cpu().numpy()
+        y = np.empty((1, qh.shape[0]), np.float32)
+        t, n = cpu_med(lambda: cr.q_s(y, xh, qh, sh), budget / 2)
+        res[key] = cr.out(round(algo / t / 1e9, 2), "GB/s", "matmul_q_s S=1 " + key, n)
+    return res
+
+
+def cpu_r4(cr, r, budget):
+    """moty_matmul_q4r4_s over the row-fused gate_up, silu_rows, down (the
+    reference's dense FFN with a fused gate_up, nn/ffn.c:26-41)."""
+    np, cl = cr.np, cr.cl
+    d = r["_cpu"]
+    gu, gus, dn, dns = [t.cpu().numpy() for t in d["w"]]
+    I = d["I"]
+    res = {}
+    for M, xt in d["x"].items():
+        x = xt.cpu().numpy()
+        D = x.shape[1]
+        g = np.empty((M, 2 * I), np.float32)
+        h = np.empty((M, I), np.float32)
+        y = np.empty((M, D), np.float32)
+
+        def ffn():
+            if cr.r is not None:
+                cr.r.moty_matmul_q4r4_s(cl.ptr(g), cl.ptr(x), cl.ptr(gu), cl.ptr(gus), M, D, 2 * I)
             else:
-                cl.o_moe(xs[:Tb], Wr, dict(zip(("G", "GS", "U", "US", "Dn", "DS"), ws)), K, "olmoe", norm=0)
-        t4, n4 = med(moe, budget, warm=1, nmin=3)
-        out["moe"] = {"value": round(Tb / t4, 1), "unit": "tokens/s", "cores": cores, "kind": kind,
-                      "sample": "C4 OLMoE layer, olmoe engine call sequence (engines/olmoe.c:219-244), "
-                                "first %d of the 256 tokens, median of %d runs" % (Tb, n4)}
+                g[...] = cl.o_matmul_r4(x, gu, gus, 2 * I)
+            h[...] = g[:, :I]
+            cr.silu(h, np.ascontiguousarray(g[:, I:]))
+            if cr.r is not None:
+                cr.r.moty_matmul_q4r4_s(cl.ptr(y), cl.ptr(h), cl.ptr(dn), cl.ptr(dns), M, I, D)
+            else:
+                y[...] = cl.o_matmul_r4(h, dn, dns, D)
+        t, n = cpu_med(ffn, budget / 2)
+        res["M%d" % M] = cr.out(round(t * 1e3, 3), "ms/step", "Q4R4 FFN M=%d (moty_matmul_q4r4_s x2 over the fused "
+                                "gate_up and down, silu_mul)" % M, n)
+    return res
+
+
+def cpu_gguf(cr, r, budget):
+    """io/gguf.h's gguf_repack_q4_0 / gguf_dequant (compiled into oracle/_ref
+    from the reference tree) on the same blocks; GB/s of block bytes read +
+    output bytes written, as the GPU lines."""
+    np, cl = cr.np, cr.cl
+    d = r["_cpu"]
+    O, I = d["O"], d["I"]
+    n = O * I
+    res = {}
+    for key, (dt, raw) in d["raw"].items():
+        rh = raw.cpu().numpy()
+        if dt == 5 and key.startswith("repack"):
+            q4, qs = np.empty(n // 2, np.uint8), np.empty(n // 32, np.float32)
+            fn = (lambda: cr.r.ref_gguf_repack_q4_0(cl.ptr(rh), cl.ptr(q4), cl.ptr(qs), O, I)) if cr.r else (
+                lambda: cl.o_gguf_repack_q4_0(rh, O, I))
+        else:
+            out = np.empty(n, np.float32)
+            fn = (lambda: cr.r.ref_gguf_dequant(dt, cl.ptr(rh), n, cl.ptr(out))) if cr.r else (
+                lambda: cl.o_gguf_dequant(dt, rh, n))
+        t, runs = cpu_med(fn, budget / 6, nmin=5, warm=1)
+        res[key] = cr.out(round(r[key]["algo_bytes"] / t / 1e9, 2), "GB/s", "io/gguf.h %s, one thread" % key, runs,
+                          cores=1)
+    return res
+
+
+def cpu_baseline(c1, c4, extra, budget):
+    """Every config's reference CPU path on the host cores; returns the C1
+    object and attaches the others to their lines."""
+    import numpy as np
+    cr = CpuRef()
+    out = cpu_c1(cr, c1, min(3.0, budget))
+    if c4 is not None:
+        tpo, n1 = cpu_moe(cr, c4, 64, "olmoe", 0, budget, nmin=3)
+        tpb, n2 = cpu_moe(cr, c4, 256, "batch", 1, budget)
+        out["moe"] = cr.out(round(tpb, 1), "tokens/s", "C4 OLMoE layer through moe_batch_core (nn/moe.c:159-205), "
+                            "all 256 tokens", n2)
+        out["moe"]["olmoe_per_token"] = cr.out(round(tpo, 1), "tokens/s", "the olmoe engine's per-token moe() "
+                                               "(engines/olmoe.c:219-244) on the first 64 of the 256 tokens", n1)
+    for r in extra:
+        w = r.get("workload", "")
+        try:
+            if w.startswith("C2"):
+                r["cpu_baseline"] = cpu_c2(cr, r, budget)
+            elif w.startswith("C3 8B"):
+                r["cpu_baseline"] = cpu_c3(cr, r, budget)
+            elif w.startswith("C3 shapes in Q4R4"):
+                r["cpu_baseline"] = cpu_r4(cr, r, budget)
+            elif w.startswith("Q8 decode GEMV"):
+                r["cpu_baseline"] = cpu_q8_sizes(cr, r, budget)
+            elif w.startswith("GGUF"):
+                r["cpu_baseline"] = cpu_gguf(cr, r, budget)
+            elif w.startswith("C5"):
+                sk = "skewed" in w
+                tp, n = cpu_moe(cr, r, 134, "batch", 1, budget, skew=np.arange(0, 128, 16) if sk else None)
+                r["cpu_baseline"] = cr.out(round(tp, 1), "tokens/s", "C5 layer through moe_batch_core on the first "
+                                           "134 of the 1072 tokens (1/8 of the batch)%s" % (
+                                               "; skew as +2.0 on the hot experts' logits through x and the router"
+                                               if sk else ""), n)
+            elif w.startswith("C4 MoE layer shape through the device expert cache") and c4 is not None:
+                res = {}
+                for cap in (64, 32):
+                    tp, n = cpu_moe(cr, c4, 256, "batch", 1, budget / 2, cap=cap, nmin=5)
+                    res["cap%d" % cap] = cr.out(round(tp, 1), "tokens/s", "C4 batch layer over the reference's "
+                                                "ExpertCache (runtime/moecache.c) with %d slots, all 256 tokens" % cap, n)
+                r["cpu_baseline"] = res
+        except Exception as e:  # the baseline is reported, never required
+            log("cpu baseline for %s failed: %s" % (w[:20], e))
     return out
 
 
@@ -566,14 +766,11 @@ def main():
                "c3": lambda: bench_c3(c, args.steps, args.warmup),
                "c3r4": lambda: bench_c3_r4(c, args.steps, args.warmup),
                "q8gemv": lambda: bench_q8_gemv_sizes(c, args.steps, args.warmup),
-               "c4": lambda: {k2: v for k2, v in bench_moe(
-                   c, 3, 256, 64, 8, 1024, 2048, 0, moty_amd.ORDER_TOPK, args.steps, args.warmup,
-                   label="C4 OLMoE MoE layer Q8, T=256").items() if k2 not in ("x", "Wr", "layer0")},
-               "c5": lambda: {k2: v for k2, v in bench_moe(
-                   c, 4, 1072, 128, 8, 768, 2048, 1, moty_amd.ORDER_EXPERT, args.steps, args.warmup,
-                   label="C5 Qwen3-30B-A3B MoE layer Q8, T=1072, uniform").items()
-                   if k2 not in ("x", "Wr", "layer0")}}[args.only]()
-        print(json.dumps(one), flush=True)
+               "c4": lambda: bench_moe(c, 3, 256, 64, 8, 1024, 2048, 0, moty_amd.ORDER_TOPK, args.steps,
+                                       args.warmup, label="C4 OLMoE MoE layer Q8, T=256"),
+               "c5": lambda: bench_moe(c, 4, 1072, 128, 8, 768, 2048, 1, moty_amd.ORDER_EXPERT, args.steps,
+                                       args.warmup, label="C5 Qwen3-30B-A3B MoE layer Q8, T=1072, uniform")}[args.only]()
+        print(json.dumps({k2: v for k2, v in one.items() if k2 not in HIDDEN}), flush=True)
         return
 
     log("C1 decode FFN")
@@ -606,18 +803,19 @@ def main():
             r5 = bench_moe(c, 4, 1072, E5, 8, 768, 2048, 1, moty_amd.ORDER_EXPERT, args.steps, args.warmup, bias=b,
                            label="C5 Qwen3-30B-A3B MoE layer Q8, T=1072 ragged batch (48 decode + 1024 prefill), "
                                  "E=128, top-8, I=768, D=2048, " + lab)
-            for k in ("x", "Wr", "layer0"):
-                r5.pop(k)
             extra.append(r5)
     cpu = None
     if not args.no_cpu:
         log("CPU baseline")
         try:
-            cpu = cpu_baseline(c1, c4, args.cpu_seconds)
+            cpu = cpu_baseline(c1, c4, extra, args.cpu_seconds)
         except Exception as e:  # the baseline is reported, never required
             log("cpu baseline failed:", e)
+    for r in extra:
+        for k in HIDDEN:
+            r.pop(k, None)
     k = c1["kernel"]
-    moe = {k2: v for k2, v in c4.items() if k2 not in ("x", "Wr", "layer0")}
+    moe = {k2: v for k2, v in c4.items() if k2 not in HIDDEN}
     moe["metric"] = "MoE layer tokens/s at T=256 (1 GPU)"
     moe["value"] = round(moe.pop("tokens_per_s"), 1)
     moe["unit"] = "tokens/s"

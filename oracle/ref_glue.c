@@ -73,19 +73,25 @@ static void stack_load(void *ctx, int layer, int eid, ExpertSlot *s, int inter, 
     memcpy(s->ds, st->DS + (int64_t)eid * hidden, sizeof(float) * hidden);
 }
 
-/* moty_nn_moe_topk_batch (nn/moe.c:159-208), f32 router, no shared expert */
-R_EXPORT void ref_moe_batch(float *out, const float *x, int S, const float *Wr,
-                            const int8_t *G, const float *GS, const int8_t *U, const float *US,
-                            const int8_t *Dn, const float *DS, int E, int K, int I, int D) {
+/* moty_nn_moe_topk_batch (nn/moe.c:159-208), f32 router, no shared expert,
+ * over an ExpertCache of `cap` slots (cap >= E: every expert resident) */
+R_EXPORT void ref_moe_batch_cap(float *out, const float *x, int S, const float *Wr,
+                                const int8_t *G, const float *GS, const int8_t *U, const float *US,
+                                const int8_t *Dn, const float *DS, int E, int K, int I, int D, int cap) {
     Mat router; memset(&router, 0, sizeof router);
     router.fmt = WF_F32; router.f = (float *)Wr; router.O = E; router.I = D;
-    ExpertCache ec; moty_expert_cache_init(&ec, E, E);
+    ExpertCache ec; moty_expert_cache_init(&ec, cap, E);
     Stack st = { G, U, Dn, GS, US, DS };
     MotyMoeView v; memset(&v, 0, sizeof v);
     v.router = &router; v.ec = &ec; v.load_expert = stack_load; v.ectx = &st;
     v.E = E; v.K = K; v.I = I; v.D = D; v.ebits = 8;
     moty_nn_moe_topk_batch(&v, x, S, out);
     moty_expert_cache_free(&ec);
+}
+R_EXPORT void ref_moe_batch(float *out, const float *x, int S, const float *Wr,
+                            const int8_t *G, const float *GS, const int8_t *U, const float *US,
+                            const int8_t *Dn, const float *DS, int E, int K, int I, int D) {
+    ref_moe_batch_cap(out, x, S, Wr, G, GS, U, US, Dn, DS, E, K, I, D, E);
 }
 
 /* moty_nn_moe_topk_d1 (nn/moe.c:33-153, S = 1): route_topk (always

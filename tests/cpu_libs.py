@@ -97,6 +97,7 @@ _SIGS = {
     "ref_expf": (F32, [F32]),
     "ref_topk": (None, [P, I32, I32, P, P, I32]),
     "ref_moe_batch": (None, [P, P, I32, P, P, P, P, P, P, P, I32, I32, I32, I32]),
+    "ref_moe_batch_cap": (None, [P, P, I32, P, P, P, P, P, P, P, I32, I32, I32, I32, I32]),
     "ref_moe_d1": (None, [P, P, P, P, P, P, P, P, P, I32, I32, I32, I32]),
     "ref_moe_olmoe": (None, [P, P, I32, P, P, P, P, P, P, P, I32, I32, I32, I32, I32, P]),
 }
