@@ -10,6 +10,7 @@
 // so both stage into LDS the same way and feed the matrix cores alike.
 #include "common.h"
 #include "kernels.h"
+#include <stdlib.h>
 
 namespace moty {
 
@@ -151,23 +152,33 @@ __global__ __launch_bounds__(GM_NT, 2) void k_gemm_q8(const int8_t* __restrict__
 // ds_read_b128 cycle serves (rows r..r+15, one chunk) hit 16 distinct
 // 16-byte bank groups.  A DMA instruction fills 8 rows (1 KiB): lane l loads
 // row l/8's chunk (l%8) ^ ((row >> 1) & 7) into slot l%8.
-template <int BM, int BN, int S>
-__global__ __launch_bounds__(GM_NT) void k_gemm_q8_dma(const int8_t* __restrict__ xq, const float* __restrict__ sx,
-                                                       const int8_t* __restrict__ W, const float* __restrict__ scale,
-                                                       float* __restrict__ y, int M, int K, int O) {
-  constexpr int STAGE = (BM + BN) * GM_KB;
-  constexpr int NI = (BM + BN) / 32;  // DMA instructions per wave per stage
-  constexpr int TM = BM / 2, TN = BN / 2, FM = TM / 32, FN = TN / 32;
-  __shared__ __align__(1024) int8_t lds[S * STAGE];
+// WGM x WGN waves over the block tile (each wave TM x TN outputs).  KS = 2
+// runs two such groups of waves on alternate K blocks (the int32 partial
+// sums are added at the end: exact), doubling the loads and MFMAs in flight
+// per workgroup where the grid has few tiles.
+template <int BM, int BN, int S, int WGM = 2, int WGN = 2, int KS = 1>
+__global__ __launch_bounds__(64 * WGM * WGN * KS) void k_gemm_q8_dma(const int8_t* __restrict__ xq,
+                                                                     const float* __restrict__ sx,
+                                                                     const int8_t* __restrict__ W,
+                                                                     const float* __restrict__ scale,
+                                                                     float* __restrict__ y, int M, int K, int O) {
+  constexpr int NW = WGM * WGN;              // waves per K group
+  constexpr int STAGE = (BM + BN) * GM_KB;   // one K group's share of a stage
+  constexpr int NI = (BM + BN) / (8 * NW);   // DMA instructions per wave per stage
+  constexpr int TM = BM / WGM, TN = BN / WGN, FM = TM / 32, FN = TN / 32;
+  static_assert((BM + BN) % (8 * NW) == 0 && FM >= 1 && FN >= 1, "tile shape");
+  static_assert(KS == 1 || KS * STAGE * S >= NW * 64 * FM * FN * 64, "room for the partial sums");
+  __shared__ __align__(1024) int8_t lds[S * KS * STAGE];
   __shared__ float s_sx[BM];
   const int tid = threadIdx.x, lane = tid % MOTY_WAVE, wv = tid / MOTY_WAVE;
-  const int wm = wv >> 1, wn = wv & 1;
+  const int kg = wv / NW, w = wv % NW;
+  const int wm = w / WGN, wn = w % WGN;
   const int r32 = lane & 31, h = lane >> 5;
   const int mb = blockIdx.y * BM, nb = blockIdx.x * BN;
   const int8_t* src[NI];
 #pragma unroll
   for (int i = 0; i < NI; i++) {
-    const int row = (i * 4 + wv) * 8 + (lane >> 3);
+    const int row = (i * NW + w) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ ((row >> 1) & 7);
     if (row < BM) {
       const int m = mb + row < M ? mb + row : M - 1;  // rows past the end: loaded, never stored
@@ -178,13 +189,16 @@ __global__ __launch_bounds__(GM_NT) void k_gemm_q8_dma(const int8_t* __restrict_
     }
   }
   const int nk = K / GM_KB;
-  // K block kb into stage kb % S; blocks past the end reload the last one
-  // (their stage is never read), so every iteration issues the same count
-  auto issue = [&](int kb) {
+  const int nsb = (nk + KS - 1) / KS;  // iterations: KS K blocks each
+  // iteration sb brings K block sb*KS + kg into this group's part of stage
+  // sb % S; blocks past the end reload the last one (their stage is never
+  // read), so every iteration issues the same count
+  auto issue = [&](int sb) {
+    const int kb = sb * KS + kg;
     const int kc = (kb < nk ? kb : nk - 1) * GM_KB;
-    const uint32_t base = (uint32_t)(uintptr_t)lds + (kb % S) * STAGE + wv * 1024;
+    const uint32_t base = (uint32_t)(uintptr_t)lds + ((sb % S) * KS + kg) * STAGE + w * 1024;
 #pragma unroll
-    for (int i = 0; i < NI; i++) dma16_to_lds(src[i] + kc, __builtin_amdgcn_readfirstlane(base + i * 4 * 1024));
+    for (int i = 0; i < NI; i++) dma16_to_lds(src[i] + kc, __builtin_amdgcn_readfirstlane(base + i * NW * 1024));
   };
   // epilogue scales first: their loads are the oldest, so the vmcnt waits
   // below (which count only the DMAs after them) also cover them
@@ -206,14 +220,15 @@ __global__ __launch_bounds__(GM_NT) void k_gemm_q8_dma(const int8_t* __restrict_
   for (int i = 0; i < FM; i++)
 #pragma unroll
     for (int j = 0; j < FN; j++) acc[i][j] = v16i{};
-  for (int kb = 0; kb < nk; kb++) {
-    // this wave's DMAs of block kb have landed (the S-2 later blocks may
+  for (int sb = 0; sb < nsb; sb++) {
+    // this wave's DMAs of iteration sb have landed (the S-2 later ones may
     // still fly); the barrier makes every wave's share visible and retires
-    // the reads of block kb-1, whose stage the next DMA overwrites
+    // the reads of iteration sb-1, whose stage the next DMA overwrites
     MOTY_WAIT_VMCNT((S - 2) * NI);
     __syncthreads();
-    issue(kb + S - 1);
-    const int8_t* st = lds + (kb % S) * STAGE;
+    issue(sb + S - 1);
+    if (KS > 1 && sb * KS + kg >= nk) continue;  // the group's block is past the end (wave-uniform)
+    const int8_t* st = lds + ((sb % S) * KS + kg) * STAGE;
 #pragma unroll
     for (int j4 = 0; j4 < 4; j4++) {
       // MFMA step j4 takes chunk 4h + j4 of row r32 (a k-permutation shared
@@ -232,10 +247,29 @@ __global__ __launch_bounds__(GM_NT) void k_gemm_q8_dma(const int8_t* __restrict_
     }
   }
   // every DMA (including the reloads past the end) lands before the
-  // workgroup's LDS can be released
+  // workgroup's LDS can be released or reused
   __builtin_amdgcn_s_waitcnt(0);
+  if (KS > 1) {
+    // the second group's partial sums through LDS, added by the first
+    __syncthreads();
+    int* part = (int*)lds + (w * 64 + lane) * (FM * FN * 16);
+    if (kg == 1) {
+#pragma unroll
+      for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) *(v16i*)(part + (i * FN + j) * 16) = acc[i][j];
+    }
+    __syncthreads();
+    if (kg == 0) {
+#pragma unroll
+      for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) acc[i][j] += *(const v16i*)(part + (i * FN + j) * 16);
+    }
+  }
   if (tid < BM) s_sx[tid] = sxr;
   __syncthreads();
+  if (kg) return;
 #pragma unroll
   for (int j = 0; j < FN; j++) {
     const int n = nb + wn * TN + j * 32 + r32;
@@ -259,11 +293,19 @@ int launch_gemm_q8(const int8_t* xq, const float* sx, const int8_t* W, const flo
     // stages for K <= 1024, four for longer rows.  Measured on MI355X, M =
     // 512: N=10240, K=1024: 17.3 us vs 18.8 register-staged; K=2048, N=1024:
     // 7.7 vs 9.6; K=3072: 10.0 vs 12.5.
-    const dim3 grid((O + 63) / 64, (M + 63) / 64);
-    if (K <= 1024)
-      hipLaunchKernelGGL((k_gemm_q8_dma<64, 64, 3>), grid, dim3(GM_NT), 0, st, xq, sx, W, scale, y, M, K, O);
-    else
-      hipLaunchKernelGGL((k_gemm_q8_dma<64, 64, 4>), grid, dim3(GM_NT), 0, st, xq, sx, W, scale, y, M, K, O);
+    // Tiles from a sweep on MI355X at M = 512 (the C2 projections): 64 x 64
+    // tiles of 4 waves while the grid holds at least 256 of them (N = 10240,
+    // K = 1024: 15.2 us); below that 64 x 32 tiles with two groups of 2 waves
+    // on alternate K blocks (N = 1024, K = 2048: 7.1 us vs 7.4; K = 3072: 8.7
+    // vs 9.3) -- these GEMMs are bound by each workgroup's K-loop latency,
+    // not by the grid's width.
+#define QD(BM, BN, S, WM, WN, KS)                                                                             \
+  hipLaunchKernelGGL((k_gemm_q8_dma<BM, BN, S, WM, WN, KS>), dim3((O + BN - 1) / BN, (M + BM - 1) / BM),       \
+                     dim3(64 * WM * WN * KS), 0, st, xq, sx, W, scale, y, M, K, O)
+    if ((int64_t)((M + 63) / 64) * ((O + 63) / 64) < 256 && K >= 2 * GM_KB) QD(64, 32, 4, 2, 1, 2);
+    else if (K <= 1024) QD(64, 64, 3, 2, 2, 1);
+    else QD(64, 64, 4, 2, 2, 1);
+#undef QD
     LAUNCH_TRY("k_gemm_q8_dma");
     return MOTY_OK;
   }
