@@ -104,20 +104,76 @@ __device__ __forceinline__ void dma16_to_lds(const void* g, uint32_t lds_base) {
       : "v"(g), "s"(lds_base));
 }
 
+// Buffer resource over `bytes` bytes at p (raw, stride 0): loads past the
+// end return zeros instead of faulting.
+__device__ __forceinline__ v4i buf_rsrc(const void* p, uint32_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)p;
+  return v4i{__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+             __builtin_amdgcn_readfirstlane((int)(uint32_t)((a >> 32) & 0xffffu)),
+             __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
+}
+
+// 16 bytes per lane from buffer offset voff + soff straight into LDS at
+// lds_base + 16*lane (buffer_load_dwordx4 ... lds); as dma16_to_lds, the
+// caller orders it with vmcnt waits and barriers.
+__device__ __forceinline__ void bdma16_to_lds(v4i rsrc, uint32_t voff, uint32_t soff, uint32_t lds_base) {
+  uint32_t save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "buffer_load_dwordx4 %1, %2, %4 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "v"(voff), "s"(rsrc), "s"(lds_base), "s"(soff));
+}
+
 // s_waitcnt vmcnt(n) alone (expcnt and lgkmcnt left at their maxima)
 #define MOTY_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
 
 // ---------------------------------------------------------------------------
-// wave64 reductions
+// Cross-lane moves without LDS: DPP within 16-lane rows and the gfx950
+// permlane swaps across rows / halves (VALU latency, where ds_bpermute
+// behind __shfl costs an LDS round trip per step).
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+#define MOTY_DPP_QXOR1 0xB1   // quad_perm [1,0,3,2]: lane ^ 1
+#define MOTY_DPP_QXOR2 0x4E   // quad_perm [2,3,0,1]: lane ^ 2
+#define MOTY_DPP_ROR4 0x124   // row_ror:4: lane i of a row takes lane (i - 4) & 15
+#define MOTY_DPP_ROR8 0x128   // row_ror:8: lane ^ 8 within the row
+#define MOTY_DPP_ROR12 0x12C  // row_ror:12: lane i takes lane (i + 4) & 15
+__device__ __forceinline__ int xor16_i(int v) {  // value of lane ^ 16
+  const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+  return (int)((threadIdx.x & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ int xor32_i(int v) {  // value of lane ^ 32
+  const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+  return (int)((threadIdx.x & 32) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float xor16_f(float v) { return __int_as_float(xor16_i(__float_as_int(v))); }
+__device__ __forceinline__ float xor32_f(float v) { return __int_as_float(xor32_i(__float_as_int(v))); }
+
+// wave64 all-reductions (order-free operations: every lane gets the result)
 __device__ __forceinline__ int wave_sum_i32(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp_i<MOTY_DPP_QXOR1>(v);
+  v += dpp_i<MOTY_DPP_QXOR2>(v);
+  v += dpp_i<MOTY_DPP_ROR4>(v);
+  v += dpp_i<MOTY_DPP_ROR8>(v);
+  v += xor16_i(v);
+  return v + xor32_i(v);
 }
 __device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, dpp_f<MOTY_DPP_QXOR1>(v));
+  v = fmaxf(v, dpp_f<MOTY_DPP_QXOR2>(v));
+  v = fmaxf(v, dpp_f<MOTY_DPP_ROR4>(v));
+  v = fmaxf(v, dpp_f<MOTY_DPP_ROR8>(v));
+  v = fmaxf(v, xor16_f(v));
+  return fmaxf(v, xor32_f(v));
 }
 
 // 4 signed int8 x 4 signed int8 -> int32 accumulate (v_dot4_i32_i8)

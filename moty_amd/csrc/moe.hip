@@ -11,10 +11,11 @@
 //             ascending expert id; engines/olmoe.c:241-242 in top-k order)
 //
 // Pipeline (7 launches, no host synchronisation):
-//   k_router_logits  tiled f32 GEMM (16 tokens x 16 experts per workgroup)
-//                  keeping dot_f32's AVX512 chain order, plus logit bias
-//   k_route_topk   wave per token: int8 row (qrow_i8), softmax, greedy top-k
-//                  as ranks
+//   k_router       router logits on f32 MFMA in dot_f32's AVX512 chain
+//                  order, plus logit bias (token tile x expert slice per
+//                  workgroup)
+//   k_route_topk   wave per token: softmax and greedy top-k; another wave:
+//                  the token's int8 row (qrow_i8)
 //   k_group        one workgroup: per-expert histogram, exclusive scan, slot
 //                  scatter (pairs grouped by expert), M-tile list
 //   k_moe_gateup   grouped GEMM, v_mfma_i32_32x32x32_i8, gate and up rows of
@@ -32,309 +33,338 @@
 namespace moty {
 
 // ---------------------------------------------------------------------------
-// Router logits as a tiled f32 GEMM that keeps dot_f32's AVX512 order
-// (nn/matmul.c:15-27 -> hw/hw_avx512.h:231-243): every (token, expert) dot is
-// 32 FMA chains -- chain c takes elements c, c+32, c+64, ... in order (s0[c]
-// for c < 16, s1[c-16] else) -- then s0+s1 and the reduce_add tree.
-// Thread (pair group g, chain c) accumulates chain c of PT x RG_PE
-// (token, expert) pairs; x and router K-chunks are staged in LDS, so each
-// router row is read once per workgroup's tokens and each x row once per
-// RG_TE experts.  The grid is 1-D and XCD-aware: workgroups are dispatched to
-// the 8 XCDs round-robin by linear id, so ids are decoded such that all the
-// expert tiles of one token tile run on the same XCD and its x rows come
-// from that XCD's L2 after the first read, rather than once per XCD.
-constexpr int RG_NT = 256;                       // 8 pair groups x 32 chains
-constexpr int RG_TE = 16;                        // experts per workgroup
-constexpr int RG_PE = 8;                         // experts per thread
-constexpr int RG_KS = 8;                         // chain steps (of 32 elements) per LDS chunk
-constexpr int RG_KC = RG_KS * 32;                // elements per chunk
-constexpr int RG_LS = RG_KC + 4;                 // padded LDS row (floats)
+// Routing.
+//
+// Router logits keep dot_f32's AVX512 order (nn/matmul.c:15-27 ->
+// hw/hw_avx512.h:231-243): each (token, expert) dot is 32 FMA chains --
+// chain c takes elements c, c+32, c+64, ... in order (s0[c] for c < 16,
+// s1[c-16] else) -- then s0+s1 and gcc's _mm512_reduce_add_ps tree.  The
+// chains run on v_mfma_f32_4x4x1_16b_f32: one instruction is 16 independent
+// 4x4 outer products with k = 1, each output a single fused multiply-add
+// (checked bit for bit against v_fma_f32 on MI355X, denormals and all bit
+// patterns included).  Block b of instruction q carries chain q*16 + b of a
+// 4-token x 4-expert sub-tile: lane l = 4b + i feeds token i's element
+// u*32 + q*16 + b (A) and expert i's (B), and holds the 4 tokens' sums for
+// expert l%4 (output rows in its 4 registers).
+//
+// x and router rows stream through an S-stage LDS ring of 64-element chunks
+// by buffer_load ... lds DMA (1 KiB per instruction = 4 rows x 64 floats);
+// a row's 16-byte column slot c is stored at c ^ ((row & 3) << 1), so the 4
+// rows x 16 chains one read touches fall in distinct banks.  A CU streams
+// (experts + tokens of its tile) x D floats at about 50 B per clock, so
+// tiles are near-square in tokens x experts rather than all experts of a
+// token: the per-token steps run in a second kernel.
+//
+// Per token, one wave: softmax (nn/norm.c:10 -> hw/hw_ops.h:22-26: max
+// order-free, exp, sum serial in expert order, per-element divide) and the
+// greedy top-k of runtime/moecache.c:97-111 as K rounds of a wave argmax
+// under (p desc, index asc) over the experts not yet taken (the reference's
+// first strict '>' over ascending e; values not above -1e30, NaN included,
+// are never taken, and a round without a candidate gives id -1 and weight
+// -1e30 as there); normalisation sum serial over k.  Another wave writes the
+// token's int8 row (qrow_i8, hw/hw_quant.h:9-16).
 
-// PT tokens per thread; workgroup = 4*PT tokens x RG_TE experts.  The next
-// K chunk's global loads are held in registers while the current chunk is
-// consumed from LDS.
-template <int PT>
-__global__ __launch_bounds__(RG_NT) void k_router_logits(const float* __restrict__ x, const float* __restrict__ Wr,
-                                                         const float* __restrict__ bias, int T, int D, int E,
-                                                         float* __restrict__ logits) {
-  constexpr int TT = 4 * PT;
-  constexpr int NX = TT * (RG_KC / 4) / RG_NT;      // float4 per thread per chunk: x
-  constexpr int NW = RG_TE * (RG_KC / 4) / RG_NT;   // and router
-  __shared__ __align__(16) float xs[TT * RG_LS];
-  __shared__ __align__(16) float ws[RG_TE * RG_LS];
-  int tb, eb;
-  {
-    const int nxcd = 8, eblk = (E + RG_TE - 1) / RG_TE;
-    const int xcd = blockIdx.x % nxcd, j = blockIdx.x / nxcd;
-    tb = ((j / eblk) * nxcd + xcd) * TT;
-    eb = (j % eblk) * RG_TE;
-    if (tb >= T) return;  // padding of the token-tile count to a multiple of 8
-  }
-  const int c = threadIdx.x % 32, g = threadIdx.x / 32;
-  const int tq = (g % 4) * PT;        // this thread's tokens tb+tq..
-  const int eq = (g / 4) * RG_PE;     // and experts eb+eq..
-  float acc[PT][RG_PE];
-#pragma unroll
-  for (int i = 0; i < PT; i++)
-#pragma unroll
-    for (int j = 0; j < RG_PE; j++) acc[i][j] = 0.f;
-  const int nsteps = D / 32;  // D % 32 == 0
-  // Two register sets of K-chunk loads, one chunk consumed from LDS while
-  // the next two are in flight.  Loads are unconditional, from clamped
-  // addresses, and zeroed when written to LDS: a branch around a load would
-  // make the compiler wait for every load in flight.  Past the row end the
-  // zeros extend every FMA chain by fma(0, 0, acc) = acc (acc is never -0:
-  // it starts at +0 and an exact zero sum rounds to +0), so full chunks are
-  // always run.
-  struct Set {
-    float4 x[NX], w[NW];
+// qrow_i8 of one row by one wave (hw/hw_quant.h:9-16): amax, scale =
+// max(amax/127, 1e-12), RNE of x/scale, as bytes.
+__device__ __forceinline__ void qrow_row_wave(const float* __restrict__ xr, int D, int8_t* __restrict__ q,
+                                              float* __restrict__ sxo) {
+  const int lane = threadIdx.x % MOTY_WAVE;
+  auto pack = [](float4 v, float inv) {
+    return (uint32_t)(rne_int(v.x * inv) & 0xff) | ((uint32_t)(rne_int(v.y * inv) & 0xff) << 8) |
+           ((uint32_t)(rne_int(v.z * inv) & 0xff) << 16) | ((uint32_t)(rne_int(v.w * inv) & 0xff) << 24);
   };
-  Set s0, s1;
-  auto gload = [&](int st0, Set& sv) {
-    const int k0 = st0 * 32;
+  if (D <= 4096) {
+    // the row held in registers: lane l owns [c*1024 + 16l, +16) of each
+    // 1 KiB chunk c (clamped loads past the end, zeroed)
+    float4 v[4][4];
 #pragma unroll
-    for (int i = 0; i < NX; i++) {
-      const int q = threadIdx.x + i * RG_NT, r = q / (RG_KC / 4), k = (q % (RG_KC / 4)) * 4;
-      const int t = tb + r < T ? tb + r : T - 1;
-      sv.x[i] = *(const float4*)(x + (int64_t)t * D + (k0 + k < D ? k0 + k : 0));
-    }
+    for (int c = 0; c < 4; c++) {
+      const int k = c * 1024 + lane * 16;
 #pragma unroll
-    for (int i = 0; i < NW; i++) {
-      const int q = threadIdx.x + i * RG_NT, r = q / (RG_KC / 4), k = (q % (RG_KC / 4)) * 4;
-      const int e = eb + r < E ? eb + r : E - 1;
-      sv.w[i] = *(const float4*)(Wr + (int64_t)e * D + (k0 + k < D ? k0 + k : 0));
-    }
-    __builtin_amdgcn_sched_barrier(0);
-  };
-  auto chunk = [&](int st0, Set& sv) {
-    const int k0 = st0 * 32;
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < NX; i++) {
-      const int q = threadIdx.x + i * RG_NT, r = q / (RG_KC / 4), k = (q % (RG_KC / 4)) * 4;
-      *(float4*)(xs + r * RG_LS + k) = sel4(k0 + k < D && tb + r < T, sv.x[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < NW; i++) {
-      const int q = threadIdx.x + i * RG_NT, r = q / (RG_KC / 4), k = (q % (RG_KC / 4)) * 4;
-      *(float4*)(ws + r * RG_LS + k) = sel4(k0 + k < D && eb + r < E, sv.w[i]);
-    }
-    __syncthreads();
-    gload(st0 + 2 * RG_KS, sv);
-#pragma unroll
-    for (int u = 0; u < RG_KS; u++) {
-      float xv[PT], wv[RG_PE];
-#pragma unroll
-      for (int i = 0; i < PT; i++) xv[i] = xs[(tq + i) * RG_LS + u * 32 + c];
-#pragma unroll
-      for (int j = 0; j < RG_PE; j++) wv[j] = ws[(eq + j) * RG_LS + u * 32 + c];
-#pragma unroll
-      for (int i = 0; i < PT; i++)
-#pragma unroll
-        for (int j = 0; j < RG_PE; j++) acc[i][j] = __fmaf_rn(xv[i], wv[j], acc[i][j]);
-    }
-  };
-  gload(0, s0);
-  gload(RG_KS, s1);
-  for (int st0 = 0; st0 < nsteps; st0 += 2 * RG_KS) {
-    chunk(st0, s0);
-    chunk(st0 + RG_KS, s1);
-  }
-  // retire the clamped prefetches still in flight before the branchy
-  // epilogue, then load this thread's biases in one batch
-  __builtin_amdgcn_s_waitcnt(0);
-  float bv[RG_PE];
-#pragma unroll
-  for (int j = 0; j < RG_PE; j++) bv[j] = 0.f;
-  if (bias) {
-#pragma unroll
-    for (int j = 0; j < RG_PE; j++) bv[j] = bias[eb + eq + j < E ? eb + eq + j : E - 1];
-  }
-  // s0[c] + s1[c], then the 16-lane reduce_add tree, per pair
-  const int base = (threadIdx.x % MOTY_WAVE) & 32;
-#pragma unroll
-  for (int i = 0; i < PT; i++)
-#pragma unroll
-    for (int j = 0; j < RG_PE; j++) {
-      const float t2 = acc[i][j] + __shfl(acc[i][j], base + ((c + 16) & 31), 64);
-      float r = hsum16_half(t2, base);
-      const int t = tb + tq + i, e = eb + eq + j;
-      if (c == 0 && t < T && e < E) {
-        if (bias) r = r + bv[j];
-        logits[(int64_t)t * E + e] = r;
-      }
-    }
-}
-
-constexpr int TK_NT = 256;  // two waves per token: routing, and the token's int8 row
-constexpr int TK_PV = 4;    // probabilities per lane (E <= 256)
-
-// Per token, two waves: one writes the int8 activation row for the expert
-// GEMMs (qrow_i8, hw/hw_quant.h:9-16); the other runs softmax (nn/norm.c:10 ->
-// hw/hw_ops.h:22-26: max order-free, sum serial in expert order, per-element
-// divide) and greedy top-k (runtime/moecache.c:97-111) as ranks: the rank of
-// expert e under (p desc, index asc); ranks 0..K-1 are the greedy picks of
-// the strict '>' scan, in order.  Normalisation sum serial over k.
-__global__ __launch_bounds__(TK_NT) void k_route_topk(const float* __restrict__ x, const float* __restrict__ logits,
-                                                      int T, int D, int E, int K, int norm, int* __restrict__ idx,
-                                                      float* __restrict__ wout, int8_t* __restrict__ xq,
-                                                      float* __restrict__ sx, float* __restrict__ probs_out) {
-  extern __shared__ float prs[];  // [TK_NT/128][E]
-  __shared__ int sel[TK_NT / 128][64];
-  __shared__ float selw[TK_NT / 128][64];
-  const int lane = threadIdx.x % MOTY_WAVE, wv = (threadIdx.x / MOTY_WAVE) >> 1;
-  const int t = blockIdx.x * (TK_NT / 128) + wv;
-  if (t >= T) return;  // whole wave; no workgroup barrier in this kernel
-  float* p = prs + wv * E;
-  if ((threadIdx.x / MOTY_WAVE) & 1) {  // qrow_i8 of x[t]
-    const float* xr = x + (int64_t)t * D;
-    if (D <= 4096) {
-      // the row held in registers: lane l owns [c*1024 + 16l, +16) of each
-      // 1 KiB chunk c (clamped loads past the end, zeroed)
-      float4 v[4][4];
-#pragma unroll
-      for (int c = 0; c < 4; c++) {
-        const int k = c * 1024 + lane * 16;
-#pragma unroll
-        for (int j = 0; j < 4; j++) v[c][j] = *(const float4*)(xr + (k < D ? k : 0) + 4 * j);
-      }
-      float amax = 0.f;
-#pragma unroll
-      for (int c = 0; c < 4; c++) {
-        const bool ok = c * 1024 + lane * 16 < D;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          v[c][j] = sel4(ok, v[c][j]);
-          amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[c][j].x), fabsf(v[c][j].y)), fmaxf(fabsf(v[c][j].z), fabsf(v[c][j].w))));
-        }
-      }
-      amax = wave_max_f32(amax);
-      float s = amax / 127.f;
-      if (s < 1e-12f) s = 1e-12f;
-      const float inv = 1.f / s;
-      if (lane == 0) sx[t] = s;
-#pragma unroll
-      for (int c = 0; c < 4; c++) {
-        const int k = c * 1024 + lane * 16;
-        if (k >= D) continue;
-        int4 o;
-        int* op = (int*)&o;
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-          op[j] = (int)((uint32_t)(rne_int(v[c][j].x * inv) & 0xff) | ((uint32_t)(rne_int(v[c][j].y * inv) & 0xff) << 8) |
-                        ((uint32_t)(rne_int(v[c][j].z * inv) & 0xff) << 16) |
-                        ((uint32_t)(rne_int(v[c][j].w * inv) & 0xff) << 24));
-        *(int4*)(xq + (int64_t)t * D + k) = o;
-      }
-      return;
+      for (int j = 0; j < 4; j++) v[c][j] = *(const float4*)(xr + (k < D ? k : 0) + 4 * j);
     }
     float amax = 0.f;
-    for (int i = lane * 4; i < D; i += MOTY_WAVE * 4) {
-      const float4 v = *(const float4*)(xr + i);
-      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const bool ok = c * 1024 + lane * 16 < D;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        v[c][j] = sel4(ok, v[c][j]);
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[c][j].x), fabsf(v[c][j].y)), fmaxf(fabsf(v[c][j].z), fabsf(v[c][j].w))));
+      }
     }
     amax = wave_max_f32(amax);
     float s = amax / 127.f;
     if (s < 1e-12f) s = 1e-12f;
     const float inv = 1.f / s;
-    if (lane == 0) sx[t] = s;
-    for (int i = lane * 4; i < D; i += MOTY_WAVE * 4) {
-      const float4 v = *(const float4*)(xr + i);
-      const uint32_t q = (uint32_t)(rne_int(v.x * inv) & 0xff) | ((uint32_t)(rne_int(v.y * inv) & 0xff) << 8) |
-                         ((uint32_t)(rne_int(v.z * inv) & 0xff) << 16) | ((uint32_t)(rne_int(v.w * inv) & 0xff) << 24);
-      *(uint32_t*)(xq + (int64_t)t * D + i) = q;
+    if (lane == 0) *sxo = s;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const int k = c * 1024 + lane * 16;
+      if (k >= D) continue;
+      int4 o;
+#pragma unroll
+      for (int j = 0; j < 4; j++) ((int*)&o)[j] = (int)pack(v[c][j], inv);
+      *(int4*)(q + k) = o;
     }
     return;
   }
-  float pv[TK_PV];
+  float amax = 0.f;
+  for (int i = lane * 4; i < D; i += MOTY_WAVE * 4) {
+    const float4 v = *(const float4*)(xr + i);
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  }
+  amax = wave_max_f32(amax);
+  float s = amax / 127.f;
+  if (s < 1e-12f) s = 1e-12f;
+  const float inv = 1.f / s;
+  if (lane == 0) *sxo = s;
+  for (int i = lane * 4; i < D; i += MOTY_WAVE * 4) *(uint32_t*)(q + i) = pack(*(const float4*)(xr + i), inv);
+}
+
+// Softmax and greedy top-k of one token's logits lg[0..E) (LDS, 16-byte
+// aligned, overwritten with the exponentials) by one wave; writes
+// idx/w[0..K) and, if probs is non-null, probs[0..E).
+__device__ __forceinline__ void route_token_wave(float* lg, int E, int K, int norm, int* __restrict__ idx,
+                                                 float* __restrict__ wout, float* __restrict__ probs) {
+  constexpr int PV = 4;  // E <= 256
+  const int lane = threadIdx.x % MOTY_WAVE;
+  float pv[PV];
 #pragma unroll
-  for (int j = 0; j < TK_PV; j++) pv[j] = (lane + 64 * j < E) ? logits[(int64_t)t * E + lane + 64 * j] : -1e30f;
+  for (int j = 0; j < PV; j++) pv[j] = (lane + 64 * j < E) ? lg[lane + 64 * j] : -1e30f;
   float m = -1e30f;
 #pragma unroll
-  for (int j = 0; j < TK_PV; j++) m = pv[j] > m ? pv[j] : m;
+  for (int j = 0; j < PV; j++) m = pv[j] > m ? pv[j] : m;
   m = wave_max_f32(m);
 #pragma unroll
-  for (int j = 0; j < TK_PV; j++)
-    if (lane + 64 * j < E) p[lane + 64 * j] = ref_expf(pv[j] - m);
+  for (int j = 0; j < PV; j++) {
+    pv[j] = ref_expf(pv[j] - m);
+    if (lane + 64 * j < E) lg[lane + 64 * j] = pv[j];
+  }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   float ssum = 0.f;  // serial in expert order (every lane runs it; reads batched)
   {
     int e = 0;
-    for (; e + 16 <= E; e += 16) {
-      float v[16];
+    for (; e + 32 <= E; e += 32) {
+      float4 v[8];
 #pragma unroll
-      for (int u = 0; u < 16; u++) v[u] = p[e + u];
+      for (int u = 0; u < 8; u++) v[u] = *(const float4*)(lg + e + 4 * u);
 #pragma unroll
-      for (int u = 0; u < 16; u++) ssum += v[u];
+      for (int u = 0; u < 8; u++) ssum = (((ssum + v[u].x) + v[u].y) + v[u].z) + v[u].w;
     }
-    for (; e < E; e++) ssum += p[e];
+    for (; e < E; e++) ssum += lg[e];
   }
+  // candidates: this lane's probabilities, -inf where not one (past E, or
+  // not above -1e30 as the reference's scan requires, NaN included)
 #pragma unroll
-  for (int j = 0; j < TK_PV; j++) pv[j] = (lane + 64 * j < E) ? p[lane + 64 * j] / ssum : 0.f;
-  if (probs_out)
+  for (int j = 0; j < PV; j++) {
+    const bool in = lane + 64 * j < E;
+    const float p = in ? pv[j] / ssum : 0.f;
+    if (probs && in) probs[lane + 64 * j] = p;
+    pv[j] = (in && p > -1e30f) ? p : -__builtin_inff();
+  }
+  // K rounds: the wave maximum, then the lowest expert id holding it (first
+  // candidate set with a lane at the maximum, its lowest lane), taken out
+  int my_e = -1;
+  float my_w = -1e30f, ws = 0.f;
+  for (int kk = 0; kk < K; kk++) {
+    float lm = pv[0];
 #pragma unroll
-    for (int j = 0; j < TK_PV; j++)
-      if (lane + 64 * j < E) probs_out[(int64_t)t * E + lane + 64 * j] = pv[j];
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int j = 1; j < PV; j++) lm = fmaxf(lm, pv[j]);
+    const float bv = wave_max_f32(lm);
+    int be = -1;
 #pragma unroll
-  for (int j = 0; j < TK_PV; j++)
-    if (lane + 64 * j < E) p[lane + 64 * j] = pv[j];
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  // branch-free compares: rank += (u > v) | (u == v & j < e)
-  const int npv = (E + 63) / 64;
-  int rank[TK_PV];
+    for (int j = PV - 1; j >= 0; j--) {
+      const uint64_t hit = __ballot(pv[j] == bv);
+      if (hit) be = 64 * j + (int)__builtin_ctzll(hit);
+    }
+    const bool none = !(bv > -__builtin_inff());
+    const float wk = none ? -1e30f : bv;
+    be = none ? -1 : be;
 #pragma unroll
-  for (int j = 0; j < TK_PV; j++) rank[j] = 0;
+    for (int j = 0; j < PV; j++) pv[j] = (be == lane + 64 * j) ? -__builtin_inff() : pv[j];
+    my_e = lane == kk ? be : my_e;
+    my_w = lane == kk ? wk : my_w;
+    ws += wk;  // the normalisation sum, serial over k
+  }
+  if (lane < K) {
+    idx[lane] = my_e;
+    wout[lane] = (norm && ws > 0) ? my_w / ws : my_w;
+  }
+}
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// Router logits, one workgroup per (token tile, expert slice): WT x WE waves,
+// each TWW tokens x EWW experts; the tile is TW = WT*TWW tokens by EG =
+// WE*EWW experts.  S ring stages of KS 32-element steps; every wave issues
+// NJ DMA instructions per stage.  Workgroup ids are decoded so that all the
+// slices of a token tile run on one XCD (workgroups go to the 8 XCDs
+// round-robin by linear id): its x rows come from that XCD's L2 after the
+// first read.
+template <int TWW, int EWW, int WT, int WE, int S, int KS, int NJ>
+__global__ __launch_bounds__(WT * WE * 64) void k_router(const float* __restrict__ x, const float* __restrict__ Wr,
+                                                         const float* __restrict__ bias, int T, int D, int E,
+                                                         float* __restrict__ logits) {
+  constexpr int TW = WT * TWW, EG = WE * EWW, NW = WT * WE, ROWS = EG + TW;
+  constexpr int RT = TWW / 4, CT = EWW / 4;  // 4 x 4 sub-tiles per wave
+  constexpr int KC = KS * 32;                // chunk elements per row
+  constexpr int ROWB = KC * 4;               // bytes per staged row
+  constexpr int RPI = 1024 / ROWB;           // rows per 1 KiB DMA instruction
+  constexpr int NSL = KC / 4;                // 16-byte slots per row
+  constexpr int J = ROWS / RPI;              // DMA instructions per stage
+  constexpr int STAGE = ROWS * ROWB + 1024;  // the rows, then 1 KiB for idle DMA slots
+  static_assert(RPI >= 1 && 4 % RPI == 0 && ROWS % 4 == 0 && J <= NJ * NW, "stage layout");
+  __shared__ __align__(1024) uint8_t lds[S * STAGE];
+  int tb, eb;
   {
-    int e = 0;
-    for (; e + 16 <= E; e += 16) {
-      float v[16];
+    const int nsl = (E + EG - 1) / EG;
+    const int xcd = blockIdx.x % 8, j = blockIdx.x / 8;
+    tb = ((j / nsl) * 8 + xcd) * TW;
+    eb = (j % nsl) * EG;
+    if (tb >= T) return;  // padding of the tile count to a multiple of 8
+  }
+  const int lane = threadIdx.x % MOTY_WAVE;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / MOTY_WAVE);
+  const int wi = wv / WE, wj = wv % WE;
+  const v4i rW = buf_rsrc(Wr, (uint32_t)E * (uint32_t)D * 4u);
+  const v4i rX = buf_rsrc(x, (uint32_t)T * (uint32_t)D * 4u);
+  // stage rows: EG router rows (clamped past E), then TW x rows (clamped
+  // past T).  This wave's DMA slots: instruction j*NW + wv of each stage;
+  // slots past J load from past the buffer end (no memory traffic) into the
+  // stage's spare KiB.
+  uint32_t vo[NJ], ldo[NJ];
+  bool isx[NJ];
 #pragma unroll
-      for (int u = 0; u < 16; u++) v[u] = p[e + u];
+  for (int j = 0; j < NJ; j++) {
+    const int jb = j * NW + wv;
+    const int row = jb * RPI + lane / NSL;
+    const int c = (lane % NSL) ^ ((row & 3) << 1);
+    isx[j] = jb * RPI >= EG;  // whole instructions: EG is a multiple of 4
+    const int r = isx[j] ? (tb + row - EG < T ? tb + row - EG : T - 1) : (eb + row < E ? eb + row : E - 1);
+    vo[j] = jb < J ? (uint32_t)r * (uint32_t)D * 4u + (uint32_t)c * 16u : 0x80000000u;
+    ldo[j] = jb < J ? (uint32_t)jb * 1024u : (uint32_t)(STAGE - 1024);
+  }
+  const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
+  auto issue = [&](int kb) {
+    const uint32_t st0 = lds0 + (uint32_t)(kb % S) * (uint32_t)STAGE;
 #pragma unroll
-      for (int j = 0; j < TK_PV; j++) {
-        if (j >= npv) break;  // wave-uniform
-        const int me = lane + 64 * j;
+    for (int j = 0; j < NJ; j++) bdma16_to_lds(isx[j] ? rX : rW, vo[j], (uint32_t)kb * (uint32_t)ROWB, st0 + ldo[j]);
+  };
+  v4f acc[RT][CT][2];
 #pragma unroll
-        for (int u = 0; u < 16; u++)
-          rank[j] += (int)(v[u] > pv[j]) | ((int)(v[u] == pv[j]) & (int)(e + u < me));
+  for (int r = 0; r < RT; r++)
+#pragma unroll
+    for (int c = 0; c < CT; c++) acc[r][c][0] = acc[r][c][1] = v4f{0.f, 0.f, 0.f, 0.f};
+  const int b = lane >> 2, i4 = lane & 3;
+  // LDS float offset of this lane's operand in a stage, chain q*16 + b of
+  // step u: row*KC + ((col/4) ^ ((row&3)<<1))*4 + col%4, with row&3 == i4
+  auto off = [&](int row, int u, int q) {
+    const int col = u * 32 + q * 16 + b;
+    return row * KC + (((col >> 2) ^ (i4 << 1)) << 2) + (col & 3);
+  };
+  // a chunk's operands in registers: read while the previous chunk's
+  // MFMAs run
+  struct Frags {
+    float a[KS][2][RT], w[KS][2][CT];
+  };
+  auto read = [&](int kb, Frags& f) {
+    const float* st = (const float*)(lds + (kb % S) * STAGE);
+#pragma unroll
+    for (int u = 0; u < KS; u++)
+#pragma unroll
+      for (int q = 0; q < 2; q++) {
+#pragma unroll
+        for (int r = 0; r < RT; r++) f.a[u][q][r] = st[off(EG + wi * TWW + r * 4 + i4, u, q)];
+#pragma unroll
+        for (int c = 0; c < CT; c++) f.w[u][q][c] = st[off(wj * EWW + c * 4 + i4, u, q)];
       }
-    }
-    for (; e < E; e++) {
-      const float u = p[e];
+  };
+  const int nsteps = D / 32, nk = (nsteps + KS - 1) / KS;
+  auto compute = [&](int kb, const Frags& f) {
 #pragma unroll
-      for (int j = 0; j < TK_PV; j++)
-        rank[j] += (int)(u > pv[j]) | ((int)(u == pv[j]) & (int)(e < lane + 64 * j));
-    }
-  }
+    for (int u = 0; u < KS; u++) {
+      if (kb * KS + u >= nsteps) break;  // the last chunk's row end (wave-uniform)
 #pragma unroll
-  for (int j = 0; j < TK_PV; j++) {
-    const int e = lane + 64 * j;
-    if (e < E && rank[j] < K) {
-      sel[wv][rank[j]] = e;
-      selw[wv][rank[j]] = pv[j];
+      for (int q = 0; q < 2; q++)
+#pragma unroll
+        for (int r = 0; r < RT; r++)
+#pragma unroll
+          for (int c = 0; c < CT; c++)
+            acc[r][c][q] = __builtin_amdgcn_mfma_f32_4x4x1f32(f.a[u][q][r], f.w[u][q][c], acc[r][c][q], 0, 0, 0);
     }
+  };
+  // every stage of the ring in flight, then chunk 0's operands to registers
+#pragma unroll
+  for (int s = 0; s < S; s++) issue(s);
+  MOTY_WAIT_VMCNT((S - 1) * NJ);
+  __syncthreads();
+  Frags f0, f1;
+  read(0, f0);
+  for (int kb = 0; kb < nk; kb += 2) {
+    // chunk kb + 1 has landed (S - 2 later ones may still fly); the barrier
+    // also retires every wave's reads of chunk kb's stage, which the next
+    // DMA overwrites.  Chunks past the end are loaded and never used.
+    MOTY_WAIT_VMCNT((S - 2) * NJ);
+    __syncthreads();
+    issue(kb + S);
+    read(kb + 1, f1);
+    compute(kb, f0);
+    if (kb + 1 >= nk) break;
+    MOTY_WAIT_VMCNT((S - 2) * NJ);
+    __syncthreads();
+    issue(kb + 1 + S);
+    read(kb + 2, f0);
+    compute(kb + 1, f1);
   }
+  __builtin_amdgcn_s_waitcnt(0);
+  // s0[c] + s1[c] (same lane), then the reduce tree over the 16 blocks
+  // (block k in lanes 4k..4k+3): t[k+8] + t[k] (lane ^ 32), a[k+4] + a[k]
+  // (lane ^ 16), then (b0 + b2) + (b1 + b3) from lanes j, j+8, j+4, j+12
+#pragma unroll
+  for (int c = 0; c < CT; c++) {
+    const int e = eb + wj * EWW + c * 4 + i4;
+    const float bv = (bias && e < E) ? bias[e] : 0.f;
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float t = acc[r][c][0][i] + acc[r][c][1][i];
+        const float a8 = xor32_f(t) + t;
+        const float b4 = xor16_f(a8) + a8;
+        const float s2 = dpp_f<MOTY_DPP_ROR8>(b4) + b4;  // lane j: b2 + b0, lane j+4: b3 + b1
+        float v = dpp_f<MOTY_DPP_ROR12>(s2) + s2;        // lane j: (b1 + b3) + (b0 + b2)
+        if (bias) v = v + bv;
+        const int tk = tb + wi * TWW + r * 4 + i;
+        if (lane < 4 && e < E && tk < T) logits[(int64_t)tk * E + e] = v;
+      }
+  }
+}
+
+// Per token, two waves: one routes (softmax, greedy top-k), the other writes
+// the token's int8 row; TK_TOK tokens per workgroup.
+constexpr int TK_TOK = 4;
+__global__ __launch_bounds__(TK_TOK * 128) void k_route_topk(const float* __restrict__ x,
+                                                            const float* __restrict__ logits, int T, int D, int E,
+                                                            int K, int norm, int* __restrict__ idx,
+                                                            float* __restrict__ wout, int8_t* __restrict__ xq,
+                                                            float* __restrict__ sx, float* __restrict__ probs_out) {
+  __shared__ float lg[TK_TOK][256];
+  const int lane = threadIdx.x % MOTY_WAVE, wv = threadIdx.x / MOTY_WAVE;
+  const int tl = wv % TK_TOK, t = blockIdx.x * TK_TOK + tl;
+  if (t >= T) return;  // whole waves; no workgroup barrier in this kernel
+  if (wv >= TK_TOK) {
+    qrow_row_wave(x + (int64_t)t * D, D, xq + (int64_t)t * D, sx + t);
+    return;
+  }
+  for (int e = lane; e < E; e += MOTY_WAVE) lg[tl][e] = logits[(int64_t)t * E + e];
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if (lane == 0) {
-    float ws = 0.f;
-    if (norm)
-      for (int kk = 0; kk < K; kk++) ws += selw[wv][kk];
-    for (int kk = 0; kk < K; kk++) {
-      float v = selw[wv][kk];
-      if (norm && ws > 0) v = v / ws;
-      idx[(int64_t)t * K + kk] = sel[wv][kk];
-      wout[(int64_t)t * K + kk] = v;
-    }
-  }
+  route_token_wave(lg[tl], E, K, norm, idx + (int64_t)t * K, wout + (int64_t)t * K,
+                   probs_out ? probs_out + (int64_t)t * E : nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -700,23 +730,30 @@ void moe_routing(const MoeArgs& a, void* scratch, const int** idx, const int** c
 
 int launch_moe_route(const MoeArgs& a, void* scratch, hipStream_t st) {
   const int T = a.T, D = a.D, E = a.E, K = a.K, I = a.I;
-  if (K < 1 || K > 64 || K > E || E > 64 * TK_PV || (D % 32) || (I % 32) || (D % 4)) return MOTY_EUNSUP;
+  if (K < 1 || K > 64 || K > E || E > 256 || (D % 32) || (I % 32) || (D % 4)) return MOTY_EUNSUP;
   const MoeBufs m = moe_bufs(a, scratch);
   const int P = T * K;
-  // 4-token tiles while that leaves at most ~2 workgroups per CU (the
-  // router is latency-bound at small T), 16-token tiles beyond (fewer router
-  // re-reads); measured on MI355X: T=256, E=64: 8.0 us vs 10.5 (8-token);
-  // T=1072, E=128: 28.7 us vs 34.7 (4-token)
-  const int eblk = (E + RG_TE - 1) / RG_TE;
-  auto rgrid = [&](int tt) { return dim3((unsigned)(((T + tt - 1) / tt + 7) / 8 * 8 * eblk)); };
-  if ((int64_t)((T + 3) / 4) * eblk <= 512)
-    hipLaunchKernelGGL(k_router_logits<1>, rgrid(4), dim3(RG_NT), 0, st, a.x, a.Wr, a.bias, T, D, E, m.logits);
-  else
-    hipLaunchKernelGGL(k_router_logits<4>, rgrid(16), dim3(RG_NT), 0, st, a.x, a.Wr, a.bias, T, D, E, m.logits);
-  LAUNCH_TRY("k_router_logits");
-  hipLaunchKernelGGL(k_route_topk, dim3((T + TK_NT / 128 - 1) / (TK_NT / 128)), dim3(TK_NT),
-                     (size_t)(TK_NT / 128) * E * 4, st, a.x, m.logits, T, D, E, K, a.norm, m.idx, m.w, m.xq, m.sx,
-                     a.probs_out);
+  // router tiles: 8 tokens x 8 experts of 4 waves for small layers (one
+  // workgroup per CU at T = 256, E = 64), 24 tokens x 32 experts of 12 waves
+  // otherwise; token slices keep every buffer offset below 2^31 bytes
+  const bool small = E <= 64 && T <= 1024;
+  const int tw = small ? 8 : 24, eg = small ? 8 : 32, nsl = (E + eg - 1) / eg;
+  const int tmax = (int)(((int64_t)1 << 31) / ((int64_t)D * 4)) / tw * tw;
+  if (tmax < tw) return MOTY_EUNSUP;
+  for (int t0 = 0; t0 < T; t0 += tmax) {
+    const int ts = T - t0 < tmax ? T - t0 : tmax;
+    const float* x = a.x + (int64_t)t0 * D;
+    const dim3 grid((unsigned)((((ts + tw - 1) / tw + 7) / 8) * 8 * nsl));
+    if (small)
+      hipLaunchKernelGGL((k_router<4, 4, 2, 2, 8, 8, 4>), grid, dim3(256), 0, st, x, a.Wr, a.bias, ts, D, E,
+                         m.logits + (int64_t)t0 * E);
+    else
+      hipLaunchKernelGGL((k_router<8, 8, 3, 4, 4, 4, 3>), grid, dim3(768), 0, st, x, a.Wr, a.bias, ts, D, E,
+                         m.logits + (int64_t)t0 * E);
+    LAUNCH_TRY("k_router");
+  }
+  hipLaunchKernelGGL(k_route_topk, dim3((T + TK_TOK - 1) / TK_TOK), dim3(TK_TOK * 128), 0, st, a.x, m.logits, T, D, E,
+                     K, a.norm, m.idx, m.w, m.xq, m.sx, a.probs_out);
   LAUNCH_TRY("k_route_topk");
   const int mt = moe_mt(a);
   hipLaunchKernelGGL(k_group, dim3(1), dim3(GR_NT), (size_t)(3 * E + 1) * 4, st, m.idx, P, K, E, 64 * mt, m.offs,

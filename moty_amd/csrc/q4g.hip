@@ -432,29 +432,6 @@ __device__ __forceinline__ v8h nib8_to_h(uint32_t w, uint32_t m, uint32_t o) {
   return v8h{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
 }
 
-// Buffer resource over `bytes` bytes at p (raw, stride 0): loads past the
-// end return zeros instead of faulting.
-__device__ __forceinline__ v4i buf_rsrc(const void* p, uint32_t bytes) {
-  const uint64_t a = (uint64_t)(uintptr_t)p;
-  return v4i{__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
-             __builtin_amdgcn_readfirstlane((int)(uint32_t)((a >> 32) & 0xffffu)),
-             __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
-}
-
-// 16 bytes per lane from buffer offset voff + soff straight into LDS at
-// lds_base + 16*lane (buffer_load_dwordx4 ... lds); as dma16_to_lds, the
-// caller orders it with vmcnt waits and barriers.
-__device__ __forceinline__ void bdma16_to_lds(v4i rsrc, uint32_t voff, uint32_t soff, uint32_t lds_base) {
-  uint32_t save;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %3\n\t"
-      "buffer_load_dwordx4 %1, %2, %4 offen lds\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(save)
-      : "v"(voff), "s"(rsrc), "s"(lds_base), "s"(soff));
-}
-
 // PAIR: gate and up rows of the same block tile in one pass (the activation
 // fragments serve both), epilogue y = silu(sx*gate) * (sx*up) -- the
 // gate_up + silu_rows of nn/ffn.c:28-37.

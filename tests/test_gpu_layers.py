@@ -123,6 +123,25 @@ def test_moe_routing_ties(ops, order):
     assert same_bits(to_np(y), y2)
 
 
+@pytest.mark.parametrize("E,K,D,S", [(40, 6, 96, 9), (100, 8, 160, 33), (200, 8, 96, 17), (256, 16, 4160, 5),
+                                     (72, 64, 128, 3), (129, 8, 64, 1)])
+def test_moe_routing_expert_counts(ops, E, K, D, S):
+    # expert counts off the routing kernel's wave tiling (8 / 16 experts per
+    # wave), the 256-expert configuration, rows past the register-held
+    # int8-row path (D > 4096) and K = 64
+    say("moe routing", E, K, D, S)
+    Wr = randn(11, (E, D), 0.02)
+    x = randn(12, (S, D))
+    ex = moe_weights(E, 32, D, seed=13)
+    from moty_amd import ORDER_EXPERT
+    L = layer(ops, Wr, ex, K, 1, ORDER_EXPERT)
+    y, idx, w, cnt = L(to_dev(x), want_routing=True)
+    y2, idx2, w2 = o_moe(x, Wr, ex, K, "batch", norm=1)
+    assert (to_np(idx) == idx2).all()
+    assert same_bits(to_np(w), w2)
+    assert same_bits(to_np(y), y2), mismatch(to_np(y), y2)
+
+
 @pytest.mark.parametrize("S", [40, 400])
 def test_moe_skewed_bias(ops, S):
     # +2.0 on 8 hot experts' logits (the skewed continuous-batch variant);
