@@ -167,6 +167,19 @@ __device__ __forceinline__ int wave_sum_i32(int v) {
   v += xor16_i(v);
   return v + xor32_i(v);
 }
+// inclusive prefix sum over the wave's lanes: row_shr steps within each
+// 16-lane row (lanes shifted in from before the row read 0), then the
+// totals of the rows below
+__device__ __forceinline__ int wave_incl_scan_i32(int v) {
+  v += dpp_i<0x111>(v);  // row_shr:1
+  v += dpp_i<0x112>(v);  // row_shr:2
+  v += dpp_i<0x114>(v);  // row_shr:4
+  v += dpp_i<0x118>(v);  // row_shr:8
+  const int r0 = __builtin_amdgcn_readlane(v, 15), r1 = __builtin_amdgcn_readlane(v, 31);
+  const int r2 = __builtin_amdgcn_readlane(v, 47);
+  const int row = (threadIdx.x % 64) >> 4;
+  return v + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
+}
 __device__ __forceinline__ float wave_max_f32(float v) {
   v = fmaxf(v, dpp_f<MOTY_DPP_QXOR1>(v));
   v = fmaxf(v, dpp_f<MOTY_DPP_QXOR2>(v));

@@ -369,29 +369,38 @@ __global__ __launch_bounds__(TK_TOK * 128) void k_route_topk(const float* __rest
 
 // ---------------------------------------------------------------------------
 constexpr int GR_NT = 1024;
+constexpr int GR_PT = 16;  // pair ids held in registers per thread (P <= 16384)
 
 // Single workgroup.  offs[E+1]: expert segment starts; slot_tok[P]: token of
 // each slot; pair_slot[P]: slot of pair (t,k); tiles[]: (expert, m0) M-tiles
-// of bm slots; ntiles[0]: their count.
+// of bm slots; ntiles[0]: their count.  Expert ids are read once into
+// registers (the rest of a larger P is read again for the scatter).
 __global__ __launch_bounds__(GR_NT) void k_group(const int* __restrict__ idx, int P, int K, int E, int bm,
                                                  int* __restrict__ offs, int* __restrict__ slot_tok,
                                                  int* __restrict__ pair_slot, int2* __restrict__ tiles,
                                                  int* __restrict__ ntiles, int* __restrict__ counts_out) {
-  extern __shared__ int gs[];
-  int* cnt = gs;          // [E]
-  int* cur = gs + E;      // [E]
-  int* tstart = gs + 2 * E;  // [E+1]
-  for (int e = threadIdx.x; e < E; e += GR_NT) cnt[e] = 0;
+  __shared__ int cnt[256], cur[256], tstart[257];
+  const int tid = threadIdx.x;
+  int ev[GR_PT];
+#pragma unroll
+  for (int i = 0; i < GR_PT; i++) {
+    const int p = tid + i * GR_NT;
+    ev[i] = p < P ? idx[p] : -1;
+  }
+  if (tid < E) cnt[tid] = 0;
   __syncthreads();
-  for (int p = threadIdx.x; p < P; p += GR_NT) {
+#pragma unroll
+  for (int i = 0; i < GR_PT; i++)
+    if (ev[i] >= 0 && ev[i] < E) atomicAdd(&cnt[ev[i]], 1);
+  for (int p = tid + GR_PT * GR_NT; p < P; p += GR_NT) {
     const int e = idx[p];
     if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
   }
   __syncthreads();
-  if (threadIdx.x < MOTY_WAVE) {
+  if (tid < MOTY_WAVE) {
     // exclusive scans of the counts and of the M-tile counts by one wave:
     // lane l owns experts 4l..4l+3 (E <= 256)
-    const int l = threadIdx.x;
+    const int l = tid;
     int c[4], t[4], so = 0, st = 0;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -401,16 +410,7 @@ __global__ __launch_bounds__(GR_NT) void k_group(const int* __restrict__ idx, in
       so += c[j];
       st += t[j];
     }
-    int io = so, it = st;  // inclusive scans over lanes
-#pragma unroll
-    for (int d = 1; d < MOTY_WAVE; d <<= 1) {
-      const int po = __shfl_up(io, d, MOTY_WAVE), pt = __shfl_up(it, d, MOTY_WAVE);
-      if (l >= d) {
-        io += po;
-        it += pt;
-      }
-    }
-    int o = io - so, tl = it - st;
+    int o = wave_incl_scan_i32(so) - so, tl = wave_incl_scan_i32(st) - st;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       const int e = 4 * l + j;
@@ -418,6 +418,7 @@ __global__ __launch_bounds__(GR_NT) void k_group(const int* __restrict__ idx, in
         cur[e] = o;
         offs[e] = o;
         tstart[e] = tl;
+        if (counts_out) counts_out[e] = c[j];
       }
       o += c[j];
       tl += t[j];
@@ -429,18 +430,23 @@ __global__ __launch_bounds__(GR_NT) void k_group(const int* __restrict__ idx, in
     }
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += GR_NT) {
-    if (counts_out) counts_out[e] = cnt[e];
-    const int nt = tstart[e + 1] - tstart[e];
-    for (int j = 0; j < nt; j++) tiles[tstart[e] + j] = int2{e, j * bm};
+  if (tid < E) {
+    const int nt = tstart[tid + 1] - tstart[tid];
+    for (int j = 0; j < nt; j++) tiles[tstart[tid] + j] = int2{tid, j * bm};
   }
-  for (int p = threadIdx.x; p < P; p += GR_NT) {
-    const int e = idx[p];
-    if (e < 0 || e >= E) { pair_slot[p] = -1; continue; }
+  auto place = [&](int p, int e) {
+    if (e < 0 || e >= E) {
+      pair_slot[p] = -1;
+      return;
+    }
     const int s = atomicAdd(&cur[e], 1);
     slot_tok[s] = p / K;
     pair_slot[p] = s;
-  }
+  };
+#pragma unroll
+  for (int i = 0; i < GR_PT; i++)
+    if (tid + i * GR_NT < P) place(tid + i * GR_NT, ev[i]);
+  for (int p = tid + GR_PT * GR_NT; p < P; p += GR_NT) place(p, idx[p]);
 }
 
 // ---------------------------------------------------------------------------
@@ -756,7 +762,7 @@ int launch_moe_route(const MoeArgs& a, void* scratch, hipStream_t st) {
                      K, a.norm, m.idx, m.w, m.xq, m.sx, a.probs_out);
   LAUNCH_TRY("k_route_topk");
   const int mt = moe_mt(a);
-  hipLaunchKernelGGL(k_group, dim3(1), dim3(GR_NT), (size_t)(3 * E + 1) * 4, st, m.idx, P, K, E, 64 * mt, m.offs,
+  hipLaunchKernelGGL(k_group, dim3(1), dim3(GR_NT), 0, st, m.idx, P, K, E, 64 * mt, m.offs,
                      m.slot_tok, m.pair_slot, m.tiles, m.ntiles, m.counts);
   LAUNCH_TRY("k_group");
   return MOTY_OK;
