@@ -40,7 +40,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=6.0, help="bound on each CPU baseline sample")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only launch the dominant kernel on distinct weights and a 64 MiB copy (for rocprofv3 --pmc)")
-    ap.add_argument("--only", choices=["c2", "c3", "c3r4", "c4", "c5", "q8gemv"],
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c3r4", "c4", "c5", "q8gemv"],
                     help="run one config alone and print its JSON object (for rocprofv3 runs of a single config)")
     return ap.parse_args()
 
@@ -173,7 +173,7 @@ def moe_weights(c, cfg, E, I, D):
     return G, GS, U, US, Dn, DS
 
 
-def bench_moe(c, cfg, T, E, K, I, D, norm, order, steps, warmup, bias=None, label=""):
+def bench_moe(c, cfg, T, E, K, I, D, norm, order, steps, warmup, bias=None, label="", traffic_key=None):
     torch, ops = c.torch, c.ops
     from moty_amd.ops import MoeLayer
     ebytes = 3 * E * I * D + E * (2 * I + D) * 4
@@ -194,7 +194,8 @@ def bench_moe(c, cfg, T, E, K, I, D, norm, order, steps, warmup, bias=None, labe
     return {
         "workload": label, "tokens_per_s": T / t, "ms_per_layer": t * 1e3, "steps": n, "weight_copies": ncopy,
         "active_experts": active, "load_max": int(cnt.max()), "load_mean": round(float(cnt.float().mean()), 2),
-        "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s"),
+        "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s",
+                             pmc_traffic("hbm_traffic_pmc", traffic_key) if traffic_key else None),
         "int_tops": round(ops_int / t / 1e12, 2),
         "x": x, "Wr": Wr, "layer0": layers[0],
     }
@@ -314,7 +315,8 @@ def bench_c2(c, steps, warmup):
     return {"workload": "C2 Qwen3-0.6B layer, 7 Q8 projections as prefill GEMMs, M=512 "
                         "(q/k/v/gate/up fused by rows: one GEMM N=10240, K=1024; o; down)",
             "ms_per_step": t * 1e3, "steps": n,
-            "roofline": roofline("mfma", ops_int / t / 1e12, INT8_PEAK_TOPS, "TOP/s"),
+            "roofline": roofline("mfma", ops_int / t / 1e12, INT8_PEAK_TOPS, "TOP/s",
+                                 pmc_traffic("hbm_traffic_pmc", "c2_step")),
             "hbm_gbs": round(algo / t / 1e9, 1),
             "gemms_only": {"ms_per_step": tg * 1e3, "tops": round(ops_int / tg / 1e12, 1)},
             "library_int_mm": lib_ref,
@@ -342,9 +344,10 @@ def bench_c3(c, steps, warmup):
         t, n = c.time_steps([step(w) for w in copies], max(8, steps // (8 if M == 1 else 64)), 8)
         ops_int = 2 * M * 3 * I * D
         algo = wbytes + M * (D + I + I + D) * 4
+        tr = pmc_traffic("hbm_traffic_pmc", "c3_M%d_step" % M)
         res["M%d" % M] = {"ms_per_step": t * 1e3, "steps": n,
-                          "hbm": roofline("hbm", algo / t / 1e9, HBM_PEAK_GBS, "GB/s"),
-                          "mfma": roofline("mfma", ops_int / t / 1e12, INT8_PEAK_TOPS, "TOP/s")}
+                          "hbm": roofline("hbm", algo / t / 1e9, HBM_PEAK_GBS, "GB/s", tr),
+                          "mfma": roofline("mfma", ops_int / t / 1e12, INT8_PEAK_TOPS, "TOP/s", tr)}
     return {"workload": "C3 8B-dense FFN, grouped int4 g32 (IDOT4=1), D=4096, I=12288, M=1 and M=256", **res}
 
 
@@ -406,9 +409,10 @@ def bench_c3_r4(c, steps, warmup):
                             max(8, steps // (8 if M == 1 else 64)), 8)
         ops_int = 2 * M * 3 * I * D
         algo = wbytes + M * (D + D) * 4
+        tr = pmc_traffic("hbm_traffic_pmc", "c3r4_M%d_step" % M)
         res["M%d" % M] = {"ms_per_step": t * 1e3, "steps": n,
-                          "hbm": roofline("hbm", algo / t / 1e9, HBM_PEAK_GBS, "GB/s"),
-                          "mfma": roofline("mfma", ops_int / t / 1e12, INT8_PEAK_TOPS, "TOP/s")}
+                          "hbm": roofline("hbm", algo / t / 1e9, HBM_PEAK_GBS, "GB/s", tr),
+                          "mfma": roofline("mfma", ops_int / t / 1e12, INT8_PEAK_TOPS, "TOP/s", tr)}
     return {"workload": "C3 shapes in Q4R4 (f16 group-32 scales, 4-row blocks, gate/up row-fused), D=4096, "
                         "I=12288, M=1 and M=256", **res}
 
@@ -762,14 +766,16 @@ def main():
         pmc_probe(c)
         return
     if args.only:
-        one = {"c2": lambda: bench_c2(c, args.steps, args.warmup),
+        one = {"c1": lambda: bench_c1(c, args.steps, args.warmup),
+               "c2": lambda: bench_c2(c, args.steps, args.warmup),
                "c3": lambda: bench_c3(c, args.steps, args.warmup),
                "c3r4": lambda: bench_c3_r4(c, args.steps, args.warmup),
                "q8gemv": lambda: bench_q8_gemv_sizes(c, args.steps, args.warmup),
                "c4": lambda: bench_moe(c, 3, 256, 64, 8, 1024, 2048, 0, moty_amd.ORDER_TOPK, args.steps,
-                                       args.warmup, label="C4 OLMoE MoE layer Q8, T=256"),
+                                       args.warmup, label="C4 OLMoE MoE layer Q8, T=256", traffic_key="c4_layer"),
                "c5": lambda: bench_moe(c, 4, 1072, 128, 8, 768, 2048, 1, moty_amd.ORDER_EXPERT, args.steps,
-                                       args.warmup, label="C5 Qwen3-30B-A3B MoE layer Q8, T=1072, uniform")}[args.only]()
+                                       args.warmup, label="C5 Qwen3-30B-A3B MoE layer Q8, T=1072, uniform",
+                                       traffic_key="c5_layer")}[args.only]()
         print(json.dumps({k2: v for k2, v in one.items() if k2 not in HIDDEN}), flush=True)
         return
 
@@ -779,7 +785,8 @@ def main():
         c1["gbs"], c1["ms_per_step"] * 1e3, c1["kernel"]["us"], c1["kernel"]["gbs"]))
     log("C4 OLMoE MoE T=256")
     c4 = bench_moe(c, 3, 256, 64, 8, 1024, 2048, 0, moty_amd.ORDER_TOPK, args.steps, args.warmup,
-                   label="C4 OLMoE MoE layer Q8, T=256, E=64, top-8 softmax (norm_topk_prob=false), I=1024, D=2048")
+                   label="C4 OLMoE MoE layer Q8, T=256, E=64, top-8 softmax (norm_topk_prob=false), I=1024, D=2048",
+                   traffic_key="c4_layer")
     log("C4: %.0f tokens/s, %.3f ms/layer" % (c4["tokens_per_s"], c4["ms_per_layer"]))
     extra = []
     if not args.quick:
@@ -802,7 +809,7 @@ def main():
         for b, lab in ((None, "uniform"), (bias, "skewed (+2.0 on 8 hot experts)")):
             r5 = bench_moe(c, 4, 1072, E5, 8, 768, 2048, 1, moty_amd.ORDER_EXPERT, args.steps, args.warmup, bias=b,
                            label="C5 Qwen3-30B-A3B MoE layer Q8, T=1072 ragged batch (48 decode + 1024 prefill), "
-                                 "E=128, top-8, I=768, D=2048, " + lab)
+                                 "E=128, top-8, I=768, D=2048, " + lab, traffic_key=None if b is not None else "c5_layer")
             extra.append(r5)
     cpu = None
     if not args.no_cpu:
@@ -828,11 +835,11 @@ def main():
         "data": "synthetic (W ~ N(0,0.02) quantized by the library's QBITS=8 kernels, x ~ N(0,1)); "
                 "weights rotate over %d copies" % c1["weight_copies"],
         "config": {"workload": c1["workload"]},
-        "roofline": dict(roofline("hbm", k["gbs"], HBM_PEAK_GBS, "GB/s", pmc_traffic("c1_gate_up_gemv_pmc")),
+        "roofline": dict(roofline("hbm", k["gbs"], HBM_PEAK_GBS, "GB/s", pmc_traffic("hbm_traffic_pmc", "c1_gate_up")),
                          kernel=k["name"], kernel_us=round(k["us"], 3), algo_bytes=k["algo_bytes"],
                          timing="HIP events around graph replays of the kernel alone (weights rotating "
                                 "over the copies), elapsed / launches"),
-        "whole_ffn_roofline": roofline("hbm", c1["gbs"], HBM_PEAK_GBS, "GB/s"),
+        "whole_ffn_roofline": roofline("hbm", c1["gbs"], HBM_PEAK_GBS, "GB/s", pmc_traffic("hbm_traffic_pmc", "c1_step")),
         "cpu_baseline": cpu,
         "moe": moe,
         "extra": extra,
