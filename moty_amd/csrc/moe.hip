@@ -739,9 +739,12 @@ int launch_moe_route(const MoeArgs& a, void* scratch, hipStream_t st) {
   if (K < 1 || K > 64 || K > E || E > 256 || (D % 32) || (I % 32) || (D % 4)) return MOTY_EUNSUP;
   const MoeBufs m = moe_bufs(a, scratch);
   const int P = T * K;
-  // router tiles: 8 tokens x 8 experts of 4 waves for small layers (one
-  // workgroup per CU at T = 256, E = 64), 24 tokens x 32 experts of 12 waves
-  // otherwise; token slices keep every buffer offset below 2^31 bytes
+  // router tiles, from a sweep on MI355X (graph replays, rotating x): 8
+  // tokens x 8 experts of 4 waves with a 4-stage ring for small layers
+  // (T = 256, E = 64: 7.0 us against 7.9 with 8 stages, 9.1 for 8 x 16),
+  // 24 tokens x 32 experts of 12 waves otherwise (T = 1072, E = 128: 20.0
+  // us; 16 x 16: 23.5, 8 x 16: 21.3, 16 x 32: 28.0); token slices keep every
+  // buffer offset below 2^31 bytes
   const bool small = E <= 64 && T <= 1024;
   const int tw = small ? 8 : 24, eg = small ? 8 : 32, nsl = (E + eg - 1) / eg;
   const int tmax = (int)(((int64_t)1 << 31) / ((int64_t)D * 4)) / tw * tw;
@@ -751,7 +754,7 @@ int launch_moe_route(const MoeArgs& a, void* scratch, hipStream_t st) {
     const float* x = a.x + (int64_t)t0 * D;
     const dim3 grid((unsigned)((((ts + tw - 1) / tw + 7) / 8) * 8 * nsl));
     if (small)
-      hipLaunchKernelGGL((k_router<4, 4, 2, 2, 8, 8, 4>), grid, dim3(256), 0, st, x, a.Wr, a.bias, ts, D, E,
+      hipLaunchKernelGGL((k_router<4, 4, 2, 2, 4, 8, 4>), grid, dim3(256), 0, st, x, a.Wr, a.bias, ts, D, E,
                          m.logits + (int64_t)t0 * E);
     else
       hipLaunchKernelGGL((k_router<8, 8, 3, 4, 4, 4, 3>), grid, dim3(768), 0, st, x, a.Wr, a.bias, ts, D, E,
