@@ -630,10 +630,11 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void k_gemm_i4g_h(const uint16_t* 
 }
 
 // The f16-MFMA GEMM (q4b/sclb non-null: PAIR, y = silu(x.q4^T) * (x.q4b^T)).
-// Tiles from a sweep on MI355X at M = 256 (K = 4096, N = 12288: 57 us; K =
-// 12288, N = 4096: 79 us): 128 x 128 block tiles of 8 waves, two stages,
-// when they give at least 160 workgroups; 64 x 64 tiles of 4 waves, three
-// stages, otherwise.
+// Tiles from sweeps on MI355X at M = 256: 128 x 128 block tiles of 8 waves
+// when they give at least 160 workgroups (PAIR gate + up, K = 4096, N =
+// 12288: three stages 88 us, two 96, 64 x 128 93, 64 x 64 97), 64 x 64
+// tiles of 4 waves, three stages, otherwise (down, K = 12288, N = 4096:
+// 67 us; four stages 77, 128 x 128 116).
 int launch_gemm_i4g_h(const uint16_t* xh, const float* sx, const uint8_t* q4, const float* scl, const uint8_t* q4b,
                       const float* sclb, float* y, int M, int I, int O, hipStream_t st) {
   if ((I % 128) || ((((uintptr_t)xh) | ((uintptr_t)q4) | ((uintptr_t)scl) | ((uintptr_t)q4b) | ((uintptr_t)sclb)) & 15))
@@ -645,7 +646,7 @@ int launch_gemm_i4g_h(const uint16_t* xh, const float* sx, const uint8_t* q4, co
   hipLaunchKernelGGL((k_gemm_i4g_h<BM, BN, S, WGM, NW, P>), dim3((O + BN - 1) / BN, (M + BM - 1) / BM),        \
                      dim3(NW * 64), 0, st, xh, sx, q4, scl, q4b, sclb, y, M, I, O)
   if (q4b) {
-    if (big) Q4H(128, 128, 2, 2, 8, true);
+    if (big) Q4H(128, 128, 3, 2, 8, true);
     else Q4H(64, 64, 3, 2, 4, true);
   } else {
     if (big) Q4H(128, 128, 2, 2, 8, false);
