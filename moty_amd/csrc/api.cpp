@@ -448,7 +448,7 @@ static int moe_check(const MotyHipMoe* m, const float* x, float* out, int S, con
   if (!m || !x || !out || S < 0) return set_error("%s: bad arguments", what), MOTY_EINVAL;
   if (m->E <= 0 || m->K <= 0 || m->K > m->E || m->K > 64 || m->I <= 0 || m->D <= 0)
     return set_error("%s: bad shape E=%d K=%d I=%d D=%d", what, m->E, m->K, m->I, m->D), MOTY_EINVAL;
-  if (S > 0 && ((m->D % 32) || (m->I % 32) || m->E > 256 || (size_t)(m->D + m->E) * 4 > 64 * 1024)) {
+  if (S > 0 && ((m->D % 32) || (m->I % 32) || m->E > 256)) {
     set_error("%s: D=%d I=%d E=%d unsupported (D, I multiples of 32, E <= 256)", what, m->D, m->I, m->E);
     return MOTY_EUNSUP;
   }

@@ -339,7 +339,7 @@ int moty_hip_moe_topk_cached_dev(const MotyHipMoe* m, MotyHipExpertCache* c, voi
   if (c->n_experts > 0 && c->n_experts != E)
     return set_error("moe_topk_cached: cache tracks %d experts, layer has %d", c->n_experts, E), MOTY_EINVAL;
   if (S == 0) return MOTY_OK;
-  if ((D % 32) || (I % 32) || E > 256 || (size_t)(D + E) * 4 > 64 * 1024)
+  if ((D % 32) || (I % 32) || E > 256)
     return set_error("moe_topk_cached: D=%d I=%d E=%d unsupported (D, I multiples of 32, E <= 256)", D, I, E),
            MOTY_EUNSUP;
   int rc = ec_check(c, 0, fn, "moe_topk_cached");

@@ -124,11 +124,13 @@ def test_moe_routing_ties(ops, order):
 
 
 @pytest.mark.parametrize("E,K,D,S", [(40, 6, 96, 9), (100, 8, 160, 33), (200, 8, 96, 17), (256, 16, 4160, 5),
-                                     (72, 64, 128, 3), (129, 8, 64, 1), (64, 8, 128, 1030), (16, 4, 96, 1025)])
+                                     (72, 64, 128, 3), (129, 8, 64, 1), (64, 8, 128, 1030), (16, 4, 96, 1025),
+                                     (32, 4, 16384, 3)])
 def test_moe_routing_expert_counts(ops, E, K, D, S):
     # expert counts off the router's tiles (8 / 32 experts per workgroup),
     # the 256-expert configuration, rows past the register-held int8-row path
-    # (D > 4096), K = 64, and few experts past 1024 tokens (the large tile)
+    # (D > 4096, up to 16384), K = 64, and few experts past 1024 tokens (the
+    # large tile)
     say("moe routing", E, K, D, S)
     Wr = randn(11, (E, D), 0.02)
     x = randn(12, (S, D))
