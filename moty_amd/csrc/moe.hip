@@ -18,10 +18,11 @@
 //                  the token's int8 row (qrow_i8)
 //   k_group        one workgroup: per-expert histogram, exclusive scan, slot
 //                  scatter (pairs grouped by expert), M-tile list
-//   k_moe_gateup   grouped GEMM, v_mfma_i32_32x32x32_i8, gate and up rows of
-//                  one expert per workgroup, epilogue silu(g)*u -> h (f32)
-//   k_qrow_i8      h rows -> int8 (the down projection's activation quant)
-//   k_moe_down     grouped GEMM over the same slots -> per-pair rows y
+//   k_moe_gemm<true>   grouped GEMM, v_mfma_i32_32x32x32_i8, gate and up
+//                  rows of one expert per workgroup, epilogue silu(g)*u -> h
+//                  (f32)
+//   k_qrow_wave    h rows -> int8 (the down projection's activation quant)
+//   k_moe_gemm<false>  grouped GEMM over the same slots -> per-pair rows y
 //   k_moe_combine  per token, its K rows in the reference's order, FMA
 // A slot's position inside its expert's segment depends on atomic order,
 // but every slot row is computed independently of the others and the
