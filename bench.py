@@ -341,7 +341,7 @@ def bench_c3(c, steps, warmup):
             # moty_nn_dense_ffn over WF_I4G Mats: gate + up + SiLU in one
             # pass (a GEMV at M = 1, the f16-MFMA GEMM at M = 256), then down
             return lambda: ops.dense_ffn_i4g(x, w[0][0], w[0][1], w[1][0], w[1][1], w[2][0], w[2][1], out=y)
-        t, n = c.time_steps([step(w) for w in copies], max(8, steps // (8 if M == 1 else 64)), 8)
+        t, n = c.time_steps([step(w) for w in copies], max(8, steps // (8 if M == 1 else 16)), 8)
         ops_int = 2 * M * 3 * I * D
         algo = wbytes + M * (D + I + I + D) * 4
         tr = pmc_traffic("hbm_traffic_pmc", "c3_M%d_step" % M)
@@ -406,7 +406,7 @@ def bench_c3_r4(c, steps, warmup):
         res["_cpu"]["x"][M] = x
         y = torch.empty((M, D), device="cuda:0")
         t, n = c.time_steps([lambda w=w: ops.dense_ffn_r4(x, w[0], w[1], w[2], w[3], I, out=y) for w in copies],
-                            max(8, steps // (8 if M == 1 else 64)), 8)
+                            max(8, steps // (8 if M == 1 else 16)), 8)
         ops_int = 2 * M * 3 * I * D
         algo = wbytes + M * (D + D) * 4
         tr = pmc_traffic("hbm_traffic_pmc", "c3r4_M%d_step" % M)
