@@ -400,11 +400,21 @@ __global__ __launch_bounds__(Q4M_NT, 2) void k_gemm_i4g(const int8_t* __restrict
 // MFMA returns d_g already as an exact float, so the epilogue is one FMA per
 // output per group instead of a conversion and an FMA.
 //
-// Weight nibbles become halves with two integer ops and a packed f16 add per
-// pair: (w >> 4i) & 0x000f000f | 0x64006400 is the half pair (1024 + n_a,
-// 1024 + n_b), minus 1032 gives (n_a - 8, n_b - 8).  One nibble dword (8
-// codes, elements e0..e7) unpacks to the order [e0,e4,e1,e5,e2,e6,e3,e7];
-// the activations arrive from k_qrow_f16p in the same order.
+// Weight nibbles become halves with one v_and_or_b32 per pair and no
+// float op: in a dword of 4 weight bytes, (w & 0x000f000f) | 0x64006400 is
+// the half pair (1024 + n) of the low nibbles of bytes 0 and 2, the mask
+// 0x00f000f0 gives (1024 + 16 n) for their high nibbles, and w >> 8 serves
+// bytes 1 and 3 alike.  So a lane's 8 bytes of a group (16 codes e0..e15)
+// become two 8-half fragments, low nibbles [e0,e4,e2,e6,e8,e12,e10,e14] and
+// high nibbles [e1,e5,...] at 16x, matched by k_qrow_f16p's activation
+// fragments x and x/16.  With the activations x, the two MFMAs give
+//   sum_lo x (1024 + n) + sum_hi x (64 + n) = d_g + 1032 sum_lo x + 72 sum_hi x,
+// and two more MFMAs of the same activation fragments against constant
+// fragments (-1032 and -1152 = -72 * 16) give the offset, once per token
+// tile and group for every weight tile: it enters the first product MFMA as
+// its accumulator.  Every value is an integer below 2^23 in magnitude (|x|
+// <= 127, 16 terms of each kind), so every sum is exact and d_g comes out
+// exactly as the reference's integer group dot.
 //
 // Block tile BM tokens x BN weight rows, 4 waves as 2 x 2, each wave FM x FN
 // 32 x 32 tiles.  K blocks of 4 groups (128 elements) move global -> LDS by
@@ -413,23 +423,27 @@ __global__ __launch_bounds__(Q4M_NT, 2) void k_gemm_i4g(const int8_t* __restrict
 // 16 distinct bank groups), BN nibble rows of 64 B (chunk c in slot
 // c ^ ((r >> 2) & 3)) and BN scale rows of 16 B (the block's 4 group scales).
 // Lane l takes, for group j, half h = l / 32 of its rows' group: elements
-// [16h, 16h + 16) -- the first 8 for MFMA 0, the next 8 for MFMA 1.
+// [16h, 16h + 16) -- the low-nibble fragment for MFMA 0, the high for MFMA 1.
 constexpr int Q4H_NT = 256;
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-// 8 nibble codes (one dword) -> 8 halves n - 8, order [e0,e4,e1,e5,e2,e6,e3,e7].
-// m = 0x000f000f and o = 0x64006400 arrive in VGPRs so that each pair is one
-// v_and_or_b32 (VOP3 takes no literal here) and one v_pk_add_f16.
-__device__ __forceinline__ v8h nib8_to_h(uint32_t w, uint32_t m, uint32_t o) {
-  const h2v bias = h2v{(_Float16)-1032.f, (_Float16)-1032.f};
-  const h2v p0 = __builtin_bit_cast(h2v, (w & m) | o) + bias;
-  const h2v p1 = __builtin_bit_cast(h2v, ((w >> 4) & m) | o) + bias;
-  const h2v p2 = __builtin_bit_cast(h2v, ((w >> 8) & m) | o) + bias;
-  const h2v p3 = __builtin_bit_cast(h2v, ((w >> 12) & m) | o) + bias;
-  return v8h{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+// A lane's 8 nibble bytes of a group -> the low- and high-nibble fragments.
+// m = 0x000f000f, m4 = 0x00f000f0 and o = 0x64006400 arrive in VGPRs so that
+// each pair is one v_and_or_b32 (VOP3 takes no literal here).
+__device__ __forceinline__ void nib16_to_h(uint2 w, uint32_t m, uint32_t m4, uint32_t o, v8h& lo, v8h& hi) {
+  const uint32_t t0 = w.x >> 8, t1 = w.y >> 8;
+  typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+  lo = __builtin_bit_cast(v8h, u4v{(w.x & m) | o, (t0 & m) | o, (w.y & m) | o, (t1 & m) | o});
+  hi = __builtin_bit_cast(v8h, u4v{(w.x & m4) | o, (t0 & m4) | o, (w.y & m4) | o, (t1 & m4) | o});
+}
+// The same fragments with the offsets taken off in the halves (packed f16
+// adds, exact): n - 8 and 16 (n - 8).
+__device__ __forceinline__ void nib16_to_h_c(uint2 w, uint32_t m, uint32_t m4, uint32_t o, v8h& lo, v8h& hi) {
+  nib16_to_h(w, m, m4, o, lo, hi);
+  lo += v8h{-1032, -1032, -1032, -1032, -1032, -1032, -1032, -1032};
+  hi += v8h{-1152, -1152, -1152, -1152, -1152, -1152, -1152, -1152};
 }
 
 // PAIR: gate and up rows of the same block tile in one pass (the activation
@@ -514,9 +528,12 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void k_gemm_i4g_h(const uint16_t* 
     const int m = mb + tid % BM;
     sxr = sx[m < M ? m : M - 1];
   }
-  uint32_t km, ko;
+  uint32_t km, km4, ko;
   asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(km));
+  asm volatile("v_mov_b32 %0, 0x00f000f0" : "=v"(km4));
   asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(ko));
+  const v8h c_lo = v8h{-1032, -1032, -1032, -1032, -1032, -1032, -1032, -1032};
+  const v8h c_hi = v8h{-1152, -1152, -1152, -1152, -1152, -1152, -1152, -1152};
   float acc[NP][FM][FN][16];
 #pragma unroll
   for (int p = 0; p < NP; p++)
@@ -561,23 +578,35 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void k_gemm_i4g_h(const uint16_t* 
         }
     }
   };
+  // PAIR takes the offsets off in the weight halves (two packed adds per
+  // 4 halves, shared by the FM token tiles); the single-matrix form, with
+  // one weight tile per wave, computes them on the matrix core instead
+  constexpr bool OFS_MFMA = !PAIR;
   auto compute = [&](const Frags& f) {
 #pragma unroll
     for (int gl = 0; gl < 4; gl++) {
+      v8h fb[NP][FN][2];
 #pragma unroll
-      for (int p = 0; p < NP; p++) {
-        v8h fb[FN][2];
+      for (int p = 0; p < NP; p++)
 #pragma unroll
         for (int j = 0; j < FN; j++) {
-          fb[j][0] = nib8_to_h(f.b[gl][p][j].x, km, ko);
-          fb[j][1] = nib8_to_h(f.b[gl][p][j].y, km, ko);
+          if (OFS_MFMA) nib16_to_h(f.b[gl][p][j], km, km4, ko, fb[p][j][0], fb[p][j][1]);
+          else nib16_to_h_c(f.b[gl][p][j], km, km4, ko, fb[p][j][0], fb[p][j][1]);
         }
 #pragma unroll
-        for (int i = 0; i < FM; i++)
+      for (int i = 0; i < FM; i++) {
+        // the offset -1032 sum_lo x - 72 sum_hi x of each token row
+        v16f d3 = v16f{};
+        if (OFS_MFMA) {
+          d3 = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[gl][i][0], c_lo, d3, 0, 0, 0);
+          d3 = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[gl][i][1], c_hi, d3, 0, 0, 0);
+        }
+#pragma unroll
+        for (int p = 0; p < NP; p++)
 #pragma unroll
           for (int j = 0; j < FN; j++) {
-            v16f d = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[gl][i][0], fb[j][0], v16f{}, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[gl][i][1], fb[j][1], d, 0, 0, 0);
+            v16f d = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[gl][i][0], fb[p][j][0], d3, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[gl][i][1], fb[p][j][1], d, 0, 0, 0);
             const float4 sv = f.s[p][j];
             const float s = gl == 0 ? sv.x : gl == 1 ? sv.y : gl == 2 ? sv.z : sv.w;
 #pragma unroll
@@ -632,9 +661,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void k_gemm_i4g_h(const uint16_t* 
 // The f16-MFMA GEMM (q4b/sclb non-null: PAIR, y = silu(x.q4^T) * (x.q4b^T)).
 // Tiles from sweeps on MI355X at M = 256: 128 x 128 block tiles of 8 waves
 // when they give at least 160 workgroups (PAIR gate + up, K = 4096, N =
-// 12288: three stages 88 us, two 96, 64 x 128 93, 64 x 64 97), 64 x 64
+// 12288: three stages 86 us, two 92, 64 x 128 93, 64 x 64 94), 64 x 64
 // tiles of 4 waves, three stages, otherwise (down, K = 12288, N = 4096:
-// 67 us; four stages 77, 128 x 128 116).
+// 64 us; four stages 69, 128 x 128 113).
 int launch_gemm_i4g_h(const uint16_t* xh, const float* sx, const uint8_t* q4, const float* scl, const uint8_t* q4b,
                       const float* sclb, float* y, int M, int I, int O, hipStream_t st) {
   if ((I % 128) || ((((uintptr_t)xh) | ((uintptr_t)q4) | ((uintptr_t)scl) | ((uintptr_t)q4b) | ((uintptr_t)sclb)) & 15))

@@ -205,60 +205,71 @@ int launch_qrow_i8(const float* x, int8_t* q, float* sx, int32_t* xg, int S, int
 }
 
 // qrow_i8 (hw/hw_quant.h:9-16) with the codes written as f16 -- exact, they
-// are integers in [-127, 127] -- for the f16-MFMA grouped-int4 GEMM.  Every
-// run of 8 codes is stored in the order [0,4,1,5,2,6,3,7], the order in
-// which that GEMM unpacks 8 weight nibbles (a k-permutation shared by both
-// operands, exact for the integer-valued dots).  One workgroup per row, the
-// row held in registers: NR runs of 8 per thread (run t + NT*j).
-template <int NT, int NR>
+// are integers in [-127, 127] -- for the f16-MFMA grouped-int4 GEMM.  Each
+// run of 16 codes c0..c15 is stored as the two 8-code fragments that GEMM
+// multiplies against the low and the high nibbles of the same 8 weight
+// bytes: [c0, c4, c2, c6, c8, c12, c10, c14] and [c1, c5, c3, c7, c9, c13,
+// c11, c15] / 16 (a k-permutation shared by both operands; the division by
+// 16 is exact and matches the high nibbles' 16x weight halves).  One
+// workgroup per row, the row held in registers: NU runs per thread (run
+// t + NT*j).
+template <int NT, int NU>
 __global__ __launch_bounds__(NT) void k_qrow_f16p(const float* __restrict__ x, uint16_t* __restrict__ xh,
                                                   float* __restrict__ sx, int I) {
   __shared__ float red[NT / MOTY_WAVE];
   const int64_t row = blockIdx.x;
   const float* xr = x + row * I;
-  const int nrun = I / 8;
-  float4 v[NR][2];
+  const int nrun = I / 16;
+  float4 v[NU][4];
   float amax = 0.f;
 #pragma unroll
-  for (int j = 0; j < NR; j++) {
+  for (int j = 0; j < NU; j++) {
     const int r = threadIdx.x + NT * j;
     const int rc = r < nrun ? r : 0;
-    v[j][0] = sel4(r < nrun, *(const float4*)(xr + 8 * rc));
-    v[j][1] = sel4(r < nrun, *(const float4*)(xr + 8 * rc + 4));
-    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j][0].x), fabsf(v[j][0].y)), fmaxf(fabsf(v[j][0].z), fabsf(v[j][0].w))));
-    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j][1].x), fabsf(v[j][1].y)), fmaxf(fabsf(v[j][1].z), fabsf(v[j][1].w))));
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      v[j][q] = sel4(r < nrun, *(const float4*)(xr + 16 * rc + 4 * q));
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j][q].x), fabsf(v[j][q].y)), fmaxf(fabsf(v[j][q].z), fabsf(v[j][q].w))));
+    }
   }
   amax = block_max<NT>(amax, red);
   float s = amax / 127.f;
   if (s < 1e-12f) s = 1e-12f;
   const float inv = 1.f / s;
   if (threadIdx.x == 0) sx[row] = s;
+  auto hb = [](float c) { return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)c); };
 #pragma unroll
-  for (int j = 0; j < NR; j++) {
+  for (int j = 0; j < NU; j++) {
     const int r = threadIdx.x + NT * j;
     if (r >= nrun) break;
-    const float e[8] = {v[j][0].x, v[j][0].y, v[j][0].z, v[j][0].w, v[j][1].x, v[j][1].y, v[j][1].z, v[j][1].w};
-    uint32_t h[8];
+    float c[16];
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const _Float16 c = (_Float16)(float)rne_int(e[k] * inv);
-      h[k] = (uint32_t)__builtin_bit_cast(uint16_t, c);
+    for (int q = 0; q < 4; q++) {
+      c[4 * q] = (float)rne_int(v[j][q].x * inv);
+      c[4 * q + 1] = (float)rne_int(v[j][q].y * inv);
+      c[4 * q + 2] = (float)rne_int(v[j][q].z * inv);
+      c[4 * q + 3] = (float)rne_int(v[j][q].w * inv);
     }
-    const uint4 o = uint4{h[0] | (h[4] << 16), h[1] | (h[5] << 16), h[2] | (h[6] << 16), h[3] | (h[7] << 16)};
-    *(uint4*)(xh + row * I + 8 * r) = o;
+    const uint4 lo = uint4{hb(c[0]) | (hb(c[4]) << 16), hb(c[2]) | (hb(c[6]) << 16), hb(c[8]) | (hb(c[12]) << 16),
+                           hb(c[10]) | (hb(c[14]) << 16)};
+    const float k = 0.0625f;
+    const uint4 hi = uint4{hb(c[1] * k) | (hb(c[5] * k) << 16), hb(c[3] * k) | (hb(c[7] * k) << 16),
+                           hb(c[9] * k) | (hb(c[13] * k) << 16), hb(c[11] * k) | (hb(c[15] * k) << 16)};
+    *(uint4*)(xh + row * I + 16 * r) = lo;
+    *(uint4*)(xh + row * I + 16 * r + 8) = hi;
   }
 }
 
 int launch_qrow_f16p(const float* x, uint16_t* xh, float* sx, int S, int I, hipStream_t st) {
   if (S <= 0) return MOTY_OK;
-  if ((I % 8) || (((uintptr_t)x) & 15) || (((uintptr_t)xh) & 15)) return MOTY_EUNSUP;
-  const int runs = (I / 8 + 255) / 256;
-  if (runs <= 2)
+  if ((I % 16) || (((uintptr_t)x) & 15) || (((uintptr_t)xh) & 15)) return MOTY_EUNSUP;
+  const int runs = (I / 16 + 255) / 256;
+  if (runs <= 1)
+    hipLaunchKernelGGL((k_qrow_f16p<256, 1>), dim3(S), dim3(256), 0, st, x, xh, sx, I);
+  else if (runs <= 2)
     hipLaunchKernelGGL((k_qrow_f16p<256, 2>), dim3(S), dim3(256), 0, st, x, xh, sx, I);
   else if (runs <= 4)
     hipLaunchKernelGGL((k_qrow_f16p<256, 4>), dim3(S), dim3(256), 0, st, x, xh, sx, I);
-  else if (runs <= 8)
-    hipLaunchKernelGGL((k_qrow_f16p<256, 8>), dim3(S), dim3(256), 0, st, x, xh, sx, I);
   else
     return MOTY_EUNSUP;
   LAUNCH_TRY("k_qrow_f16p");
