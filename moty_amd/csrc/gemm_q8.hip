@@ -167,7 +167,7 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_gemm_q8_dma(const int8_
   constexpr int NI = (BM + BN) / (8 * NW);   // DMA instructions per wave per stage
   constexpr int TM = BM / WGM, TN = BN / WGN, FM = TM / 32, FN = TN / 32;
   static_assert((BM + BN) % (8 * NW) == 0 && FM >= 1 && FN >= 1, "tile shape");
-  static_assert(KS == 1 || KS * STAGE * S >= NW * 64 * FM * FN * 64, "room for the partial sums");
+  static_assert(KS == 1 || KS * STAGE * S >= (KS - 1) * NW * 64 * FM * FN * 64, "room for the partial sums");
   __shared__ __align__(1024) int8_t lds[S * KS * STAGE];
   __shared__ float s_sx[BM];
   const int tid = threadIdx.x, lane = tid % MOTY_WAVE, wv = tid / MOTY_WAVE;
@@ -250,10 +250,12 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_gemm_q8_dma(const int8_
   // workgroup's LDS can be released or reused
   __builtin_amdgcn_s_waitcnt(0);
   if (KS > 1) {
-    // the second group's partial sums through LDS, added by the first
+    // the other groups' partial sums through LDS, added by the first (int32:
+    // exact in any order)
     __syncthreads();
-    int* part = (int*)lds + (w * 64 + lane) * (FM * FN * 16);
-    if (kg == 1) {
+    constexpr int PW = FM * FN * 16;  // ints per lane
+    if (kg > 0) {
+      int* part = (int*)lds + (((kg - 1) * NW + w) * 64 + lane) * PW;
 #pragma unroll
       for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -262,9 +264,13 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_gemm_q8_dma(const int8_
     __syncthreads();
     if (kg == 0) {
 #pragma unroll
-      for (int i = 0; i < FM; i++)
+      for (int q = 1; q < KS; q++) {
+        const int* part = (const int*)lds + (((q - 1) * NW + w) * 64 + lane) * PW;
 #pragma unroll
-        for (int j = 0; j < FN; j++) acc[i][j] += *(const v16i*)(part + (i * FN + j) * 16);
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+          for (int j = 0; j < FN; j++) acc[i][j] += *(const v16i*)(part + (i * FN + j) * 16);
+      }
     }
   }
   if (tid < BM) s_sx[tid] = sxr;
@@ -298,11 +304,16 @@ int launch_gemm_q8(const int8_t* xq, const float* sx, const int8_t* W, const flo
     // K = 1024: 15.2 us); below that 64 x 32 tiles with two groups of 2 waves
     // on alternate K blocks (N = 1024, K = 2048: 7.1 us vs 7.4; K = 3072: 8.7
     // vs 9.3) -- these GEMMs are bound by each workgroup's K-loop latency,
-    // not by the grid's width.
+    // not by the grid's width.  Four groups of 2 waves (three stages) where
+    // K holds at least 4 blocks: 6.3 / 7.3 us against 6.9 / 8.5 with two,
+    // timed back to back on rotating weights (inside the C2 layer step, after
+    // the wide GEMM, both forms average 8.0 us).
 #define QD(BM, BN, S, WM, WN, KS)                                                                             \
   hipLaunchKernelGGL((k_gemm_q8_dma<BM, BN, S, WM, WN, KS>), dim3((O + BN - 1) / BN, (M + BM - 1) / BM),       \
                      dim3(64 * WM * WN * KS), 0, st, xq, sx, W, scale, y, M, K, O)
-    if ((int64_t)((M + 63) / 64) * ((O + 63) / 64) < 256 && K >= 2 * GM_KB) QD(64, 32, 4, 2, 1, 2);
+    const bool narrow = (int64_t)((M + 63) / 64) * ((O + 63) / 64) < 256;
+    if (narrow && K >= 4 * GM_KB) QD(64, 32, 3, 2, 1, 4);
+    else if (narrow && K >= 2 * GM_KB) QD(64, 32, 4, 2, 1, 2);
     else if (K <= 1024) QD(64, 64, 3, 2, 2, 1);
     else QD(64, 64, 4, 2, 2, 1);
 #undef QD

@@ -107,6 +107,8 @@ Q8_CASES = [(1, 1024, 3072), (1, 3072, 1024), (2, 1024, 100), (3, 48, 24), (4, 2
             (130, 2048, 200), (33, 16, 17), (1024, 1024, 4096), (256, 1040, 8192), (200, 3072, 1000),
             # K % 128 == 0 past the GEMV: the DMA-staged GEMM, one-block and ragged tiles
             (70, 128, 33), (9, 256, 1), (130, 384, 65), (600, 4096, 100), (5, 128, 7),
+            # few tiles: K split over four wave groups (K blocks 4, 5, 16)
+            (17, 512, 50), (40, 640, 96), (130, 2048, 200),
             # S = 1 past 16 MiB of weights: the shared-activation GEMV, full and ragged
             (1, 4096, 4096), (1, 3088, 5500), (1, 1040, 16200)]
 
