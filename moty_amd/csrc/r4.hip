@@ -387,12 +387,19 @@ static int launch_r4_gemv(const float* x, const uint8_t* W, const uint16_t* d16,
 //   acc = fma(float(s + m8), dd*xs, acc);  acc = fma(-dd, xct, acc)
 // reproduces both reference forms (the second FMA adds -dd*0 to a nonzero-
 // signed or +0 accumulator: exactly nothing).  Q8R4 runs the first FMA only.
+// WV = 8 / 16: eight waves of 16 tokens x 32 rows each (two
+// v_mfma_i32_16x16x32_i8 per group) or sixteen of 16 x 16, over the same block tile and staging (done by the first four
+// waves), for grids that give one workgroup per CU: two waves per SIMD
+// instead of one.  Lane l's fragments: A = codes [8(l/16), +8) of token row
+// l % 16; B = the same k of weight row l % 16 -- for Q4R4 the low (k < 16)
+// or high nibbles of bytes [8(l/16 % 2), +8) of the row's 16 group bytes,
+// byte j holding codes j and j + 16.
 constexpr int R4M_NT = 256;
 constexpr int R4M_KG = 4;                 // groups per K block
 constexpr int R4M_AS = R4M_KG * 32 + 16;  // A row stride (bytes)
 
-template <bool Q8, bool TILE = false>
-__global__ __launch_bounds__(R4M_NT, 2) void k_r4_gemm(const int8_t* __restrict__ xq, const float* __restrict__ xs,
+template <bool Q8, bool TILE = false, int WV = 4>
+__global__ __launch_bounds__(64 * WV, WV <= 8 ? 8 / WV : 1) void k_r4_gemm(const int8_t* __restrict__ xq, const float* __restrict__ xs,
                                                        const int32_t* __restrict__ xm,
                                                        const uint8_t* __restrict__ W,
                                                        const uint16_t* __restrict__ d16, float* __restrict__ y,
@@ -401,6 +408,8 @@ __global__ __launch_bounds__(R4M_NT, 2) void k_r4_gemm(const int8_t* __restrict_
   constexpr int RB = Q8 ? 32 : 16;          // bytes per (row, group)
   constexpr int BS = R4M_KG * RB + 16;      // B row stride (bytes)
   constexpr int NBC = Q8 ? 2 : 1;           // B chunks per thread
+  constexpr int NWN = WV / 4, JN = 4 / NWN;  // WV >= 8: waves along the rows, 16-row tiles per wave
+  static_assert(WV == 4 || WV == 8 || WV == 16, "waves");
   __shared__ __align__(16) int8_t sA[64 * R4M_AS];
   __shared__ __align__(16) uint8_t sB[64 * BS];
   __shared__ float sD[64 * R4M_KG];         // [row][group]
@@ -441,8 +450,10 @@ __global__ __launch_bounds__(R4M_NT, 2) void k_r4_gemm(const int8_t* __restrict_
     int m;
   };
   Set s0, s1;
+  const bool stager = WV == 4 || tid < R4M_NT;  // wave-uniform
   const int glast = (nb - 1) / R4M_KG * R4M_KG;
   auto gload = [&](int g0, Set& sv) {
+    if (!stager) return;
     const int gc = g0 < nb ? g0 : glast;
     const int kb = gc * 32;
 #pragma unroll
@@ -464,6 +475,7 @@ __global__ __launch_bounds__(R4M_NT, 2) void k_r4_gemm(const int8_t* __restrict_
   for (int r = 0; r < 16; r++) accf[r] = 0.f;
   auto stage = [&](int g0, Set& sv) {
     const int kb = g0 * 32;
+    if (stager) {
 #pragma unroll
     for (int i = 0; i < 2; i++) {
       const int q = tid + i * R4M_NT;
@@ -480,9 +492,49 @@ __global__ __launch_bounds__(R4M_NT, 2) void k_r4_gemm(const int8_t* __restrict_
       sM[st_g * 64 + (tid & 63)] = (ok && !st_tile) ? -8 * sv.m : 0;
       sC[st_g * 64 + (tid & 63)] = (ok && st_tile) ? (8.f * (float)sv.m) * xv : 0.f;
     }
+    }
     __syncthreads();
     gload(g0 + 2 * R4M_KG, sv);
-    if constexpr (Q8) {
+    if constexpr (WV >= 8) {
+      // wave: tokens wm16 * 16 + [0, 16) x rows wn16 * 16 * JN + [0, 16 * JN)
+      const int wm16 = wv / NWN, wn16 = wv % NWN, r16 = lane & 15, q4 = lane >> 4;
+      const int ngk = (nb - g0) < R4M_KG ? (nb - g0) : R4M_KG;
+      const int tb = wm16 * 16 + 4 * q4;  // this lane's 4 tokens (D rows)
+#pragma unroll
+      for (int gg = 0; gg < R4M_KG; gg++) {
+        if (gg >= ngk) break;  // wave-uniform
+        const long a = *(const long*)(sA + (wm16 * 16 + r16) * R4M_AS + gg * 32 + q4 * 8);
+        const float4 xv = *(const float4*)(sX + gg * 64 + tb);
+        const int4 mv = (Q8 || TILE) ? int4{0, 0, 0, 0} : *(const int4*)(sM + gg * 64 + tb);
+        const float4 cv = Q8 ? float4{0.f, 0.f, 0.f, 0.f} : *(const float4*)(sC + gg * 64 + tb);
+#pragma unroll
+        for (int jn = 0; jn < JN; jn++) {
+          const int row = wn16 * 16 * JN + jn * 16 + r16;
+          long b;
+          if (Q8) {
+            b = *(const long*)(sB + row * BS + gg * RB + q4 * 8);
+          } else {
+            const uint2 w = *(const uint2*)(sB + row * BS + gg * RB + (q4 & 1) * 8);
+            const int sh = (q4 >> 1) * 4;
+            b = (long)(((w.x >> sh) & 0x0f0f0f0fu) | ((uint64_t)((w.y >> sh) & 0x0f0f0f0fu) << 32));
+          }
+          const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, v4i{0, 0, 0, 0}, 0, 0, 0);
+          const float dd = sD[row * R4M_KG + gg];
+          float* ac = accf + 4 * jn;
+          if (Q8) {
+            ac[0] = __fmaf_rn((float)d[0], dd * xv.x, ac[0]);
+            ac[1] = __fmaf_rn((float)d[1], dd * xv.y, ac[1]);
+            ac[2] = __fmaf_rn((float)d[2], dd * xv.z, ac[2]);
+            ac[3] = __fmaf_rn((float)d[3], dd * xv.w, ac[3]);
+          } else {
+            ac[0] = __fmaf_rn(-dd, cv.x, __fmaf_rn((float)(d[0] + mv.x), dd * xv.x, ac[0]));
+            ac[1] = __fmaf_rn(-dd, cv.y, __fmaf_rn((float)(d[1] + mv.y), dd * xv.y, ac[1]));
+            ac[2] = __fmaf_rn(-dd, cv.z, __fmaf_rn((float)(d[2] + mv.z), dd * xv.z, ac[2]));
+            ac[3] = __fmaf_rn(-dd, cv.w, __fmaf_rn((float)(d[3] + mv.w), dd * xv.w, ac[3]));
+          }
+        }
+      }
+    } else if constexpr (Q8) {
       // Straight-line over the block's groups -- fragments, the MFMAs, then
       // the epilogues in group order -- so the MFMAs overlap.  Groups past
       // the row end hold zero codes and scales: their steps add exactly
@@ -550,6 +602,20 @@ __global__ __launch_bounds__(R4M_NT, 2) void k_r4_gemm(const int8_t* __restrict_
   }
   // retire the clamped prefetches once before the conditional stores
   __builtin_amdgcn_s_waitcnt(0);
+  if constexpr (WV >= 8) {
+    const int wm16 = wv / NWN, wn16 = wv % NWN, r16 = lane & 15, q4 = lane >> 4;
+#pragma unroll
+    for (int jn = 0; jn < JN; jn++) {
+      const int col = nb0 + wn16 * 16 * JN + jn * 16 + r16;
+      if (col >= O) continue;
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int t = mb + wm16 * 16 + 4 * q4 + r;
+        if (t < S) y[(int64_t)t * O + col] = accf[4 * jn + r];
+      }
+    }
+    return;
+  }
   const int col = nb0 + wn * 32 + r32;
   if (col >= O) return;
 #pragma unroll
@@ -573,12 +639,25 @@ int launch_r4_matmul(bool q8, const float* x, const uint8_t* W, const uint16_t* 
   int rc = launch_quant_g32(x, xq, xs, xm, S, I, st);
   if (rc) return rc;
   dim3 grid((O + 63) / 64, (S + 63) / 64);
-  if (q8)
-    hipLaunchKernelGGL(k_r4_gemm<true>, grid, dim3(R4M_NT), 0, st, xq, xs, xm, W, d16, y, S, I, O);
-  else if (S % 4 == 0)  // every token in the tile kernel's form
-    hipLaunchKernelGGL((k_r4_gemm<false, true>), grid, dim3(R4M_NT), 0, st, xq, xs, xm, W, d16, y, S, I, O);
-  else
-    hipLaunchKernelGGL(k_r4_gemm<false>, grid, dim3(R4M_NT), 0, st, xq, xs, xm, W, d16, y, S, I, O);
+  // at most one workgroup per CU: sixteen waves of 16 x 16 (four per SIMD
+  // instead of one); measured on MI355X at S = 256, 4096 x 12288: Q4R4 92.7
+  // us against 132 with four waves (eight: 112), Q8R4 95.9 against 104.  The
+  // wider grids keep four waves of 32 x 32 (24576 x 4096: 147 us; eight or
+  // sixteen waves 179 / 191).
+  const bool few = (int64_t)grid.x * grid.y <= 256;
+#define R4G(Q, T, WV) \
+  hipLaunchKernelGGL((k_r4_gemm<Q, T, WV>), grid, dim3(64 * WV), 0, st, xq, xs, xm, W, d16, y, S, I, O)
+  if (q8) {
+    if (few) R4G(true, false, 16);
+    else R4G(true, false, 4);
+  } else if (S % 4 == 0) {  // every token in the tile kernel's form
+    if (few) R4G(false, true, 16);
+    else R4G(false, true, 4);
+  } else {
+    if (few) R4G(false, false, 16);
+    else R4G(false, false, 4);
+  }
+#undef R4G
   LAUNCH_TRY("k_r4_gemm");
   return MOTY_OK;
 }

@@ -55,7 +55,9 @@ CASES = [(64, 96, 1), (37, 64, 1), (38, 128, 7), (20, 64, 37), (12, 4800, 6), (1
          (8, 64, 33), (1000, 1024, 1), (3072, 1024, 1), (1024, 3072, 1), (1024, 4096, 2), (256, 8192, 1),
          (100, 12288, 1), (192, 4096, 64), (130, 1024, 130), (4096, 1024, 5), (2048, 2048, 4), (64, 4096, 3),
          (1, 32, 1), (7, 32, 9), (64, 16384, 1), (64, 8192, 2), (300, 12288, 1), (40, 8192, 1),
-         (256, 3040, 1), (520, 7200, 2), (6000, 2048, 1), (4100, 1056, 3)]
+         (256, 3040, 1), (520, 7200, 2), (6000, 2048, 1), (4100, 1056, 3),
+         # GEMM grids past 256 tiles (four 32 x 32 waves), ragged and whole token tiles
+         (8192, 512, 130), (17000, 256, 64)]
 
 
 @pytest.mark.parametrize("q8", [False, True])
