@@ -312,7 +312,7 @@ int moty_hip_matmul_i4_grouped_s_dev(float* y, const float* x, const uint8_t* q4
       if (rc) return rc;
       uint16_t* xh = (uint16_t*)sp;
       float* sx = (float*)((char*)sp + hb);
-      if ((rc = launch_qrow_f16p(x, xh, sx, S, I, st))) return rc;
+      if ((rc = launch_qrow_f16p(x, xh, sx, S, I, gemm_i4g_h_f8(S, O, false), st))) return rc;
       return launch_gemm_i4g_h(xh, sx, q4, scale, nullptr, nullptr, y, S, I, O, st);
     }
     const size_t xb = al256((size_t)S * I);
@@ -510,9 +510,9 @@ int moty_hip_dense_ffn_i4g_dev(float* out, const float* x, int S, const uint8_t*
   void* xq = (char*)sp + 2 * bh;
   float* sx = (float*)((char*)sp + 2 * bh + bq);
   if (h16) {
-    if ((rc = launch_qrow_f16p(x, (uint16_t*)xq, sx, S, D, st))) return rc;
+    if ((rc = launch_qrow_f16p(x, (uint16_t*)xq, sx, S, D, gemm_i4g_h_f8(S, I, true), st))) return rc;
     if ((rc = launch_gemm_i4g_h((const uint16_t*)xq, sx, gate, gs, up, us, h, S, D, I, st))) return rc;
-    if ((rc = launch_qrow_f16p(h, (uint16_t*)xq, sx, S, I, st))) return rc;
+    if ((rc = launch_qrow_f16p(h, (uint16_t*)xq, sx, S, I, gemm_i4g_h_f8(S, D, false), st))) return rc;
     return launch_gemm_i4g_h((const uint16_t*)xq, sx, down, ds, nullptr, nullptr, out, S, I, D, st);
   }
   if (vec && S == 1) {

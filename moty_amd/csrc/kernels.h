@@ -14,9 +14,10 @@ constexpr int MOE_NBUF = 15;   // MoE scratch sub-buffers
 
 int launch_qrow_i8(const float* x, int8_t* q, float* sx, int32_t* xg, int S, int I, int64_t ldx, int64_t ldq,
                    hipStream_t st);
-// qrow_i8 with f16 codes in the k-permuted run order of the f16-MFMA
-// grouped-int4 GEMM; I % 8 == 0, I <= 16384, x and xh 16-byte aligned
-int launch_qrow_f16p(const float* x, uint16_t* xh, float* sx, int S, int I, hipStream_t st);
+// qrow_i8 with f16 codes in the k-permuted fragment order of the f16-MFMA
+// grouped-int4 GEMM (f8: its 16 x 16 form, see gemm_i4g_h_f8); I % 16 == 0,
+// I <= 16384, x and xh 16-byte aligned
+int launch_qrow_f16p(const float* x, uint16_t* xh, float* sx, int S, int I, int f8, hipStream_t st);
 // per-row int4 weights (WF_I4, nn/quant.c:34-55) and their expansion to
 // int8 codes n - 8 (I % 16 == 0; n = O * I codes)
 int launch_pack_i4row(const float* w, uint8_t* q4, float* scale, int O, int I, hipStream_t st);
@@ -42,6 +43,9 @@ int launch_gemm_i4g(const int8_t* xq, const float* sx, const uint8_t* q4, const 
 // I % 128 != 0 or a pointer is not 16-byte aligned
 int launch_gemm_i4g_h(const uint16_t* xh, const float* sx, const uint8_t* q4, const float* scl, const uint8_t* q4b,
                       const float* sclb, float* y, int M, int I, int O, hipStream_t st);
+// 1 when launch_gemm_i4g_h runs its 16 x 16 form at this shape: its
+// activations then come from launch_qrow_f16p with f8 = 1
+int gemm_i4g_h_f8(int M, int O, bool pair);
 int launch_i4g_f32(const float* x, const uint8_t* q4, const float* scl, float* y, int S, int I, int O,
                    hipStream_t st);
 

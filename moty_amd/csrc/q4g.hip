@@ -16,6 +16,8 @@
 #include "kernels.h"
 #include <stdlib.h>
 
+#include <type_traits>
+
 namespace moty {
 
 // ---------------------------------------------------------------------------
@@ -428,6 +430,7 @@ constexpr int Q4H_NT = 256;
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 // A lane's 8 nibble bytes of a group -> the low- and high-nibble fragments.
 // m = 0x000f000f, m4 = 0x00f000f0 and o = 0x64006400 arrive in VGPRs so that
@@ -437,6 +440,16 @@ __device__ __forceinline__ void nib16_to_h(uint2 w, uint32_t m, uint32_t m4, uin
   typedef uint32_t u4v __attribute__((ext_vector_type(4)));
   lo = __builtin_bit_cast(v8h, u4v{(w.x & m) | o, (t0 & m) | o, (w.y & m) | o, (t1 & m) | o});
   hi = __builtin_bit_cast(v8h, u4v{(w.x & m4) | o, (t0 & m4) | o, (w.y & m4) | o, (t1 & m4) | o});
+}
+// T16 (16 x 16 x 32 MFMA, a whole group per instruction): one dword of 4
+// weight bytes (codes e0..e7 of a lane's 8-element slice) -> the fragment
+// [e0,e4,e2,e6 | e1,e5,e3,e7 at 16x] with the offsets taken off: n - 8 and
+// 16 (n - 8), matched by activations [x0,x4,x2,x6 | x1,x5,x3,x7 / 16].
+__device__ __forceinline__ v8h nib8_to_h_c(uint32_t w, uint32_t m, uint32_t m4, uint32_t o) {
+  typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+  const uint32_t t = w >> 8;
+  return __builtin_bit_cast(v8h, u4v{(w & m) | o, (t & m) | o, (w & m4) | o, (t & m4) | o}) +
+         v8h{-1032, -1032, -1032, -1032, -1152, -1152, -1152, -1152};
 }
 // The same fragments with the offsets taken off in the halves (packed f16
 // adds, exact): n - 8 and 16 (n - 8).
@@ -449,8 +462,8 @@ __device__ __forceinline__ void nib16_to_h_c(uint2 w, uint32_t m, uint32_t m4, u
 // PAIR: gate and up rows of the same block tile in one pass (the activation
 // fragments serve both), epilogue y = silu(sx*gate) * (sx*up) -- the
 // gate_up + silu_rows of nn/ffn.c:28-37.
-template <int BM, int BN, int S, int WGM, int NW, bool PAIR>
-__global__ __launch_bounds__(NW * 64, 8 / NW) void k_gemm_i4g_h(const uint16_t* __restrict__ xh,
+template <int BM, int BN, int S, int WGM, int NW, bool PAIR, bool T16 = false>
+__global__ __launch_bounds__(NW * 64, NW <= 8 ? 8 / NW : 1) void k_gemm_i4g_h(const uint16_t* __restrict__ xh,
                                                                 const float* __restrict__ sx,
                                                                 const uint8_t* __restrict__ q4,
                                                                 const float* __restrict__ scl,
@@ -467,7 +480,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void k_gemm_i4g_h(const uint16_t* 
   constexpr int NA = (JA + NW - 1) / NW, NB = (JB + NW - 1) / NW, NS = (JS + NW - 1) / NW;
   constexpr int NI = NA + NB + NS;
   constexpr int WGN = NW / WGM;  // waves along the tokens x along the rows
-  constexpr int TM = BM / WGM, TN = BN / WGN, FM = TM / 32, FN = TN / 32;
+  constexpr int MT = T16 ? 16 : 32;  // MFMA tile edge
+  constexpr int TM = BM / WGM, TN = BN / WGN, FM = TM / MT, FN = TN / MT;
+  constexpr int NR = T16 ? 4 : 16;   // accumulators per lane and tile
   static_assert(BN % 64 == 0 && BM % 64 == 0 && FM >= 1 && FN >= 1, "whole 1 KiB DMA rows");
   __shared__ __align__(1024) uint8_t lds[S * STAGE];
   __shared__ float s_sx[BM];
@@ -534,7 +549,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void k_gemm_i4g_h(const uint16_t* 
   asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(ko));
   const v8h c_lo = v8h{-1032, -1032, -1032, -1032, -1032, -1032, -1032, -1032};
   const v8h c_hi = v8h{-1152, -1152, -1152, -1152, -1152, -1152, -1152, -1152};
-  float acc[NP][FM][FN][16];
+  float acc[NP][FM][FN][NR];
 #pragma unroll
   for (int p = 0; p < NP; p++)
 #pragma unroll
@@ -542,17 +557,48 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void k_gemm_i4g_h(const uint16_t* 
 #pragma unroll
       for (int j = 0; j < FN; j++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) acc[p][i][j][r] = 0.f;
+        for (int r = 0; r < NR; r++) acc[p][i][j][r] = 0.f;
   // A K block's operands in registers: the activation fragments, the raw
   // nibble pairs and the scales of its 4 groups.  The next block's are read
   // from LDS while this one is unpacked and multiplied.
-  struct Frags {
+  struct Frags32 {
     v8h a[4][FM][2];
     uint2 b[4][NP][FN];
     float4 s[NP][FN];
   };
+  // T16: one 8-half activation fragment and one nibble dword per group
+  struct Frags16 {
+    v8h a[4][FM];
+    uint32_t b[4][NP][FN];
+    float4 s[NP][FN];
+  };
+  using Frags = typename std::conditional<T16, Frags16, Frags32>::type;
   auto read = [&](int kb, Frags& f) {
     const uint8_t* st = lds + (kb % S) * STAGE;
+    if constexpr (T16) {
+      const int r16 = lane & 15, q = lane >> 4;
+#pragma unroll
+      for (int p = 0; p < NP; p++)
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+          f.s[p][j] = *(const float4*)(st + SA + NP * SB + p * SS + (wn * TN + j * 16 + r16) * 16);
+#pragma unroll
+      for (int gl = 0; gl < 4; gl++) {
+#pragma unroll
+        for (int i = 0; i < FM; i++) {
+          const int row = wm * TM + i * 16 + r16;
+          f.a[gl][i] = *(const v8h*)(st + row * 256 + (((4 * gl + q) ^ (row & 15)) * 16));
+        }
+#pragma unroll
+        for (int p = 0; p < NP; p++)
+#pragma unroll
+          for (int j = 0; j < FN; j++) {
+            const int row = wn * TN + j * 16 + r16;
+            f.b[gl][p][j] = *(const uint32_t*)(st + SA + p * SB + row * 64 + ((gl ^ ((row >> 2) & 3)) * 16) + 4 * q);
+          }
+      }
+      return;
+    } else {
 #pragma unroll
     for (int p = 0; p < NP; p++)
 #pragma unroll
@@ -577,12 +623,36 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void k_gemm_i4g_h(const uint16_t* 
           f.b[gl][p][j] = *(const uint2*)(st + SA + p * SB + row * 64 + ((gl ^ ((row >> 2) & 3)) * 16) + 8 * h);
         }
     }
+    }
   };
   // PAIR takes the offsets off in the weight halves (two packed adds per
   // 4 halves, shared by the FM token tiles); the single-matrix form, with
   // one weight tile per wave, computes them on the matrix core instead
   constexpr bool OFS_MFMA = !PAIR;
   auto compute = [&](const Frags& f) {
+    if constexpr (T16) {
+#pragma unroll
+      for (int gl = 0; gl < 4; gl++) {
+        v8h fb[NP][FN];
+#pragma unroll
+        for (int p = 0; p < NP; p++)
+#pragma unroll
+          for (int j = 0; j < FN; j++) fb[p][j] = nib8_to_h_c(f.b[gl][p][j], km, km4, ko);
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+          for (int p = 0; p < NP; p++)
+#pragma unroll
+            for (int j = 0; j < FN; j++) {
+              const v4f d = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.a[gl][i], fb[p][j], v4f{}, 0, 0, 0);
+              const float4 sv = f.s[p][j];
+              const float s = gl == 0 ? sv.x : gl == 1 ? sv.y : gl == 2 ? sv.z : sv.w;
+#pragma unroll
+              for (int r = 0; r < 4; r++) acc[p][i][j][r] = __fmaf_rn(s, d[r], acc[p][i][j][r]);
+            }
+      }
+      return;
+    } else {
 #pragma unroll
     for (int gl = 0; gl < 4; gl++) {
       v8h fb[NP][FN][2];
@@ -614,6 +684,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void k_gemm_i4g_h(const uint16_t* 
           }
       }
     }
+    }
   };
   // every stage of the ring in flight, then block 0's operands to registers
 #pragma unroll
@@ -641,6 +712,25 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void k_gemm_i4g_h(const uint16_t* 
   __builtin_amdgcn_s_waitcnt(0);
   if (tid < BM) s_sx[tid] = sxr;
   __syncthreads();
+  if constexpr (T16) {
+    const int r16 = lane & 15, q = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+      const int n = nb + wn * TN + j * 16 + r16;
+      if (n >= O) continue;
+#pragma unroll
+      for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int ml = wm * TM + i * 16 + 4 * q + r;
+          if (mb + ml >= M) continue;
+          const float sv = s_sx[ml];
+          y[(int64_t)(mb + ml) * O + n] =
+              PAIR ? ref_silu_mul(sv * acc[0][i][j][r], sv * acc[NP - 1][i][j][r]) : sv * acc[0][i][j][r];
+        }
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < FN; j++) {
     const int n = nb + wn * TN + j * 32 + r32;
@@ -661,25 +751,30 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void k_gemm_i4g_h(const uint16_t* 
 // The f16-MFMA GEMM (q4b/sclb non-null: PAIR, y = silu(x.q4^T) * (x.q4b^T)).
 // Tiles from sweeps on MI355X at M = 256: 128 x 128 block tiles of 8 waves
 // when they give at least 160 workgroups (PAIR gate + up, K = 4096, N =
-// 12288: three stages 86 us, two 92, 64 x 128 93, 64 x 64 94), 64 x 64
-// tiles of 4 waves, three stages, otherwise (down, K = 12288, N = 4096:
-// 64 us; four stages 69, 128 x 128 113).
+// 12288: three stages 86 us, two 92, 64 x 128 93, 64 x 64 94; the 16 x 16
+// form 93); otherwise 64 x 64 tiles, PAIR of 4 waves in three stages, the
+// single matrix in the 16 x 16 form: 8 waves of 32 x 16, four stages (down,
+// K = 12288, N = 4096: 57 us; five or six stages 57.5 / 58, three 62; the
+// 32 x 32 form of 4 waves 66, four stages 69, 128 x 128 113).
+static bool gemm_i4g_h_big(int M, int O) { return (int64_t)((M + 127) / 128) * ((O + 127) / 128) >= 160; }
+int gemm_i4g_h_f8(int M, int O, bool pair) { return !pair && !gemm_i4g_h_big(M, O); }
+
 int launch_gemm_i4g_h(const uint16_t* xh, const float* sx, const uint8_t* q4, const float* scl, const uint8_t* q4b,
                       const float* sclb, float* y, int M, int I, int O, hipStream_t st) {
   if ((I % 128) || ((((uintptr_t)xh) | ((uintptr_t)q4) | ((uintptr_t)scl) | ((uintptr_t)q4b) | ((uintptr_t)sclb)) & 15))
     return MOTY_EUNSUP;
   if ((int64_t)M * I * 2 >= ((int64_t)1 << 32) || (int64_t)O * I / 2 >= ((int64_t)1 << 32)) return MOTY_EUNSUP;
   if (M <= 0 || O <= 0) return MOTY_OK;
-  const bool big = (int64_t)((M + 127) / 128) * ((O + 127) / 128) >= 160;
-#define Q4H(BM, BN, S, WGM, NW, P)                                                                              \
-  hipLaunchKernelGGL((k_gemm_i4g_h<BM, BN, S, WGM, NW, P>), dim3((O + BN - 1) / BN, (M + BM - 1) / BM),        \
+  const bool big = gemm_i4g_h_big(M, O);
+#define Q4H(BM, BN, S, WGM, NW, P, T16)                                                                         \
+  hipLaunchKernelGGL((k_gemm_i4g_h<BM, BN, S, WGM, NW, P, T16>), dim3((O + BN - 1) / BN, (M + BM - 1) / BM),   \
                      dim3(NW * 64), 0, st, xh, sx, q4, scl, q4b, sclb, y, M, I, O)
   if (q4b) {
-    if (big) Q4H(128, 128, 3, 2, 8, true);
-    else Q4H(64, 64, 3, 2, 4, true);
+    if (big) Q4H(128, 128, 3, 2, 8, true, false);
+    else Q4H(64, 64, 3, 2, 4, true, false);
   } else {
-    if (big) Q4H(128, 128, 2, 2, 8, false);
-    else Q4H(64, 64, 3, 2, 4, false);
+    if (big) Q4H(128, 128, 2, 2, 8, false, false);
+    else Q4H(64, 64, 4, 2, 8, false, true);
   }
 #undef Q4H
   LAUNCH_TRY("k_gemm_i4g_h");

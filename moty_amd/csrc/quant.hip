@@ -210,10 +210,11 @@ int launch_qrow_i8(const float* x, int8_t* q, float* sx, int32_t* xg, int S, int
 // multiplies against the low and the high nibbles of the same 8 weight
 // bytes: [c0, c4, c2, c6, c8, c12, c10, c14] and [c1, c5, c3, c7, c9, c13,
 // c11, c15] / 16 (a k-permutation shared by both operands; the division by
-// 16 is exact and matches the high nibbles' 16x weight halves).  One
-// workgroup per row, the row held in registers: NU runs per thread (run
-// t + NT*j).
-template <int NT, int NU>
+// 16 is exact and matches the high nibbles' 16x weight halves).  F8: the
+// fragments of the 16 x 16 x 32 form, per 8 codes: [c0, c4, c2, c6, c1, c5,
+// c3, c7] with the last four / 16.  One workgroup per row, the row held in
+// registers: NU runs per thread (run t + NT*j).
+template <int NT, int NU, bool F8>
 __global__ __launch_bounds__(NT) void k_qrow_f16p(const float* __restrict__ x, uint16_t* __restrict__ xh,
                                                   float* __restrict__ sx, int I) {
   __shared__ float red[NT / MOTY_WAVE];
@@ -250,28 +251,36 @@ __global__ __launch_bounds__(NT) void k_qrow_f16p(const float* __restrict__ x, u
       c[4 * q + 2] = (float)rne_int(v[j][q].z * inv);
       c[4 * q + 3] = (float)rne_int(v[j][q].w * inv);
     }
-    const uint4 lo = uint4{hb(c[0]) | (hb(c[4]) << 16), hb(c[2]) | (hb(c[6]) << 16), hb(c[8]) | (hb(c[12]) << 16),
-                           hb(c[10]) | (hb(c[14]) << 16)};
     const float k = 0.0625f;
-    const uint4 hi = uint4{hb(c[1] * k) | (hb(c[5] * k) << 16), hb(c[3] * k) | (hb(c[7] * k) << 16),
-                           hb(c[9] * k) | (hb(c[13] * k) << 16), hb(c[11] * k) | (hb(c[15] * k) << 16)};
+    uint4 lo, hi;
+    if (F8) {
+      lo = uint4{hb(c[0]) | (hb(c[4]) << 16), hb(c[2]) | (hb(c[6]) << 16), hb(c[1] * k) | (hb(c[5] * k) << 16),
+                 hb(c[3] * k) | (hb(c[7] * k) << 16)};
+      hi = uint4{hb(c[8]) | (hb(c[12]) << 16), hb(c[10]) | (hb(c[14]) << 16), hb(c[9] * k) | (hb(c[13] * k) << 16),
+                 hb(c[11] * k) | (hb(c[15] * k) << 16)};
+    } else {
+      lo = uint4{hb(c[0]) | (hb(c[4]) << 16), hb(c[2]) | (hb(c[6]) << 16), hb(c[8]) | (hb(c[12]) << 16),
+                 hb(c[10]) | (hb(c[14]) << 16)};
+      hi = uint4{hb(c[1] * k) | (hb(c[5] * k) << 16), hb(c[3] * k) | (hb(c[7] * k) << 16),
+                 hb(c[9] * k) | (hb(c[13] * k) << 16), hb(c[11] * k) | (hb(c[15] * k) << 16)};
+    }
     *(uint4*)(xh + row * I + 16 * r) = lo;
     *(uint4*)(xh + row * I + 16 * r + 8) = hi;
   }
 }
 
-int launch_qrow_f16p(const float* x, uint16_t* xh, float* sx, int S, int I, hipStream_t st) {
+int launch_qrow_f16p(const float* x, uint16_t* xh, float* sx, int S, int I, int f8, hipStream_t st) {
   if (S <= 0) return MOTY_OK;
   if ((I % 16) || (((uintptr_t)x) & 15) || (((uintptr_t)xh) & 15)) return MOTY_EUNSUP;
   const int runs = (I / 16 + 255) / 256;
-  if (runs <= 1)
-    hipLaunchKernelGGL((k_qrow_f16p<256, 1>), dim3(S), dim3(256), 0, st, x, xh, sx, I);
-  else if (runs <= 2)
-    hipLaunchKernelGGL((k_qrow_f16p<256, 2>), dim3(S), dim3(256), 0, st, x, xh, sx, I);
-  else if (runs <= 4)
-    hipLaunchKernelGGL((k_qrow_f16p<256, 4>), dim3(S), dim3(256), 0, st, x, xh, sx, I);
-  else
-    return MOTY_EUNSUP;
+#define QF(NU)                                                                                          \
+  if (f8) hipLaunchKernelGGL((k_qrow_f16p<256, NU, true>), dim3(S), dim3(256), 0, st, x, xh, sx, I); \
+  else hipLaunchKernelGGL((k_qrow_f16p<256, NU, false>), dim3(S), dim3(256), 0, st, x, xh, sx, I)
+  if (runs <= 1) QF(1);
+  else if (runs <= 2) QF(2);
+  else if (runs <= 4) QF(4);
+  else return MOTY_EUNSUP;
+#undef QF
   LAUNCH_TRY("k_qrow_f16p");
   return MOTY_OK;
 }
