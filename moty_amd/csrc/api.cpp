@@ -697,7 +697,11 @@ static int r4_ffn(bool q8, const char* what, float* out, const float* x, int S, 
   int8_t* xq = (int8_t*)((char*)sp + bh + bgu);
   float* xs = (float*)((char*)sp + bh + bgu + bq);
   int32_t* xm = (int32_t*)((char*)sp + bh + bgu + bq + bs);
-  rc = S == 1 ? launch_r4_gate_up_silu(q8, x, gu, gs16, h, D, I, st) : MOTY_EUNSUP;
+  // S = 1: the decode GEMV with its SiLU epilogue; S > 3: one GEMM pass over
+  // gate and up tiles with the SiLU epilogue; else the GEMV then silu_rows
+  rc = S == 1 ? launch_r4_gate_up_silu(q8, x, gu, gs16, h, D, I, st)
+       : S > 3 ? launch_r4_gate_up_gemm(q8, x, gu, gs16, h, S, D, I, xq, xs, xm, st)
+               : MOTY_EUNSUP;
   if (rc == MOTY_EUNSUP) {
     if ((rc = launch_r4_matmul(q8, x, gu, gs16, g2, S, D, 2 * I, xq, xs, xm, st))) return rc;
     rc = launch_silu_rows(h, g2, S, I, st);

@@ -55,6 +55,9 @@ int launch_i4g_f32(const float* x, const uint8_t* q4, const float* scl, float* y
 int launch_quant_g32(const float* x, int8_t* xq, float* xs, int32_t* xm, int S, int I, hipStream_t st);
 int launch_r4_matmul(bool q8, const float* x, const uint8_t* W, const uint16_t* d16, float* y, int S, int I, int O,
                      int8_t* xq, float* xs, int32_t* xm, hipStream_t st);
+// the same for S > 3 (GEMM, xq/xs/xm: activation scratch for S*D codes)
+int launch_r4_gate_up_gemm(bool q8, const float* x, const uint8_t* W, const uint16_t* d16, float* h, int S, int D,
+                           int I, int8_t* xq, float* xs, int32_t* xm, hipStream_t st);
 int launch_r4_gate_up_silu(bool q8, const float* x, const uint8_t* W, const uint16_t* d16, float* h, int D, int I,
                            hipStream_t st);
 int launch_pack_r4(bool q8, const float* w, uint8_t* q, uint16_t* d16, int O, int I, hipStream_t st);

@@ -398,7 +398,12 @@ constexpr int R4M_NT = 256;
 constexpr int R4M_KG = 4;                 // groups per K block
 constexpr int R4M_AS = R4M_KG * 32 + 16;  // A row stride (bytes)
 
-template <bool Q8, bool TILE = false, int WV = 4>
+// PAIR (WV = 4): W is a row-fused [gate; up] matrix of 2*O rows; the tile's
+// first 32 weight rows are gate rows 32*bx + [0, 32), the last 32 the up rows
+// O + 32*bx + [0, 32), and the epilogue writes y [S][O] = silu(gate) * up
+// (the gate_up + silu_rows of nn/ffn.c:28-37; the up waves hand their sums
+// over through LDS).
+template <bool Q8, bool TILE = false, int WV = 4, bool PAIR = false>
 __global__ __launch_bounds__(64 * WV, WV <= 8 ? 8 / WV : 1) void k_r4_gemm(const int8_t* __restrict__ xq, const float* __restrict__ xs,
                                                        const int32_t* __restrict__ xm,
                                                        const uint8_t* __restrict__ W,
@@ -410,6 +415,7 @@ __global__ __launch_bounds__(64 * WV, WV <= 8 ? 8 / WV : 1) void k_r4_gemm(const
   constexpr int NBC = Q8 ? 2 : 1;           // B chunks per thread
   constexpr int NWN = WV / 4, JN = 4 / NWN;  // WV >= 8: waves along the rows, 16-row tiles per wave
   static_assert(WV == 4 || WV == 8 || WV == 16, "waves");
+  static_assert(!PAIR || WV == 4, "PAIR runs the 32 x 32 waves");
   __shared__ __align__(16) int8_t sA[64 * R4M_AS];
   __shared__ __align__(16) uint8_t sB[64 * BS];
   __shared__ float sD[64 * R4M_KG];         // [row][group]
@@ -418,9 +424,9 @@ __global__ __launch_bounds__(64 * WV, WV <= 8 ? 8 / WV : 1) void k_r4_gemm(const
   const int tid = threadIdx.x, lane = tid % MOTY_WAVE, wv = tid / MOTY_WAVE;
   const int wm = wv >> 1, wn = wv & 1;
   const int r32 = lane & 31, hk = lane >> 5;
-  const int mb = blockIdx.y * 64, nb0 = blockIdx.x * 64;
+  const int mb = blockIdx.y * 64, nb0 = blockIdx.x * (PAIR ? 32 : 64);
   const int nb = I / 32, S4 = S / 4 * 4;
-  const int O4 = (O + 3) / 4;
+  const int O4 = ((PAIR ? 2 * O : O) + 3) / 4;
 
   // copy assignments
   const int8_t* srcA[2];
@@ -432,7 +438,8 @@ __global__ __launch_bounds__(64 * WV, WV <= 8 ? 8 / WV : 1) void k_r4_gemm(const
     srcA[i] = xq + (int64_t)m * I + (q & 7) * 16;
   }
   // B: thread -> (row tid/4, group tid%4), Q8R4 two 16-byte halves
-  int orow = nb0 + (tid >> 2);
+  const int trow = tid >> 2;
+  int orow = !PAIR ? nb0 + trow : trow < 32 ? nb0 + trow : O + nb0 + trow - 32;
   int ob = orow / 4;
   ob = ob < O4 ? ob : O4 - 1;
   const uint8_t* srcB = W + (size_t)ob * nb * GB + (size_t)(orow & 3) * RB;
@@ -616,6 +623,24 @@ __global__ __launch_bounds__(64 * WV, WV <= 8 ? 8 / WV : 1) void k_r4_gemm(const
     }
     return;
   }
+  if constexpr (PAIR) {
+    // up sums (wn = 1) to the gate waves through LDS, [r][wm][lane]
+    float* xch = (float*)sA;
+    __syncthreads();
+    if (wn == 1) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) xch[r * 128 + wm * 64 + lane] = accf[r];
+    }
+    __syncthreads();
+    const int col = nb0 + r32;
+    if (wn == 1 || col >= O) return;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int t = mb + wm * 32 + 8 * (r >> 2) + 4 * hk + (r & 3);
+      if (t < S) y[(int64_t)t * O + col] = ref_silu_mul(accf[r], xch[r * 128 + wm * 64 + lane]);
+    }
+    return;
+  }
   const int col = nb0 + wn * 32 + r32;
   if (col >= O) return;
 #pragma unroll
@@ -659,6 +684,24 @@ int launch_r4_matmul(bool q8, const float* x, const uint8_t* W, const uint16_t* 
   }
 #undef R4G
   LAUNCH_TRY("k_r4_gemm");
+  return MOTY_OK;
+}
+
+// gate/up + SiLU over a row-fused [gate; up] R4 matrix (2*I rows) for S > 3
+// tokens: h [S][I] = silu(x.gate^T) * (x.up^T) in one GEMM pass (PAIR tiles)
+int launch_r4_gate_up_gemm(bool q8, const float* x, const uint8_t* W, const uint16_t* d16, float* h, int S, int D,
+                           int I, int8_t* xq, float* xs, int32_t* xm, hipStream_t st) {
+  if (D % 32 || D <= 0 || I % 4 || I <= 0) return MOTY_EUNSUP;
+  if (S <= 0) return MOTY_OK;
+  int rc = launch_quant_g32(x, xq, xs, xm, S, D, st);
+  if (rc) return rc;
+  dim3 grid((I + 31) / 32, (S + 63) / 64);
+#define R4P(Q, T) hipLaunchKernelGGL((k_r4_gemm<Q, T, 4, true>), grid, dim3(R4M_NT), 0, st, xq, xs, xm, W, d16, h, S, D, I)
+  if (q8) R4P(true, false);
+  else if (S % 4 == 0) R4P(false, true);
+  else R4P(false, false);
+#undef R4P
+  LAUNCH_TRY("k_r4_gemm<pair>");
   return MOTY_OK;
 }
 

@@ -154,7 +154,8 @@ def test_gate_up_silu_r4(ops, q8, D, I):
 
 
 @pytest.mark.parametrize("q8", [False, True])
-@pytest.mark.parametrize("S,D,I", [(1, 1024, 3072), (2, 256, 512), (5, 512, 256), (33, 256, 1024), (1, 4096, 1024)])
+@pytest.mark.parametrize("S,D,I", [(1, 1024, 3072), (2, 256, 512), (5, 512, 256), (33, 256, 1024), (1, 4096, 1024),
+                                   (68, 256, 1056), (7, 512, 160), (3, 256, 96)])
 def test_dense_ffn_r4(ops, q8, S, D, I):
     # moty_nn_dense_ffn with the fused gate_up (nn/ffn.c:26-41)
     say("dense_ffn_r4", q8, S, D, I)
