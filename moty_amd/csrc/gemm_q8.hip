@@ -307,13 +307,18 @@ int launch_gemm_q8(const int8_t* xq, const float* sx, const int8_t* W, const flo
     // not by the grid's width.  Four groups of 2 waves (three stages) where
     // K holds at least 4 blocks: 6.3 / 7.3 us against 6.9 / 8.5 with two,
     // timed back to back on rotating weights (inside the C2 layer step, after
-    // the wide GEMM, both forms average 8.0 us).
+    // the wide GEMM, both forms average 8.0 us).  Grids of at least 512
+    // tiles of 64 x 128 with K <= 1024 (C2's fused N = 10240): those tiles,
+    // 8 waves, two stages, 13.3 us against 15.0 (median 14.2 against 16.8)
+    // for 64 x 64 in three; 128 x 64 13.5, 128 x 128 13.8-14.1, three stages
+    // of 64 x 128 16.2.
 #define QD(BM, BN, S, WM, WN, KS)                                                                             \
   hipLaunchKernelGGL((k_gemm_q8_dma<BM, BN, S, WM, WN, KS>), dim3((O + BN - 1) / BN, (M + BM - 1) / BM),       \
                      dim3(64 * WM * WN * KS), 0, st, xq, sx, W, scale, y, M, K, O)
     const bool narrow = (int64_t)((M + 63) / 64) * ((O + 63) / 64) < 256;
     if (narrow && K >= 4 * GM_KB) QD(64, 32, 3, 2, 1, 4);
     else if (narrow && K >= 2 * GM_KB) QD(64, 32, 4, 2, 1, 2);
+    else if (K <= 1024 && (int64_t)((M + 63) / 64) * ((O + 127) / 128) >= 512) QD(64, 128, 2, 2, 4, 1);
     else if (K <= 1024) QD(64, 64, 3, 2, 2, 1);
     else QD(64, 64, 4, 2, 2, 1);
 #undef QD
