@@ -139,7 +139,7 @@ __global__ __launch_bounds__(GM_NT, 2) void k_gemm_q8(const int8_t* __restrict__
 #pragma unroll
       for (int r = 0; r < 16; r++) {
         const int ml = wm * 32 * WM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (mb + ml < M) y[(int64_t)(mb + ml) * O + n] = (scn[j] * s_sx[ml]) * (float)acc[i][j][r];
+        if (mb + ml < M) __builtin_nontemporal_store((scn[j] * s_sx[ml]) * (float)acc[i][j][r], y + (int64_t)(mb + ml) * O + n);
       }
   }
 }
@@ -285,7 +285,7 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_gemm_q8_dma(const int8_
 #pragma unroll
       for (int r = 0; r < 16; r++) {
         const int ml = wm * TM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (mb + ml < M) y[(int64_t)(mb + ml) * O + n] = (scn[j] * s_sx[ml]) * (float)acc[i][j][r];
+        if (mb + ml < M) __builtin_nontemporal_store((scn[j] * s_sx[ml]) * (float)acc[i][j][r], y + (int64_t)(mb + ml) * O + n);
       }
   }
 }
@@ -311,7 +311,9 @@ int launch_gemm_q8(const int8_t* xq, const float* sx, const int8_t* W, const flo
     // tiles of 64 x 128 with K <= 1024 (C2's fused N = 10240): those tiles,
     // 8 waves, two stages, 13.3 us against 15.0 (median 14.2 against 16.8)
     // for 64 x 64 in three; 128 x 64 13.5, 128 x 128 13.8-14.1, three stages
-    // of 64 x 128 16.2.
+    // of 64 x 128 16.2.  Both GEMMs write y with nontemporal stores: the
+    // output (21 MB for C2's fused GEMM) then does not sit dirty in L2 to be
+    // evicted under the next kernels' reads (C2 step 42.7 -> 40.8 us).
 #define QD(BM, BN, S, WM, WN, KS)                                                                             \
   hipLaunchKernelGGL((k_gemm_q8_dma<BM, BN, S, WM, WN, KS>), dim3((O + BN - 1) / BN, (M + BM - 1) / BM),       \
                      dim3(64 * WM * WN * KS), 0, st, xq, sx, W, scale, y, M, K, O)
