@@ -752,11 +752,17 @@ __global__ __launch_bounds__(NW * 64, NW <= 8 ? 8 / NW : 1) void k_gemm_i4g_h(co
 // Tiles from sweeps on MI355X at M = 256: 128 x 128 block tiles of 8 waves
 // when they give at least 160 workgroups (PAIR gate + up, K = 4096, N =
 // 12288: three stages 86 us, two 92, 64 x 128 93, 64 x 64 94; the 16 x 16
-// form 93); otherwise 64 x 64 tiles, PAIR of 4 waves in three stages, the
+// form 93) -- except PAIR, where 64 x 192 tiles of 12 waves (32 x 32 each,
+// two stages) take over while 128 x 128 ones would leave CUs idle and they
+// number at least 192 (the same GEMM: 256 workgroups on 256 CUs against 192,
+// 81 us against 86-91 alone, 88.0 against 92.6 inside the FFN under
+// rocprofv3; three stages 84, the 16 x 16 form 87-95); otherwise 64 x 64 tiles, PAIR of 4 waves in three stages, the
 // single matrix in the 16 x 16 form: 8 waves of 32 x 16, four stages (down,
 // K = 12288, N = 4096: 57 us; five or six stages 57.5 / 58, three 62; the
 // 32 x 32 form of 4 waves 66, four stages 69, 128 x 128 113).
 static bool gemm_i4g_h_big(int M, int O) { return (int64_t)((M + 127) / 128) * ((O + 127) / 128) >= 160; }
+// 128 x 128 tiles give every CU a workgroup
+static bool gemm_i4g_h_full(int M, int O) { return (int64_t)((M + 127) / 128) * ((O + 127) / 128) >= 256; }
 int gemm_i4g_h_f8(int M, int O, bool pair) { return !pair && !gemm_i4g_h_big(M, O); }
 
 int launch_gemm_i4g_h(const uint16_t* xh, const float* sx, const uint8_t* q4, const float* scl, const uint8_t* q4b,
@@ -769,8 +775,10 @@ int launch_gemm_i4g_h(const uint16_t* xh, const float* sx, const uint8_t* q4, co
 #define Q4H(BM, BN, S, WGM, NW, P, T16)                                                                         \
   hipLaunchKernelGGL((k_gemm_i4g_h<BM, BN, S, WGM, NW, P, T16>), dim3((O + BN - 1) / BN, (M + BM - 1) / BM),   \
                      dim3(NW * 64), 0, st, xh, sx, q4, scl, q4b, sclb, y, M, I, O)
+  const bool pair192 = !gemm_i4g_h_full(M, O) && (int64_t)((M + 63) / 64) * ((O + 191) / 192) >= 192;
   if (q4b) {
-    if (big) Q4H(128, 128, 3, 2, 8, true, false);
+    if (pair192) Q4H(64, 192, 2, 2, 12, true, false);
+    else if (big) Q4H(128, 128, 3, 2, 8, true, false);
     else Q4H(64, 64, 3, 2, 4, true, false);
   } else {
     if (big) Q4H(128, 128, 2, 2, 8, false, false);

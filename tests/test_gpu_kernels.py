@@ -206,7 +206,9 @@ def test_silu_and_softmax(ops):
 
 @pytest.mark.parametrize("idot4", [True, False])
 @pytest.mark.parametrize("S,D,I", [(37, 256, 384), (5, 128, 128), (4, 256, 128), (1, 128, 64), (130, 1024, 640),
-                                   (70, 192, 320), (3, 4096, 96), (300, 512, 1280)])
+                                   (70, 192, 320), (3, 4096, 96), (300, 512, 1280),
+                                   # 64 x 192 gate/up tiles, ragged in tokens and rows
+                                   (130, 256, 12416)])
 def test_dense_ffn_i4g(ops, idot4, S, D, I):
     # nn/ffn.c:26-55 over grouped-int4 Mats: the fused gate/up f16 pass
     # (S > 4, D and I multiples of 128), the int8 GEMM fallback (other
