@@ -159,8 +159,11 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
         // clamped (unused past ng): unconditional loads keep the wave's
         // loads in one straight run, with no wait at branch joins
         const int g = c * 64 + lane < ng ? c * 64 + lane : 0;
-        wb[m][r][c] = *(const int4*)((m ? q4b : q4) + o * rb + g * 16);
-        wsc[m][r][c] = ((m ? sclb : scl) + o * ng)[g];
+        {
+          const v4i t = __builtin_nontemporal_load((const v4i*)((m ? q4b : q4) + o * rb + g * 16));
+          wb[m][r][c] = int4{t.x, t.y, t.z, t.w};
+        }
+        wsc[m][r][c] = __builtin_nontemporal_load((m ? sclb : scl) + o * ng + g);
       }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll

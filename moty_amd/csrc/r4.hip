@@ -174,9 +174,12 @@ __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, con
     for (int m = 0; m < NM; m++) {
       const int ci = lane + 64 * (k * KS + part);
       const int cc = ci < nchunk ? ci : 0;
-      wc[m][k] = *(const int4*)(W + ((size_t)(blk + m * O4) * nb * GB + (size_t)cc * 16));
+      {
+        const v4i t = __builtin_nontemporal_load((const v4i*)(W + ((size_t)(blk + m * O4) * nb * GB + (size_t)cc * 16)));
+        wc[m][k] = int4{t.x, t.y, t.z, t.w};
+      }
       // chunk ci: group ci/4, row ci%4 (Q8R4: group ci/8, row (ci/2)%4)
-      dc[m][k] = d16[(size_t)(blk + m * O4) * nb * 4 + (Q8 ? (cc >> 3) * 4 + ((cc >> 1) & 3) : cc)];
+      dc[m][k] = __builtin_nontemporal_load(d16 + (size_t)(blk + m * O4) * nb * 4 + (Q8 ? (cc >> 3) * 4 + ((cc >> 1) & 3) : cc));
     }
   };
   MOTY_WAIT_VMCNT(0);
