@@ -111,7 +111,10 @@ __device__ __forceinline__ float4 gg_decode4(const uint8_t* p, int pos) {
   return make_float4(v[0], v[1], v[2], v[3]);
 }
 
-// One workgroup per NBW blocks (8192 elements): stage, then float4 stores.
+// One workgroup per NBW blocks (8192 elements): stage, then float4 stores,
+// nontemporal: the f32 output (four times the input bytes or more) is not
+// read again by this kernel and would only crowd L2 (12288 x 4096 Q8_0:
+// 48.2 -> 41.3 us, Q4_K 45 -> 35).
 template <int DT, bool ALIGNED>
 __global__ __launch_bounds__(GG_TPB) void k_gguf_dequant(const uint8_t* __restrict__ raw, float* __restrict__ out,
                                                          int64_t nblk) {
@@ -125,7 +128,9 @@ __global__ __launch_bounds__(GG_TPB) void k_gguf_dequant(const uint8_t* __restri
   const int n4 = nb * (F::E / 4);
   for (int f = threadIdx.x; f < n4; f += GG_TPB) {
     const int e = 4 * f, b = e / F::E;
-    o[f] = gg_decode4<DT>(lds + b * F::B, e - b * F::E);
+    const float4 v = gg_decode4<DT>(lds + b * F::B, e - b * F::E);
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    __builtin_nontemporal_store(f4v{v.x, v.y, v.z, v.w}, reinterpret_cast<f4v*>(o + f));
   }
 }
 
