@@ -670,7 +670,9 @@ __global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ y
       // unconditional loads (clamped slot; skipped pairs are not used): a
       // branch around each load would serialize their latencies
       const int sl = (j0 + u < K) ? slot_s[j0 + u] : -1;
-      v[u] = *(const float4*)(y + (int64_t)(sl >= 0 ? sl : 0) * D + d);
+      // nontemporal: every row is read once (C5: 70 MB; 220 -> 216 us per layer)
+      const v4f t = __builtin_nontemporal_load((const v4f*)(y + (int64_t)(sl >= 0 ? sl : 0) * D + d));
+      v[u] = float4{t.x, t.y, t.z, t.w};
     }
 #pragma unroll
     for (int u = 0; u < 8; u++) {
