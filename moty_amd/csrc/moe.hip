@@ -471,9 +471,12 @@ constexpr int MG_KB = 128;   // K bytes per stage
 constexpr int MG_LS = 144;   // padded LDS row stride
 
 __device__ __forceinline__ int4 ldg16(const int8_t* p) { return *(const int4*)p; }
-// expert weights: read once per M-tile, streamed past the caches so that the
-// activation rows every N-tile shares stay in L2 (C4 121-124 -> 118-120 us,
-// C5 220 -> 217-218 per layer)
+// expert weights, streamed past the caches in the 64-slot form (experts
+// averaging at most 48 slots: one M-tile each, the weights read once), so
+// that the activation rows every N-tile shares stay in L2: C4 122-125 ->
+// 118-120 us per layer.  The 128-slot form keeps them cacheable: at C5 the
+// streamed form was no faster uniform and 13 us slower skewed (hot experts
+// span several M-tiles that share each weight tile).
 __device__ __forceinline__ int4 ldg16_nt(const int8_t* p) {
   const v4i t = __builtin_nontemporal_load((const v4i*)p);
   return int4{t.x, t.y, t.z, t.w};
@@ -563,7 +566,7 @@ __global__ __launch_bounds__(MOTY_WAVE * MT * NW) void k_moe_gemm(
 #pragma unroll
     for (int i = 0; i < NA; i++) ra[i] = ldg16(srcA[i] + off);
 #pragma unroll
-    for (int i = 0; i < NBW; i++) rb[i] = ldg16_nt(srcB[i] + off);
+    for (int i = 0; i < NBW; i++) rb[i] = MT == 1 ? ldg16_nt(srcB[i] + off) : ldg16(srcB[i] + off);
     // keep each set's loads together and in issue order
     __builtin_amdgcn_sched_barrier(0);
   };
