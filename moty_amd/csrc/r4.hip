@@ -583,7 +583,11 @@ __global__ __launch_bounds__(64 * WV, WV <= 8 ? 8 / WV : 1) void k_r4_gemm(const
         if (gg >= ngk) break;  // wave-uniform
         const v4i a = *(const v4i*)(sA + (wm * 32 + r32) * R4M_AS + gg * 32 + hk * 16);
         const int4 w = *(const int4*)(sB + (wn * 32 + r32) * BS + gg * RB);
-        const int4 u = hk ? r4_hi(w) : r4_lo(w);
+        // this half's nibbles (low for hk = 0, high for hk = 1): one shift
+        // and one mask per word in every lane, no divergent branch
+        const int sh = 4 * hk;
+        const int4 u = int4{(w.x >> sh) & 0x0f0f0f0f, (w.y >> sh) & 0x0f0f0f0f, (w.z >> sh) & 0x0f0f0f0f,
+                            (w.w >> sh) & 0x0f0f0f0f};
         v16i dsum = {};
         dsum = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, v4i{u.x, u.y, u.z, u.w}, dsum, 0, 0, 0);
         const float dd = sD[(wn * 32 + r32) * R4M_KG + gg];
