@@ -16,8 +16,8 @@
 //                  workgroup)
 //   k_route_topk   wave per token: softmax and greedy top-k; another wave:
 //                  the token's int8 row (qrow_i8)
-//   k_group        one workgroup: per-expert histogram, exclusive scan, slot
-//                  scatter (pairs grouped by expert), M-tile list
+//   k_group        per-expert histogram, exclusive scan, slot scatter (pairs
+//                  grouped by expert; each workgroup places one chunk), M-tiles
 //   k_moe_gemm<true>   grouped GEMM, v_mfma_i32_32x32x32_i8, gate and up
 //                  rows of one expert per workgroup, epilogue silu(g)*u -> h
 //                  (f32)
@@ -370,38 +370,57 @@ __global__ __launch_bounds__(TK_TOK * 128) void k_route_topk(const float* __rest
 
 // ---------------------------------------------------------------------------
 constexpr int GR_NT = 1024;
-constexpr int GR_PT = 16;  // pair ids held in registers per thread (P <= 16384)
+constexpr int GR_CHUNK = 256;  // pairs placed per workgroup (at most 32 workgroups)
+constexpr int GR_U = 8;        // expert ids loaded ahead in the counting pass
 
-// Single workgroup.  offs[E+1]: expert segment starts; slot_tok[P]: token of
-// each slot; pair_slot[P]: slot of pair (t,k); tiles[]: (expert, m0) M-tiles
-// of bm slots; ntiles[0]: their count.  Expert ids are read once into
-// registers (the rest of a larger P is read again for the scatter).
-__global__ __launch_bounds__(GR_NT) void k_group(const int* __restrict__ idx, int P, int K, int E, int bm,
+// Grouping over G workgroups, with no hand-off between them: every
+// workgroup counts all P expert ids (the histogram, and the part of it from
+// pairs before its own chunk), scans the counts itself and places only its
+// chunk's pairs, at offs[e] + (pairs of e in earlier chunks) + its rank
+// among its chunk's pairs of e.  offs[E+1]: expert segment starts;
+// slot_tok[P]: token of each slot; pair_slot[P]: slot of pair (t,k);
+// tiles[]: (expert, m0) M-tiles of bm slots; ntiles[0]: their count (these
+// three and counts_out from workgroup 0).  Within an expert's segment the
+// slot order is free: every GEMM row is computed on its own and the combine
+// finds each pair through pair_slot.
+__global__ __launch_bounds__(GR_NT) void k_group(const int* __restrict__ idx, int P, int K, int E, int bm, int chunk,
                                                  int* __restrict__ offs, int* __restrict__ slot_tok,
                                                  int* __restrict__ pair_slot, int2* __restrict__ tiles,
                                                  int* __restrict__ ntiles, int* __restrict__ counts_out) {
-  __shared__ int cnt[256], cur[256], tstart[257];
+  __shared__ int cnt[256], pre[256], cur[256], base[256], tstart[257];
   const int tid = threadIdx.x;
-  int ev[GR_PT];
-#pragma unroll
-  for (int i = 0; i < GR_PT; i++) {
-    const int p = tid + i * GR_NT;
-    ev[i] = p < P ? idx[p] : -1;
+  const int c0 = blockIdx.x * chunk, c1 = c0 + chunk < P ? c0 + chunk : P;
+  // this thread's first pair of the chunk, loaded with the counting pass's
+  // ids rather than after the scan
+  const int eo = c0 + tid < c1 ? idx[c0 + tid] : -1;
+  if (tid < E) {
+    cnt[tid] = 0;
+    pre[tid] = 0;
+    cur[tid] = 0;
   }
-  if (tid < E) cnt[tid] = 0;
   __syncthreads();
+  for (int p0 = 0; p0 < P; p0 += GR_U * GR_NT) {
+    int ev[GR_U];
 #pragma unroll
-  for (int i = 0; i < GR_PT; i++)
-    if (ev[i] >= 0 && ev[i] < E) atomicAdd(&cnt[ev[i]], 1);
-  for (int p = tid + GR_PT * GR_NT; p < P; p += GR_NT) {
-    const int e = idx[p];
-    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+    for (int u = 0; u < GR_U; u++) {
+      const int p = p0 + u * GR_NT + tid;
+      ev[u] = p < P ? idx[p] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < GR_U; u++) {
+      const int p = p0 + u * GR_NT + tid;
+      if (ev[u] >= 0 && ev[u] < E) {
+        atomicAdd(&cnt[ev[u]], 1);
+        if (p < c0) atomicAdd(&pre[ev[u]], 1);
+      }
+    }
   }
   __syncthreads();
   if (tid < MOTY_WAVE) {
     // exclusive scans of the counts and of the M-tile counts by one wave:
     // lane l owns experts 4l..4l+3 (E <= 256)
     const int l = tid;
+    const bool w0 = blockIdx.x == 0;
     int c[4], t[4], so = 0, st = 0;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -416,38 +435,39 @@ __global__ __launch_bounds__(GR_NT) void k_group(const int* __restrict__ idx, in
     for (int j = 0; j < 4; j++) {
       const int e = 4 * l + j;
       if (e < E) {
-        cur[e] = o;
-        offs[e] = o;
+        base[e] = o + pre[e];
         tstart[e] = tl;
-        if (counts_out) counts_out[e] = c[j];
+        if (w0) {
+          offs[e] = o;
+          if (counts_out) counts_out[e] = c[j];
+        }
       }
       o += c[j];
       tl += t[j];
     }
     if (l == MOTY_WAVE - 1) {
-      offs[E] = o;
       tstart[E] = tl;
-      ntiles[0] = tl;
+      if (w0) {
+        offs[E] = o;
+        ntiles[0] = tl;
+      }
     }
   }
   __syncthreads();
-  if (tid < E) {
+  if (blockIdx.x == 0 && tid < E) {
     const int nt = tstart[tid + 1] - tstart[tid];
     for (int j = 0; j < nt; j++) tiles[tstart[tid] + j] = int2{tid, j * bm};
   }
-  auto place = [&](int p, int e) {
+  for (int p = c0 + tid; p < c1; p += GR_NT) {
+    const int e = p == c0 + tid ? eo : idx[p];
     if (e < 0 || e >= E) {
       pair_slot[p] = -1;
-      return;
+      continue;
     }
-    const int s = atomicAdd(&cur[e], 1);
+    const int s = base[e] + atomicAdd(&cur[e], 1);
     slot_tok[s] = p / K;
     pair_slot[p] = s;
-  };
-#pragma unroll
-  for (int i = 0; i < GR_PT; i++)
-    if (tid + i * GR_NT < P) place(tid + i * GR_NT, ev[i]);
-  for (int p = tid + GR_PT * GR_NT; p < P; p += GR_NT) place(p, idx[p]);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -778,8 +798,12 @@ int launch_moe_route(const MoeArgs& a, void* scratch, hipStream_t st) {
                      K, a.norm, m.idx, m.w, m.xq, m.sx, a.probs_out);
   LAUNCH_TRY("k_route_topk");
   const int mt = moe_mt(a);
-  hipLaunchKernelGGL(k_group, dim3(1), dim3(GR_NT), 0, st, m.idx, P, K, E, 64 * mt, m.offs,
-                     m.slot_tok, m.pair_slot, m.tiles, m.ntiles, m.counts);
+  {
+    const int g = P <= GR_CHUNK ? 1 : (P + GR_CHUNK - 1) / GR_CHUNK < 32 ? (P + GR_CHUNK - 1) / GR_CHUNK : 32;
+    const int chunk = (P + g - 1) / g;
+    hipLaunchKernelGGL(k_group, dim3(g), dim3(GR_NT), 0, st, m.idx, P, K, E, 64 * mt, chunk, m.offs, m.slot_tok,
+                       m.pair_slot, m.tiles, m.ntiles, m.counts);
+  }
   LAUNCH_TRY("k_group");
   return MOTY_OK;
 }
