@@ -755,11 +755,14 @@ __global__ __launch_bounds__(NW * 64, NW <= 8 ? 8 / NW : 1) void k_gemm_i4g_h(co
 // Tiles from sweeps on MI355X at M = 256: 128 x 128 block tiles of 8 waves
 // when they give at least 160 workgroups (PAIR gate + up, K = 4096, N =
 // 12288: three stages 86 us, two 92, 64 x 128 93, 64 x 64 94; the 16 x 16
-// form 93) -- except PAIR, where 64 x 192 tiles of 12 waves (32 x 32 each,
-// two stages) take over while 128 x 128 ones would leave CUs idle and they
-// number at least 192 (the same GEMM: 256 workgroups on 256 CUs against 192,
-// 81 us against 86-91 alone, 88.0 against 92.6 inside the FFN under
-// rocprofv3; three stages 84, the 16 x 16 form 87-95); otherwise 64 x 64 tiles, PAIR of 4 waves in three stages, the
+// form 93) -- except PAIR, where 64 x 192 tiles take over while 128 x 128
+// ones would leave CUs idle and they number at least 192 (the same GEMM:
+// 256 workgroups on 256 CUs against 192, 81 us against 86-91 alone; three
+// stages 84, the 16 x 16 form 87-95).  Their 6 waves each take all 64 tokens
+// of 32 gate and 32 up rows, so each unpacked weight fragment serves two
+// token tiles: 78-80 us against 80-84 for 12 waves of 32 tokens (the FFN
+// 157.0 against 159.6 us), though 6 waves leave two SIMDs a wave short;
+// otherwise 64 x 64 tiles, PAIR of 4 waves in three stages, the
 // single matrix in the 16 x 16 form: 8 waves of 32 x 16, four stages (down,
 // K = 12288, N = 4096: 57 us; five or six stages 57.5 / 58, three 62; the
 // 32 x 32 form of 4 waves 66, four stages 69, 128 x 128 113).
@@ -780,7 +783,7 @@ int launch_gemm_i4g_h(const uint16_t* xh, const float* sx, const uint8_t* q4, co
                      dim3(NW * 64), 0, st, xh, sx, q4, scl, q4b, sclb, y, M, I, O)
   const bool pair192 = !gemm_i4g_h_full(M, O) && (int64_t)((M + 63) / 64) * ((O + 191) / 192) >= 192;
   if (q4b) {
-    if (pair192) Q4H(64, 192, 2, 2, 12, true, false);
+    if (pair192) Q4H(64, 192, 2, 1, 6, true, false);
     else if (big) Q4H(128, 128, 3, 2, 8, true, false);
     else Q4H(64, 64, 3, 2, 4, true, false);
   } else {
