@@ -799,7 +799,10 @@ int launch_moe_route(const MoeArgs& a, void* scratch, hipStream_t st) {
   LAUNCH_TRY("k_route_topk");
   const int mt = moe_mt(a);
   {
-    const int g = P <= GR_CHUNK ? 1 : (P + GR_CHUNK - 1) / GR_CHUNK < 32 ? (P + GR_CHUNK - 1) / GR_CHUNK : 32;
+    // one workgroup per GR_CHUNK pairs, at most 32 (each one reads all P
+    // ids, so more would only add L2 reads): C5's 8576 pairs take 32
+    const int nch = (P + GR_CHUNK - 1) / GR_CHUNK;
+    const int g = nch < 1 ? 1 : nch < 32 ? nch : 32;
     const int chunk = (P + g - 1) / g;
     hipLaunchKernelGGL(k_group, dim3(g), dim3(GR_NT), 0, st, m.idx, P, K, E, 64 * mt, chunk, m.offs, m.slot_tok,
                        m.pair_slot, m.tiles, m.ntiles, m.counts);
