@@ -138,7 +138,8 @@ def test_matmul_q8_extremes(ops):
 @pytest.mark.parametrize("S,I,O", [(1, 4096, 256), (2, 1024, 64), (4, 12288, 128), (1, 64, 5),
                                    (256, 4096, 192), (37, 1024, 100), (5, 128, 64), (1, 12288, 100),
                                    (9, 192, 40), (70, 64, 33), (65, 12288, 70),
-                                   (1, 8192, 77), (1, 16384, 40), (1, 2048, 1000), (130, 1088, 200), (64, 12288, 64)])
+                                   (1, 8192, 77), (1, 16384, 40), (1, 2048, 1000), (130, 1088, 200), (64, 12288, 64),
+                                   (250, 1024, 4100)])
 def test_i4g_idot4(ops, S, I, O):
     say("i4g idot4", S, I, O)
     w = randn(O + I, (O, I), 0.02)
