@@ -167,6 +167,41 @@ __device__ __forceinline__ int wave_sum_i32(int v) {
   v += xor16_i(v);
   return v + xor32_i(v);
 }
+// Integer wave sums of RPW = 1, 2 or 4 values at once (exact: integer adds
+// in any order).  Pairs of registers are folded by permlane swaps, each
+// swap + add halving the lanes a value spans while packing two values into
+// one register, then each 16-lane row by DPP: 4 values cost 10 VALU
+// operations instead of 4 x 8.  Lane l then holds the total of value
+// wave_sum_row<RPW>(l): RPW 4: value [0, 2, 1, 3][l / 16]; RPW 2: l / 32.
+template <int RPW>
+__device__ __forceinline__ int wave_sum_row(int lane) {
+  return RPW == 4 ? (((lane >> 4) & 1) << 1) | (lane >> 5) : RPW == 2 ? lane >> 5 : 0;
+}
+__device__ __forceinline__ int fold32_i(int a, int b) {  // lanes 0-31: a's halves, 32-63: b's
+  const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)a, (uint32_t)b, false, false);
+  return (int)r[0] + (int)r[1];
+}
+__device__ __forceinline__ int fold16_i(int a, int b) {  // per 32-lane half: rows a, b
+  const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)a, (uint32_t)b, false, false);
+  return (int)r[0] + (int)r[1];
+}
+__device__ __forceinline__ int row_sum_i32(int v) {
+  v += dpp_i<MOTY_DPP_QXOR1>(v);
+  v += dpp_i<MOTY_DPP_QXOR2>(v);
+  v += dpp_i<MOTY_DPP_ROR4>(v);
+  return v + dpp_i<MOTY_DPP_ROR8>(v);
+}
+template <int RPW>
+__device__ __forceinline__ int wave_sum_multi_i32(const int (&v)[RPW]) {
+  static_assert(RPW == 1 || RPW == 2 || RPW == 4, "1, 2 or 4 values");
+  if constexpr (RPW == 4) return row_sum_i32(fold16_i(fold32_i(v[0], v[1]), fold32_i(v[2], v[3])));
+  else if constexpr (RPW == 2) {
+    const int t = fold32_i(v[0], v[1]);
+    return row_sum_i32(fold16_i(t, t));
+  } else {
+    return wave_sum_i32(v[0]);
+  }
+}
 // inclusive prefix sum over the wave's lanes: row_shr steps within each
 // 16-lane row (lanes shifted in from before the row read 0), then the
 // totals of the rows below

@@ -205,11 +205,13 @@ __global__ __launch_bounds__(NW * MOTY_WAVE) void k_gemv1_q8(const float* __rest
       if (PAIR) wq2[r][c] = ldnt16(W2 + (int64_t)o * I + kc);
     }
   }
-  // lane r holds the scales of the wave's row r, loaded with the weights so
-  // the epilogue waits on no further memory latency
+  // each lane loads the scales of the row whose sum it will hold
+  // (wave_sum_row), with the weights, so the epilogue waits on no further
+  // memory latency
+  const int rl = wave_sum_row<RPW>(lane);
   float sc = 0.f, sc2 = 0.f;
   {
-    const int o = o0 + (lane < RPW ? lane : 0);
+    const int o = o0 + rl;
     sc = scale[o < O ? o : O - 1];
     if (PAIR) sc2 = scale2[o < O ? o : O - 1];
   }
@@ -233,21 +235,16 @@ __global__ __launch_bounds__(NW * MOTY_WAVE) void k_gemv1_q8(const float* __rest
       acc[r] = dot16(wq[r][c], xq[c], acc[r]);
       if (PAIR) acc2[r] = dot16(wq2[r][c], xq[c], acc2[r]);
     }
-    acc[r] = wave_sum_i32(acc[r]);
-    if (PAIR) acc2[r] = wave_sum_i32(acc2[r]);
   }
-  // lane r finishes row o0 + r; computed on every lane (wave-wide cost is
-  // the same) so the scale loads above stay where they were issued
-  int a = acc[0], a2 = acc2[0];
-#pragma unroll
-  for (int r = 1; r < RPW; r++) {
-    a = lane == r ? acc[r] : a;
-    a2 = lane == r ? acc2[r] : a2;
-  }
+  // the RPW row sums at once: lane l ends with row rl's; the first lane of
+  // each group holding a row finishes it (computed on every lane, so the
+  // scale loads above stay where they were issued)
+  const int a = wave_sum_multi_i32<RPW>(acc);
+  const int a2 = PAIR ? wave_sum_multi_i32<RPW>(acc2) : 0;
   float v = (sc * sx) * (float)a;
   if (PAIR) v = ref_silu_mul(v, (sc2 * sx) * (float)a2);
-  const int o = o0 + lane;
-  if (lane < RPW && o < O) y[o] = v;
+  const int o = o0 + rl;
+  if ((lane & (MOTY_WAVE / RPW - 1)) == 0 && o < O) y[o] = v;
 }
 
 // S = 1, I <= 4096, large matrices (the weight stream is long enough for
@@ -294,11 +291,13 @@ __global__ __launch_bounds__(NW * MOTY_WAVE) void k_gemv1_q8_lds(const float* __
       if (PAIR) wq2[r][c] = ldnt16(W2 + (int64_t)o * I + kc);
     }
   }
-  // lane r holds the scales of the wave's row r, loaded with the weights so
-  // the epilogue waits on no further memory latency
+  // each lane loads the scales of the row whose sum it will hold
+  // (wave_sum_row), with the weights, so the epilogue waits on no further
+  // memory latency
+  const int rl = wave_sum_row<RPW>(lane);
   float sc = 0.f, sc2 = 0.f;
   {
-    const int o = o0 + (lane < RPW ? lane : 0);
+    const int o = o0 + rl;
     sc = scale[o < O ? o : O - 1];
     if (PAIR) sc2 = scale2[o < O ? o : O - 1];
   }
@@ -341,21 +340,16 @@ __global__ __launch_bounds__(NW * MOTY_WAVE) void k_gemv1_q8_lds(const float* __
       acc[r] = dot16(wq[r][c], xq[c], acc[r]);
       if (PAIR) acc2[r] = dot16(wq2[r][c], xq[c], acc2[r]);
     }
-    acc[r] = wave_sum_i32(acc[r]);
-    if (PAIR) acc2[r] = wave_sum_i32(acc2[r]);
   }
-  // lane r finishes row o0 + r; computed on every lane (wave-wide cost is
-  // the same) so the scale loads above stay where they were issued
-  int a = acc[0], a2 = acc2[0];
-#pragma unroll
-  for (int r = 1; r < RPW; r++) {
-    a = lane == r ? acc[r] : a;
-    a2 = lane == r ? acc2[r] : a2;
-  }
+  // the RPW row sums at once: lane l ends with row rl's; the first lane of
+  // each group holding a row finishes it (computed on every lane, so the
+  // scale loads above stay where they were issued)
+  const int a = wave_sum_multi_i32<RPW>(acc);
+  const int a2 = PAIR ? wave_sum_multi_i32<RPW>(acc2) : 0;
   float v = (sc * sx) * (float)a;
   if (PAIR) v = ref_silu_mul(v, (sc2 * sx) * (float)a2);
-  const int o = o0 + lane;
-  if (lane < RPW && o < O) y[o] = v;
+  const int o = o0 + rl;
+  if ((lane & (MOTY_WAVE / RPW - 1)) == 0 && o < O) y[o] = v;
 }
 
 template <int NC, bool PAIR>
