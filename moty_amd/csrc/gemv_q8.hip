@@ -358,8 +358,12 @@ static int launch_1(const float* x, const int8_t* W, const float* scale, const i
   // Launch shape from a sweep of rows/wave x waves/workgroup on MI355X over
   // decode shapes (O 1024..12288, I 1024..4096, plain and PAIR): four rows
   // per wave (fewer when that leaves < 256 waves), then enough waves per
-  // workgroup to bring the grid near one workgroup per CU.
+  // workgroup to bring the grid near one workgroup per CU.  Plain rows of
+  // 3-4 KiB take two rows per wave where that still gives two waves on every
+  // CU (C1's down, 1024 x 3072: FFN step 5.98 / 5.90 against 6.04 / 5.91 us
+  // on two boxes with four rows in one-wave workgroups; one row 6.33).
   int rpw = 4;
+  if (!PAIR && NC >= 3 && O / 2 >= 512) rpw = 2;
   while (rpw > 1 && (O + rpw - 1) / rpw < 256) rpw >>= 1;
   const int waves = (O + rpw - 1) / rpw;
   const int nw = waves > 768 ? 4 : (waves + 255) / 256;  // one workgroup per CU, up to 4 waves each
@@ -390,7 +394,7 @@ static int launch_1(const float* x, const int8_t* W, const float* scale, const i
     LAUNCH_TRY("k_gemv1_q8");                                                                                \
     return MOTY_OK;                                                                                          \
   }
-  L1(4, 4) L1(4, 3) L1(4, 2) L1(4, 1) L1(2, 2) L1(2, 1) L1(1, 2) L1(1, 1)
+  L1(4, 4) L1(4, 3) L1(4, 2) L1(4, 1) L1(2, 4) L1(2, 3) L1(2, 2) L1(2, 1) L1(1, 2) L1(1, 1)
 #undef L1
   return MOTY_EUNSUP;
 }
