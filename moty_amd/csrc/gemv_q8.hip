@@ -258,7 +258,11 @@ __global__ __launch_bounds__(NW * MOTY_WAVE) void k_gemv1_q8(const float* __rest
 // they fly the row is quantized (qrow_i8 bit for bit: the row's amax from a
 // wave max and an LDS exchange across the waves) into LDS, from where each
 // lane takes exactly the 16 codes per chunk its dot needs.
-template <int NC, int RPW, bool PAIR, int NW>
+// XF: the weight loads are issued right after the activation loads, without
+// waiting for them -- for short weight streams, where the activation row is
+// as large as a wave's weights (C1's down: 12 KiB of h against 3 KiB per
+// row) and is better loaded once per workgroup than once per wave.
+template <int NC, int RPW, bool PAIR, int NW, bool XF = false>
 __global__ __launch_bounds__(NW * MOTY_WAVE) void k_gemv1_q8_lds(const float* __restrict__ x, const int8_t* __restrict__ W,
                                                       const float* __restrict__ scale,
                                                       const int8_t* __restrict__ W2,
@@ -277,8 +281,10 @@ __global__ __launch_bounds__(NW * MOTY_WAVE) void k_gemv1_q8_lds(const float* __
     const int k = e0 + 4 * j;
     xv[j] = *(const float4*)(x + (k < I ? k : 0));
   }
-  MOTY_WAIT_VMCNT(0);
-  __builtin_amdgcn_s_barrier();
+  if (!XF) {
+    MOTY_WAIT_VMCNT(0);
+    __builtin_amdgcn_s_barrier();
+  }
   int4 wq[RPW][NC], wq2[RPW][NC];
 #pragma unroll
   for (int r = 0; r < RPW; r++) {
@@ -358,12 +364,8 @@ static int launch_1(const float* x, const int8_t* W, const float* scale, const i
   // Launch shape from a sweep of rows/wave x waves/workgroup on MI355X over
   // decode shapes (O 1024..12288, I 1024..4096, plain and PAIR): four rows
   // per wave (fewer when that leaves < 256 waves), then enough waves per
-  // workgroup to bring the grid near one workgroup per CU.  Plain rows of
-  // 3-4 KiB take two rows per wave where that still gives two waves on every
-  // CU (C1's down, 1024 x 3072: FFN step 5.98 / 5.90 against 6.04 / 5.91 us
-  // on two boxes with four rows in one-wave workgroups; one row 6.33).
+  // workgroup to bring the grid near one workgroup per CU.
   int rpw = 4;
-  if (!PAIR && NC >= 3 && O / 2 >= 512) rpw = 2;
   while (rpw > 1 && (O + rpw - 1) / rpw < 256) rpw >>= 1;
   const int waves = (O + rpw - 1) / rpw;
   const int nw = waves > 768 ? 4 : (waves + 255) / 256;  // one workgroup per CU, up to 4 waves each
@@ -387,6 +389,20 @@ static int launch_1(const float* x, const int8_t* W, const float* scale, const i
     LAUNCH_TRY("k_gemv1_q8_lds");
     return MOTY_OK;
   }
+  // plain rows of 3-4 KiB with at least 1024 of them: the shared-activation
+  // kernel in 4-wave workgroups, weight loads issued before the row lands
+  // (C1's down, 1024 x 3072: FFN step 5.63 against 5.95 us for the per-wave
+  // kernel; waiting for the row first 5.94; 2 rows x 2 waves 5.65)
+  if (!PAIR && NC >= 3 && O >= 1024) {
+    if (O >= 2048)
+      hipLaunchKernelGGL((k_gemv1_q8_lds<NC, 2, false, 4, true>), dim3((O + 7) / 8), dim3(4 * MOTY_WAVE), 0, st, x, W,
+                         scale, W2, scale2, y, I, O);
+    else
+      hipLaunchKernelGGL((k_gemv1_q8_lds<NC, 1, false, 4, true>), dim3((O + 3) / 4), dim3(4 * MOTY_WAVE), 0, st, x, W,
+                         scale, W2, scale2, y, I, O);
+    LAUNCH_TRY("k_gemv1_q8_lds");
+    return MOTY_OK;
+  }
 #define L1(R, N)                                                                                              \
   if (rpw == R && nw == N) {                                                                                 \
     hipLaunchKernelGGL((k_gemv1_q8<NC, R, PAIR, N>), dim3(nb), dim3(N * MOTY_WAVE), 0, st, x, W, scale, W2,   \
@@ -394,7 +410,7 @@ static int launch_1(const float* x, const int8_t* W, const float* scale, const i
     LAUNCH_TRY("k_gemv1_q8");                                                                                \
     return MOTY_OK;                                                                                          \
   }
-  L1(4, 4) L1(4, 3) L1(4, 2) L1(4, 1) L1(2, 4) L1(2, 3) L1(2, 2) L1(2, 1) L1(1, 2) L1(1, 1)
+  L1(4, 4) L1(4, 3) L1(4, 2) L1(4, 1) L1(2, 2) L1(2, 1) L1(1, 2) L1(1, 1)
 #undef L1
   return MOTY_EUNSUP;
 }

@@ -102,7 +102,7 @@ def test_pack_int4_grouped(ops, O, I, gs):
     assert same_bits(to_np(q4), q42) and same_bits(to_np(s), s2)
 
 
-Q8_CASES = [(1, 1024, 3072), (1, 3072, 1024), (1, 3072, 2000), (1, 4096, 1500), (2, 1024, 100), (3, 48, 24), (4, 2048, 1024),
+Q8_CASES = [(1, 1024, 3072), (1, 3072, 1024), (1, 3072, 2000), (1, 4096, 1500), (1, 4096, 2100), (2, 1024, 100), (3, 48, 24), (4, 2048, 1024),
             (1, 16384, 64), (5, 1024, 256), (8, 3072, 96), (64, 1024, 1024), (512, 1024, 2048),
             (130, 2048, 200), (33, 16, 17), (1024, 1024, 4096), (256, 1040, 8192), (200, 3072, 1000),
             # K % 128 == 0 past the GEMV: the DMA-staged GEMM, one-block and ragged tiles
