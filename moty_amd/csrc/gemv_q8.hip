@@ -249,7 +249,7 @@ __global__ __launch_bounds__(NW * MOTY_WAVE) void k_gemv1_q8(const float* __rest
 
 // S = 1, I <= 4096, large matrices (the weight stream is long enough for
 // its queueing to matter).  The workgroup loads the activation row once
-// (thread t takes XE contiguous values) and waits for it before any weight
+// (thread t takes float4 units t, t + NT, ...) and waits for it before any weight
 // load is issued: queued behind the weight stream, in the CU's load path
 // and in L2, it would arrive with the weights.  Then it streams its
 // weights: wave w owns
@@ -268,17 +268,16 @@ __global__ __launch_bounds__(NW * MOTY_WAVE) void k_gemv1_q8_lds(const float* __
                                                       const int8_t* __restrict__ W2,
                                                       const float* __restrict__ scale2, float* __restrict__ y,
                                                       int I, int O) {
-  constexpr int XE = 16 * NC / NW;  // activation values per thread
-  static_assert(XE % 4 == 0 && XE > 0, "whole float4 of the activation row per thread");
+  constexpr int NU = NC * CHUNK / 4;                         // float4 units of the row
+  constexpr int XV = (NU + NW * MOTY_WAVE - 1) / (NW * MOTY_WAVE);  // per thread (unit t + j*NT)
   __shared__ __align__(16) int8_t xq_s[NC * CHUNK];
   __shared__ float red[NW];
   const int lane = threadIdx.x % MOTY_WAVE, wv = threadIdx.x / MOTY_WAVE;
   const int o0 = (blockIdx.x * NW + wv) * RPW;
-  const int e0 = threadIdx.x * XE;
-  float4 xv[XE / 4];
+  float4 xv[XV];
 #pragma unroll
-  for (int j = 0; j < XE / 4; j++) {
-    const int k = e0 + 4 * j;
+  for (int j = 0; j < XV; j++) {
+    const int k = (threadIdx.x + j * NW * MOTY_WAVE) * 4;
     xv[j] = *(const float4*)(x + (k < I ? k : 0));
   }
   if (!XF) {
@@ -313,8 +312,8 @@ __global__ __launch_bounds__(NW * MOTY_WAVE) void k_gemv1_q8_lds(const float* __
   // weights there are multiplied by these zeros)
   float amax = 0.f;
 #pragma unroll
-  for (int j = 0; j < XE / 4; j++) {
-    xv[j] = sel4(e0 + 4 * j < I, xv[j]);
+  for (int j = 0; j < XV; j++) {
+    xv[j] = sel4((threadIdx.x + j * NW * MOTY_WAVE) * 4 < I, xv[j]);
     amax = fmaxf(amax, fmaxf(fmaxf(fabsf(xv[j].x), fabsf(xv[j].y)), fmaxf(fabsf(xv[j].z), fabsf(xv[j].w))));
   }
   amax = wave_max_f32(amax);
@@ -328,10 +327,13 @@ __global__ __launch_bounds__(NW * MOTY_WAVE) void k_gemv1_q8_lds(const float* __
   if (sx < 1e-12f) sx = 1e-12f;
   const float inv = 1.f / sx;
 #pragma unroll
-  for (int j = 0; j < XE / 4; j++)
-    *(uint32_t*)(xq_s + e0 + 4 * j) =
-        (uint32_t)(rne_int(xv[j].x * inv) & 0xff) | ((uint32_t)(rne_int(xv[j].y * inv) & 0xff) << 8) |
-        ((uint32_t)(rne_int(xv[j].z * inv) & 0xff) << 16) | ((uint32_t)(rne_int(xv[j].w * inv) & 0xff) << 24);
+  for (int j = 0; j < XV; j++) {
+    const int k = (threadIdx.x + j * NW * MOTY_WAVE) * 4;
+    if (k < NC * CHUNK)
+      *(uint32_t*)(xq_s + k) =
+          (uint32_t)(rne_int(xv[j].x * inv) & 0xff) | ((uint32_t)(rne_int(xv[j].y * inv) & 0xff) << 8) |
+          ((uint32_t)(rne_int(xv[j].z * inv) & 0xff) << 16) | ((uint32_t)(rne_int(xv[j].w * inv) & 0xff) << 24);
+  }
   __syncthreads();
   int4 xq[NC];
 #pragma unroll
