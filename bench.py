@@ -40,7 +40,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=6.0, help="bound on each CPU baseline sample")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only launch the dominant kernel on distinct weights and a 64 MiB copy (for rocprofv3 --pmc)")
-    ap.add_argument("--only", choices=["c1", "c2", "c3", "c3r4", "c4", "c5", "q8gemv"],
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c3r4", "c4", "c5", "c5s", "q8gemv"],
                     help="run one config alone and print its JSON object (for rocprofv3 runs of a single config)")
     return ap.parse_args()
 
@@ -117,6 +117,17 @@ class Ctx:
         e1.record()
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / 1e3 / steps, steps
+
+
+C5_SKEW_LABEL = "skewed (+2.0 on 8 hot experts)"
+
+
+def c5_skew_bias():
+    """C5's skewed routing: +2.0 on the router logits of every 16th of the 128 experts."""
+    import torch
+    bias = torch.zeros(128, device="cuda:0")
+    bias[torch.arange(0, 128, 16, device="cuda:0")] = 2.0
+    return bias
 
 
 def pmc_traffic(name, key=None):
@@ -775,7 +786,11 @@ def main():
                                        args.warmup, label="C4 OLMoE MoE layer Q8, T=256", traffic_key="c4_layer"),
                "c5": lambda: bench_moe(c, 4, 1072, 128, 8, 768, 2048, 1, moty_amd.ORDER_EXPERT, args.steps,
                                        args.warmup, label="C5 Qwen3-30B-A3B MoE layer Q8, T=1072, uniform",
-                                       traffic_key="c5_layer")}[args.only]()
+                                       traffic_key="c5_layer"),
+               "c5s": lambda: bench_moe(c, 4, 1072, 128, 8, 768, 2048, 1, moty_amd.ORDER_EXPERT, args.steps,
+                                        args.warmup, bias=c5_skew_bias(),
+                                        label="C5 Qwen3-30B-A3B MoE layer Q8, T=1072, " + C5_SKEW_LABEL,
+                                        traffic_key="c5s_layer")}[args.only]()
         print(json.dumps({k2: v for k2, v in one.items() if k2 not in HIDDEN}), flush=True)
         return
 
@@ -803,13 +818,10 @@ def main():
         log("GGUF loading")
         extra.append(bench_gguf(c, args.steps, args.warmup))
         log("C5")
-        E5 = 128
-        bias = torch.zeros(E5, device="cuda:0")
-        bias[torch.arange(0, 128, 16, device="cuda:0")] = 2.0
-        for b, lab in ((None, "uniform"), (bias, "skewed (+2.0 on 8 hot experts)")):
-            r5 = bench_moe(c, 4, 1072, E5, 8, 768, 2048, 1, moty_amd.ORDER_EXPERT, args.steps, args.warmup, bias=b,
+        for b, lab in ((None, "uniform"), (c5_skew_bias(), C5_SKEW_LABEL)):
+            r5 = bench_moe(c, 4, 1072, 128, 8, 768, 2048, 1, moty_amd.ORDER_EXPERT, args.steps, args.warmup, bias=b,
                            label="C5 Qwen3-30B-A3B MoE layer Q8, T=1072 ragged batch (48 decode + 1024 prefill), "
-                                 "E=128, top-8, I=768, D=2048, " + lab, traffic_key=None if b is not None else "c5_layer")
+                                 "E=128, top-8, I=768, D=2048, " + lab, traffic_key="c5_layer" if b is None else "c5s_layer")
             extra.append(r5)
     cpu = None
     if not args.no_cpu:
