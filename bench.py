@@ -26,6 +26,8 @@ for _k, _v in (("OMP_WAIT_POLICY", "active"), ("OMP_PROC_BIND", "close"), ("GOMP
 ROOT = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA
+F16_PEAK_TFLOPS = 2500.0  # dense f16 MFMA
+F32_PEAK_TFLOPS = 157.3  # f32
 METRIC = "Q8 GEMV HBM GB/s (% peak); MoE layer tokens/s at T=256 (1 GPU)"
 HIDDEN = ("x", "Wr", "layer0", "_cpu", "w0")  # inputs kept for the CPU baseline, never printed
 
@@ -40,7 +42,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=6.0, help="bound on each CPU baseline sample")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only launch the dominant kernel on distinct weights and a 64 MiB copy (for rocprofv3 --pmc)")
-    ap.add_argument("--only", choices=["c1", "c2", "c3", "c3r4", "c4", "c5", "c5s", "q8gemv"],
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c3r4", "c4", "c5", "c5s", "q8gemv", "floor", "d1"],
                     help="run one config alone and print its JSON object (for rocprofv3 runs of a single config)")
     return ap.parse_args()
 
@@ -56,7 +58,8 @@ def roofline(bound, achieved, peak, unit, traffic=None):
 
 class Ctx:
     def __init__(self, torch, ops):
-        self.torch, self.ops = torch, ops
+        import moty_amd
+        self.torch, self.ops, self.ops_mod = torch, ops, moty_amd
 
     def gen(self, cfg, tensor):
         return self.torch.Generator(device="cuda:0").manual_seed(0x4D4F5459 ^ (cfg << 8) ^ tensor)
@@ -75,14 +78,15 @@ class Ctx:
         w = self.randn(shape, g, 0.02)
         return self.ops.pack_int4_grouped(w, 32)
 
-    def time_steps(self, fns, steps, warmup):
+    def time_steps(self, fns, steps, warmup, replays=7):
         """Time exactly `steps` steps: step k runs fns[k % len(fns)] (the
         weight copies rotate), captured into one HIP graph; `warmup` steps
-        from a second graph run just before it on
-        the same stream, so the timed graph is queued while the GPU is still
-        busy and no launch gap enters the timed region.  Events sit on the
-        stream the library launches on (torch's current stream).  Returns
-        (seconds per step, steps timed)."""
+        from a second graph run just before it on the same stream, so the
+        timed graph is queued while the GPU is still busy and no launch gap
+        enters the timed region.  The pair is replayed `replays` times on a
+        stream of its own, HIP events around each timed replay; the result
+        is the median replay's seconds per step (self.last holds the replay
+        count and the spread).  Returns (seconds per step, steps timed)."""
         torch = self.torch
         n = len(fns)
         steps = max(1, int(steps))
@@ -97,7 +101,7 @@ class Ctx:
 
         def capture(first, count):
             g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
+            with torch.cuda.graph(g, stream=s):
                 for k in range(count):
                     fns[(first + k) % n]()
             return g
@@ -107,16 +111,23 @@ class Ctx:
         # untouched by the warm-up or was touched at its start, with the
         # rest of the rotation (more than the 256 MB Infinity Cache) after it
         warm = capture((-warmup) % n, warmup)
-        warm.replay()  # first replay of each graph uploads it
-        timed.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        warm.replay()
-        e0.record()
-        timed.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / 1e3 / steps, steps
+        ts = []
+        with torch.cuda.stream(s):
+            warm.replay()  # first replay of each graph uploads it
+            timed.replay()
+            torch.cuda.synchronize()
+            for _ in range(max(1, replays)):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                warm.replay()
+                e0.record(s)
+                timed.replay()
+                e1.record(s)
+                torch.cuda.synchronize()
+                ts.append(e0.elapsed_time(e1) / 1e3 / steps)
+        ts.sort()
+        med = ts[len(ts) // 2]
+        self.last = {"replays": len(ts), "spread_us": [round(ts[0] * 1e6, 3), round(ts[-1] * 1e6, 3)]}
+        return med, steps
 
 
 C5_SKEW_LABEL = "skewed (+2.0 on 8 hot experts)"
@@ -162,18 +173,44 @@ def bench_c1(c, steps, warmup):
     out = torch.empty((1, D), device="cuda:0")
     h = torch.empty((1, I), device="cuda:0")
     t, n = c.time_steps([lambda w=w: ops.dense_ffn_q8(x, *w, out=out) for w in copies], steps, warmup)
+    rep = dict(c.last)
     # dominant kernel alone: the fused gate+up GEMV (k_gemv_q8 PAIR mode)
     gu = [lambda w=w: ops.gate_up_silu_q8(x, w[0], w[1], w[2], w[3], out=h) for w in copies]
     tg, _ = c.time_steps(gu, steps, warmup)
     gu_algo = 2 * I * D + 2 * I * 4 + D * 4 + I * 4
+    # the one-launch form of the same FFN (workgroups exchanging h through
+    # device memory; bit-exact, off by default), timed alike
+    ops.set_ffn1(1)
+    try:
+        t1, _ = c.time_steps([lambda w=w: ops.dense_ffn_q8(x, *w, out=out) for w in copies], steps, warmup)
+    finally:
+        ops.set_ffn1(0)
     torch.cuda.synchronize()
     return {
         "workload": "C1 Qwen3-0.6B FFN decode, Q8_0 (fused gate/up GEMV + SiLU, down GEMV), S=1, D=1024, I=3072",
         "gbs": algo / t / 1e9, "ms_per_step": t * 1e3, "steps": n, "algo_bytes": algo,
-        "weight_copies": ncopy, "x": x, "w0": copies[0],
+        "weight_copies": ncopy, "x": x, "w0": copies[0], "timing": rep,
         "kernel": {"name": "k_gemv1_q8<1,4,PAIR,3> gate+up+SiLU", "us": tg * 1e6, "algo_bytes": gu_algo,
                    "gbs": gu_algo / tg / 1e9},
+        "one_launch_us": round(t1 * 1e6, 3),
     }
+
+
+def floor_probe():
+    """Launch and pure-read floors and hand-off latencies of this GPU
+    (libmoty_probe.so, built from moty_amd/csrc/floor_probe.hip)."""
+    import ctypes as C
+    try:
+        L = C.CDLL(os.path.join(ROOT, "moty_amd", "libmoty_probe.so"))
+        L.moty_probe_floor_names.restype = C.c_char_p
+        names = L.moty_probe_floor_names().decode().split(",")
+        out = (C.c_float * len(names))()
+        rc = L.moty_probe_floor(out)
+        if rc:
+            return {"error": "hip error %d" % rc}
+        return {k: round(float(v), 3) for k, v in zip(names, out)}
+    except OSError as e:
+        return {"error": str(e)[:160]}
 
 
 def moe_weights(c, cfg, E, I, D):
@@ -203,13 +240,37 @@ def bench_moe(c, cfg, T, E, K, I, D, norm, order, steps, warmup, bias=None, labe
     t, n = c.time_steps([lambda L=L: L(x, out=out) for L in layers], max(8, steps // 16), max(4, warmup // 16))
     gbs = algo / t / 1e9
     return {
-        "workload": label, "tokens_per_s": T / t, "ms_per_layer": t * 1e3, "steps": n, "weight_copies": ncopy,
+        "workload": label, "tokens_per_s": T / t, "ms_per_layer": t * 1e3, "steps": n, "timing": dict(c.last),
+        "weight_copies": ncopy,
         "active_experts": active, "load_max": int(cnt.max()), "load_mean": round(float(cnt.float().mean()), 2),
         "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s",
                              pmc_traffic("hbm_traffic_pmc", traffic_key) if traffic_key else None),
         "int_tops": round(ops_int / t / 1e12, 2),
         "x": x, "Wr": Wr, "layer0": layers[0],
     }
+
+
+def bench_moe_d1(c, cfg, E, K, I, D, steps, warmup, label):
+    """Decode MoE, S = 1: moty_nn_moe_topk_d1 (nn/moe.c:33-153) -- router,
+    softmax top-k (normalised), the K active experts' FFNs, combine in top-k
+    order.  Only the K routed experts' weights move, so the weight copies
+    rotate until the touched bytes exceed the Infinity Cache."""
+    torch = c.torch
+    from moty_amd.ops import MoeLayer
+    ebytes = 3 * I * D + (2 * I + D) * 4  # one expert
+    algo = K * ebytes + E * D * 4 + 2 * D * 4
+    ncopy = n_copies(K * ebytes, lo=2)
+    Wr = c.randn((E, D), c.gen(cfg, 1), 0.02)
+    x = c.randn((1, D), c.gen(cfg, 2))
+    layers = [MoeLayer(Wr, *moe_weights(c, cfg + 32 * k, E, I, D), K, norm_topk=1, order=c.ops_mod.ORDER_TOPK)
+              for k in range(ncopy)]
+    out = torch.empty((1, D), device="cuda:0")
+    t, n = c.time_steps([lambda L=L: L(x, out=out) for L in layers], steps, warmup)
+    rep = dict(c.last)
+    return {"workload": label, "us_per_token": round(t * 1e6, 3), "tokens_per_s": round(1 / t, 1), "steps": n,
+            "timing": rep, "weight_copies": ncopy, "algo_bytes": algo,
+            "roofline": roofline("hbm", algo / t / 1e9, HBM_PEAK_GBS, "GB/s"),
+            "x": x, "Wr": Wr, "layer0": layers[0]}
 
 
 def bench_moe_cached(c, steps):
@@ -305,6 +366,7 @@ def bench_c2(c, steps, warmup):
                 ops.matmul_q8_preq(xq[I], sx[I], q, s, out=ys[I])
         return f
     t, n = c.time_steps([step(w) for w in copies], max(16, steps // 8), max(4, warmup // 8))
+    rep = dict(c.last)
     ops_int = 2 * M * sum(O * I for _, O, I in shapes)
 
     # the three GEMMs alone, and the platform library's int8 GEMM
@@ -325,7 +387,7 @@ def bench_c2(c, steps, warmup):
     algo = wbytes + M * (1024 + 2048 + 3072) * 4 + sum(M * O * 4 for _, O, _ in shapes)
     return {"workload": "C2 Qwen3-0.6B layer, 7 Q8 projections as prefill GEMMs, M=512 "
                         "(q/k/v/gate/up fused by rows: one GEMM N=10240, K=1024; o; down)",
-            "ms_per_step": t * 1e3, "steps": n,
+            "ms_per_step": t * 1e3, "steps": n, "timing": rep,
             "roofline": roofline("mfma", ops_int / t / 1e12, INT8_PEAK_TOPS, "TOP/s",
                                  pmc_traffic("hbm_traffic_pmc", "c2_step")),
             "hbm_gbs": round(algo / t / 1e9, 1),
@@ -356,10 +418,26 @@ def bench_c3(c, steps, warmup):
         ops_int = 2 * M * 3 * I * D
         algo = wbytes + M * (D + I + I + D) * 4
         tr = pmc_traffic("hbm_traffic_pmc", "c3_M%d_step" % M)
-        res["M%d" % M] = {"ms_per_step": t * 1e3, "steps": n,
+        res["M%d" % M] = {"ms_per_step": t * 1e3, "steps": n, "timing": dict(c.last),
                           "hbm": roofline("hbm", algo / t / 1e9, HBM_PEAK_GBS, "GB/s", tr),
                           "mfma": roofline("mfma", ops_int / t / 1e12, INT8_PEAK_TOPS, "TOP/s", tr)}
-    return {"workload": "C3 8B-dense FFN, grouped int4 g32 (IDOT4=1), D=4096, I=12288, M=1 and M=256", **res}
+        if M > 1:
+            # the M = 256 GEMMs multiply on f16 MFMA (exact for these
+            # integers), whose dense peak is half the int8 one
+            res["M%d" % M]["mfma_f16"] = roofline("mfma", ops_int / t / 1e12, F16_PEAK_TFLOPS, "TFLOP/s")
+
+        # the reference's default path (IDOT4 unset: exact f32 activations,
+        # nn/matmul.c:199-253), same weights and inputs
+        def step_f32(w):
+            return lambda: ops.dense_ffn_i4g(x, w[0][0], w[0][1], w[1][0], w[1][1], w[2][0], w[2][1], idot4=False,
+                                             out=y)
+        t, n = c.time_steps([step_f32(w) for w in copies], max(4, steps // (8 if M == 1 else 64)), 4)
+        res["M%d_exact_f32" % M] = {"ms_per_step": t * 1e3, "steps": n, "timing": dict(c.last),
+                                    "hbm": roofline("hbm", algo / t / 1e9, HBM_PEAK_GBS, "GB/s"),
+                                    "vector_f32": roofline("valu", 2 * M * 3 * I * D / t / 1e12, F32_PEAK_TFLOPS,
+                                                           "TFLOP/s")}
+    return {"workload": "C3 8B-dense FFN, grouped int4 g32, D=4096, I=12288, M=1 and M=256: IDOT4=1 (int8 "
+                        "activations) and, as M*_exact_f32, the reference default IDOT4 unset (exact f32)", **res}
 
 
 def bench_q8_gemv_sizes(c, steps, warmup):
@@ -609,6 +687,22 @@ def cpu_moe(cr, r, T_sample, order, norm, budget, nmin=20, skew=None, cap=0):
     return T_sample / t, n
 
 
+def cpu_moe_d1(cr, r, budget):
+    np, cl = cr.np, cr.cl
+    lay = r["layer0"]
+    x = np.ascontiguousarray(r["x"].cpu().numpy())
+    Wr = r["Wr"].cpu().numpy()
+    ws = [t.cpu().numpy() for t in lay.keep[1:7]]
+    out = np.empty((1, lay.D), np.float32)
+    if cr.r is not None:
+        fn = lambda: cr.r.ref_moe_d1(cl.ptr(out), cl.ptr(x), cl.ptr(Wr), *[cl.ptr(a) for a in ws], lay.E, lay.K,
+                                     lay.I, lay.D)
+    else:
+        fn = lambda: cl.o_moe(x, Wr, dict(zip(("G", "GS", "U", "US", "Dn", "DS"), ws)), lay.K, "olmoe", norm=1)
+    t, n = cpu_med(fn, budget)
+    return cr.out(round(t * 1e6, 1), "us/token", "moty_nn_moe_topk_d1 (nn/moe.c:33-153), one token", n)
+
+
 def cpu_c2(cr, c2, budget):
     np = cr.np
     d = c2["_cpu"]
@@ -739,6 +833,8 @@ def cpu_baseline(c1, c4, extra, budget):
                 r["cpu_baseline"] = cpu_q8_sizes(cr, r, budget)
             elif w.startswith("GGUF"):
                 r["cpu_baseline"] = cpu_gguf(cr, r, budget)
+            elif w.startswith("Decode MoE"):
+                r["cpu_baseline"] = cpu_moe_d1(cr, r, budget)
             elif w.startswith("C5"):
                 sk = "skewed" in w
                 tp, n = cpu_moe(cr, r, 134, "batch", 1, budget, skew=np.arange(0, 128, 16) if sk else None)
@@ -778,6 +874,8 @@ def main():
         return
     if args.only:
         one = {"c1": lambda: bench_c1(c, args.steps, args.warmup),
+               "floor": floor_probe,
+               "d1": lambda: bench_moe_d1(c, 5, 64, 8, 1024, 2048, args.steps, args.warmup, "Decode MoE S=1, C4 shape"),
                "c2": lambda: bench_c2(c, args.steps, args.warmup),
                "c3": lambda: bench_c3(c, args.steps, args.warmup),
                "c3r4": lambda: bench_c3_r4(c, args.steps, args.warmup),
@@ -813,6 +911,11 @@ def main():
         extra.append(bench_c3(c, args.steps, args.warmup))
         log("C3 in Q4R4")
         extra.append(bench_c3_r4(c, args.steps, args.warmup))
+        log("decode MoE (S = 1)")
+        extra.append(bench_moe_d1(c, 5, 64, 8, 1024, 2048, args.steps, args.warmup,
+                                  "Decode MoE S=1 (moty_nn_moe_topk_d1), C4 expert shape: E=64, top-8, I=1024, D=2048"))
+        extra.append(bench_moe_d1(c, 6, 128, 8, 768, 2048, args.steps, args.warmup,
+                                  "Decode MoE S=1 (moty_nn_moe_topk_d1), C5 expert shape: E=128, top-8, I=768, D=2048"))
         log("C4 through the expert cache")
         extra.append(bench_moe_cached(c, args.steps))
         log("GGUF loading")
@@ -834,6 +937,7 @@ def main():
         for k in HIDDEN:
             r.pop(k, None)
     k = c1["kernel"]
+    fl = floor_probe()
     moe = {k2: v for k2, v in c4.items() if k2 not in HIDDEN}
     moe["metric"] = "MoE layer tokens/s at T=256 (1 GPU)"
     moe["value"] = round(moe.pop("tokens_per_s"), 1)
@@ -850,8 +954,15 @@ def main():
         "roofline": dict(roofline("hbm", k["gbs"], HBM_PEAK_GBS, "GB/s", pmc_traffic("hbm_traffic_pmc", "c1_gate_up")),
                          kernel=k["name"], kernel_us=round(k["us"], 3), algo_bytes=k["algo_bytes"],
                          timing="HIP events around graph replays of the kernel alone (weights rotating "
-                                "over the copies), elapsed / launches"),
-        "whole_ffn_roofline": roofline("hbm", c1["gbs"], HBM_PEAK_GBS, "GB/s", pmc_traffic("hbm_traffic_pmc", "c1_step")),
+                                "over the copies), elapsed / launches, median of the replays",
+                         floor_us=fl.get("read_6332416B_us")),
+        "whole_ffn_roofline": dict(roofline("hbm", c1["gbs"], HBM_PEAK_GBS, "GB/s",
+                                            pmc_traffic("hbm_traffic_pmc", "c1_step")),
+                                   floor_us=fl.get("read_pair_6332416B_3170304B_us"),
+                                   one_launch_floor_us=fl.get("read_9474048B_us")),
+        "timing": c1["timing"],
+        "one_launch_us": c1["one_launch_us"],
+        "floors": fl,
         "cpu_baseline": cpu,
         "moe": moe,
         "extra": extra,

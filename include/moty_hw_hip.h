@@ -56,6 +56,18 @@ const char *moty_hip_last_error(void);
 /* Kernel tier string, the analogue of HW_IDOT_KERNEL/HW_F32_KERNEL
  * (hw/hw.h:160-208): "gfx950-mfma-i8/gfx950-f32". */
 const char *moty_hip_kernel_tier(void);
+/* No reference counterpart (the CPU kernels never wait on each other).
+ * The one-launch form of the S = 1 Q8 dense FFN (moty_hip_set_ffn1) hands h
+ * between workgroups through device memory; every such wait is bounded.  Waits for the current thread's device and returns in *count
+ * the number of calls since the last query whose wait ran out (0: every
+ * output since then is valid), and clears it. */
+int moty_hip_wait_errors(int *count);
+/* No reference counterpart: on = 1 routes the S = 1 Q8 dense FFN (when
+ * D % 1024 == 0, D <= 2048, I % 1024 == 0, I <= 4096 on a 256-CU device)
+ * through the one-launch form instead of the two GEMV launches (gate/up +
+ * SiLU, then down), for this thread's device.  Default off (slower on
+ * MI355X); env MOTY_FFN1=1 at set-up turns it on.  Both give the same bits. */
+int moty_hip_set_ffn1(int on);
 
 /* ---------------- host-pointer drop-ins ---------------- */
 /* moty_matmul_q_s (nn/nn_matmul.h:64, nn/matmul.c:51-66): Q8_0 per-row int8

@@ -42,6 +42,8 @@ SIGNATURES = {
     "moty_hip_shutdown": (I32, []),
     "moty_hip_last_error": (C.c_char_p, []),
     "moty_hip_kernel_tier": (C.c_char_p, []),
+    "moty_hip_wait_errors": (I32, [C.POINTER(I32)]),
+    "moty_hip_set_ffn1": (I32, [I32]),
     "moty_hip_matmul_q_s": (I32, [P, P, P, P, I32, I32, I32]),
     "moty_hip_matmul_i4_grouped_s": (I32, [P, P, P, P, I32, I32, I32, I32]),
     "moty_hip_matmul_q4r4_s": (I32, [P, P, P, P, I32, I32, I32]),

@@ -16,7 +16,11 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmoty_hw_hip.so")
-SOURCES = ["quant.hip", "gemv_q8.hip", "gemm_q8.hip", "q4g.hip", "r4.hip", "moe.hip", "ops.hip", "gguf.hip", "api.cpp", "expert_cache.cpp"]
+# measurement support for bench.py (launch and pure-read floors, hand-off
+# latency); not part of the product library
+PROBE_SRC = "floor_probe.hip"
+PROBE_LIB = os.path.join(HERE, "libmoty_probe.so")
+SOURCES = ["quant.hip", "gemv_q8.hip", "ffn1.hip", "gemm_q8.hip", "q4g.hip", "r4.hip", "moe.hip", "ops.hip", "gguf.hip", "api.cpp", "expert_cache.cpp"]
 HEADERS = ["common.h", "kernels.h", "dev.h"]
 
 
@@ -54,8 +58,14 @@ def build(verbose=False):
     if r.returncode != 0:
         raise RuntimeError("link failed: %s\n%s\n%s" % (" ".join(cmd), r.stdout, r.stderr))
     os.replace(tmp, LIB)
+    pobj = _compile(PROBE_SRC)
+    cmd = [hipcc(), "-shared", "-fPIC", "--offload-arch=gfx950", "-o", PROBE_LIB + ".tmp", pobj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("link failed: %s\n%s\n%s" % (" ".join(cmd), r.stdout, r.stderr))
+    os.replace(PROBE_LIB + ".tmp", PROBE_LIB)
     if verbose:
-        print("built", LIB)
+        print("built", LIB, "and", PROBE_LIB)
     return LIB
 
 

@@ -62,6 +62,20 @@ static int dev_init(int d) {
     void* fp = nullptr;
     HIP_TRY(hipGetSymbolAddress(&fp, HIP_SYMBOL(scratch)));
     g_dev[d].fixed_scratch = fp;
+    {
+      // the one-launch FFN's exchange words (9 copies of I <= 4096 words),
+      // per-workgroup call counters and wait-error flag, zeroed once
+      const size_t xb = (9 * 4096) * 8, eb = al256((size_t)g_dev[d].cus * 4);
+      void* p = nullptr;
+      HIP_TRY(hipMalloc(&p, xb + eb + 256));
+      HIP_TRY(hipMemset(p, 0, xb + eb + 256));
+      HIP_TRY(hipDeviceSynchronize());
+      g_dev[d].f1_xh = (unsigned long long*)p;
+      g_dev[d].f1_epoch = (unsigned*)((char*)p + xb);
+      g_dev[d].f1_err = (unsigned*)((char*)p + xb + eb);
+      const char* e = getenv("MOTY_FFN1");
+      g_dev[d].f1_on = e && e[0] == '1';
+    }
     HIP_TRY(hipStreamCreateWithFlags(&g_dev[d].stream, hipStreamNonBlocking));
     g_dev[d].ready = true;
   }
@@ -240,6 +254,24 @@ int moty_hip_shutdown(void) {
 
 const char* moty_hip_last_error(void) { return g_err; }
 const char* moty_hip_kernel_tier(void) { return "gfx950-mfma-i8/gfx950-f32"; }
+
+int moty_hip_wait_errors(int* count) {
+  CUR(d);
+  if (!count) return set_error("wait_errors: count is NULL"), MOTY_EINVAL;
+  unsigned v = 0;
+  HIP_TRY(hipDeviceSynchronize());
+  HIP_TRY(hipMemcpy(&v, d->f1_err, 4, hipMemcpyDeviceToHost));
+  if (v) HIP_TRY(hipMemset(d->f1_err, 0, 4));
+  HIP_TRY(hipDeviceSynchronize());
+  *count = (int)v;
+  return MOTY_OK;
+}
+
+int moty_hip_set_ffn1(int on) {
+  CUR(d);
+  d->f1_on = on != 0;
+  return MOTY_OK;
+}
 
 // ---------------- device-pointer entry points ----------------
 
@@ -420,6 +452,13 @@ int moty_hip_dense_ffn_q8_dev(float* out, const float* x, int S, const int8_t* g
   }
   hipStream_t st = STREAM(stream);
   void* sp;
+  if (S == 1 && d->f1_on && ffn1h_q8_fits(D, I, d->cus)) {
+    // the exchange words and call counters are per-device state shared by
+    // every call: the scratch ordering keeps calls on two streams apart
+    int rc = scratch_get(d, 256, st, &sp);
+    if (rc) return rc;
+    return launch_ffn1h_q8(x, gate, gs, up, us, down, ds, out, D, I, d->cus, d->f1_xh, d->f1_epoch, d->f1_err, st);
+  }
   if (S <= GEMV_MAX_S) {
     int rc = scratch_get(d, al256((size_t)S * I * 4), st, &sp);
     if (rc) return rc;

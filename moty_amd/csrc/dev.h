@@ -33,6 +33,13 @@ struct Dev {
   // device address of this device's copy of the fixed no-allocation
   // scratch array (api.cpp), taken once at set-up
   void* fixed_scratch = nullptr;
+  // one-launch decode FFN: the h exchange words, one call counter per
+  // workgroup of its grid (which is always `cus` workgroups) and the
+  // bounded-wait error flag; allocated and zeroed at set-up
+  unsigned long long* f1_xh = nullptr;
+  unsigned* f1_epoch = nullptr;
+  unsigned* f1_err = nullptr;
+  bool f1_on = true;
   std::unordered_map<const void*, WEntry> wcache;
 };
 

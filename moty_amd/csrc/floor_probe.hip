@@ -1,0 +1,180 @@
+// floor_probe.hip -- measurement support for bench.py (libmoty_probe.so),
+// not part of the product library: what the memory system and the launch
+// path of this GPU allow a decode-sized kernel at best.
+//
+//  * the graph launch floor: an empty kernel (256 x 256 threads) replayed
+//    from a HIP graph, microseconds per launch;
+//  * pure-read floors: a kernel that only streams B bytes with 16-byte
+//    non-temporal loads (one per lane, one wave per 1 KiB) over rotating
+//    copies larger than the Infinity Cache, so every byte comes from HBM;
+//    as one launch per step, and as two launches per step (6.3 + 3.2 MB:
+//    the byte counts of the decode FFN's gate/up and down GEMVs);
+//  * hand-off latency between two workgroups, one way (store issued ->
+//    seen by the polling workgroup), on the same XCD (plain store, device-
+//    scope load) and across XCDs (device-scope store and load).
+// moty_probe_floor writes its figures into out[] in the order of
+// moty_probe_floor_names() and returns 0, or a HIP error code.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <vector>
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+__global__ void k_empty(int* o) {
+  if (threadIdx.x == 4096) o[0] = 1;  // never true: keeps the kernel
+}
+
+__global__ __launch_bounds__(256) void k_read(const int8_t* __restrict__ p, size_t bytes, int* o) {
+  const size_t a = ((size_t)blockIdx.x * 256 + threadIdx.x) * 16;
+  v4i v = {0, 0, 0, 0};
+  if (a < bytes) v = __builtin_nontemporal_load((const v4i*)(p + a));
+  if ((v.x ^ v.y ^ v.z ^ v.w) == 0x7e3a5c11) o[0] = v.x;  // data-dependent, practically never
+}
+
+__device__ __forceinline__ unsigned ld_dev(const unsigned* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// block 0 writes flag = i at a recorded time; block `reader` polls it and
+// records when it sees it, then acknowledges; every wait is bounded
+template <bool PLAIN>
+__global__ void k_handoff(unsigned* flag, unsigned long long* t, int iters, int reader) {
+  if (threadIdx.x) return;
+  const int b = blockIdx.x;
+  if (b != 0 && b != reader) return;
+  unsigned* ack = flag + 64;
+  for (int i = 1; i <= iters; i++) {
+    if (b == 0) {
+      int n = 0;
+      while (ld_dev(ack) != (unsigned)(i - 1) && ++n < 8192) {}
+      if (n >= 8192) break;
+      __builtin_amdgcn_s_sleep(20);
+      t[2 * i] = wall_clock64();
+      if (PLAIN)
+        *(volatile unsigned*)flag = (unsigned)i;
+      else
+        __hip_atomic_store(flag, (unsigned)i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      int n = 0;
+      while (ld_dev(flag) != (unsigned)i && ++n < 8192) {}
+      if (n >= 8192) break;
+      t[2 * i + 1] = wall_clock64();
+      __hip_atomic_store(ack, (unsigned)i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+#define PT(call)                         \
+  do {                                   \
+    hipError_t e_ = (call);              \
+    if (e_ != hipSuccess) return (int)e_; \
+  } while (0)
+
+template <class F>
+int graph_us(hipStream_t st, int n, F f, float* us) {
+  hipGraph_t g;
+  hipGraphExec_t e;
+  PT(hipStreamBeginCapture(st, hipStreamCaptureModeGlobal));
+  for (int i = 0; i < n; i++) f(i);
+  PT(hipStreamEndCapture(st, &g));
+  PT(hipGraphInstantiate(&e, g, nullptr, nullptr, 0));
+  hipEvent_t a, b;
+  PT(hipEventCreate(&a));
+  PT(hipEventCreate(&b));
+  PT(hipGraphLaunch(e, st));
+  PT(hipStreamSynchronize(st));
+  std::vector<float> v;
+  for (int r = 0; r < 7; r++) {
+    PT(hipEventRecord(a, st));
+    PT(hipGraphLaunch(e, st));
+    PT(hipEventRecord(b, st));
+    PT(hipStreamSynchronize(st));
+    float ms;
+    PT(hipEventElapsedTime(&ms, a, b));
+    v.push_back(ms * 1000.f / n);
+  }
+  std::sort(v.begin(), v.end());
+  *us = v[v.size() / 2];
+  PT(hipEventDestroy(a));
+  PT(hipEventDestroy(b));
+  PT(hipGraphExecDestroy(e));
+  PT(hipGraphDestroy(g));
+  return 0;
+}
+
+// median one-way hand-off in ns, or -1 if the flag was not seen
+int handoff_ns(hipStream_t st, bool plain, int reader, float* ns) {
+  const int iters = 200;
+  unsigned* fl;
+  unsigned long long* t;
+  PT(hipMalloc(&fl, 4096));
+  PT(hipMalloc(&t, 8 * 2 * (iters + 1)));
+  PT(hipMemsetAsync(fl, 0, 4096, st));
+  PT(hipMemsetAsync(t, 0, 8 * 2 * (iters + 1), st));
+  if (plain)
+    hipLaunchKernelGGL(k_handoff<true>, dim3(256), dim3(64), 0, st, fl, t, iters, reader);
+  else
+    hipLaunchKernelGGL(k_handoff<false>, dim3(256), dim3(64), 0, st, fl, t, iters, reader);
+  PT(hipGetLastError());
+  PT(hipStreamSynchronize(st));
+  std::vector<unsigned long long> h(2 * (iters + 1));
+  PT(hipMemcpy(h.data(), t, h.size() * 8, hipMemcpyDeviceToHost));
+  std::vector<double> d;
+  for (int i = 10; i <= iters; i++)
+    if (h[2 * i + 1] && h[2 * i]) d.push_back(((long long)h[2 * i + 1] - (long long)h[2 * i]) * 10.0);
+  std::sort(d.begin(), d.end());
+  *ns = d.size() < (size_t)(iters / 2) ? -1.f : (float)d[d.size() / 2];
+  PT(hipFree(fl));
+  PT(hipFree(t));
+  return 0;
+}
+
+const char* kNames =
+    "empty_launch_us,read_6332416B_us,read_3170304B_us,read_9474048B_us,read_pair_6332416B_3170304B_us,"
+    "handoff_same_xcd_ns,handoff_cross_xcd_ns";
+
+}  // namespace
+
+extern "C" const char* moty_probe_floor_names(void) { return kNames; }
+
+extern "C" int moty_probe_floor(float* out) {
+  hipStream_t st;
+  PT(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+  int* o;
+  PT(hipMalloc(&o, 256));
+  const int NCP = 133;
+  const size_t MAXB = 10u << 20;
+  int8_t* big;
+  PT(hipMalloc(&big, NCP * MAXB));
+  PT(hipMemsetAsync(big, 1, NCP * MAXB, st));
+  PT(hipStreamSynchronize(st));
+  auto rd = [&](size_t bytes) {
+    return [=](int i) {
+      const int8_t* p = big + (size_t)(i % NCP) * MAXB;
+      hipLaunchKernelGGL(k_read, dim3((unsigned)((bytes + 4095) / 4096)), dim3(256), 0, st, p, bytes, o);
+    };
+  };
+  int rc;
+  if ((rc = graph_us(st, 266, [&](int) { hipLaunchKernelGGL(k_empty, dim3(256), dim3(256), 0, st, o); }, &out[0])))
+    return rc;
+  const size_t bb[3] = {6332416, 3170304, 9474048};
+  for (int k = 0; k < 3; k++)
+    if ((rc = graph_us(st, 266, rd(bb[k]), &out[1 + k]))) return rc;
+  {
+    auto a = rd(bb[0]), b = rd(bb[1]);
+    float t;
+    if ((rc = graph_us(st, 266, [&](int i) { (i & 1) ? b(i) : a(i); }, &t))) return rc;
+    out[4] = 2 * t;
+  }
+  // block 8 shares block 0's XCD and block 1 is on the next one (workgroups
+  // go round-robin over the 8 XCDs)
+  if ((rc = handoff_ns(st, true, 8, &out[5]))) return rc;
+  if ((rc = handoff_ns(st, false, 1, &out[6]))) return rc;
+  PT(hipFree(big));
+  PT(hipFree(o));
+  PT(hipStreamDestroy(st));
+  return 0;
+}

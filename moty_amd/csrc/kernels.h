@@ -30,6 +30,13 @@ int launch_pack_i4g(const float* w, uint8_t* q4, float* scale, int O, int I, int
 
 int launch_gemv_q8(const float* x, const int8_t* W, const float* scale, const int8_t* W2, const float* scale2,
                    float* y, int S, int I, int O, hipStream_t st);
+// the S = 1 Q8 FFN in one launch of 256 co-resident workgroups (one per CU;
+// nwg must be 256); xh holds 9 * 4096 words and epoch nwg counters, both
+// zeroed once and owned by this launcher from then on
+int ffn1h_q8_fits(int D, int I, int nwg);
+int launch_ffn1h_q8(const float* x, const int8_t* G, const float* gs, const int8_t* U, const float* us,
+                    const int8_t* Dn, const float* ds, float* y, int D, int I, int nwg, unsigned long long* xh,
+                    unsigned* epoch, unsigned* err, hipStream_t st);
 int launch_gemm_q8(const int8_t* xq, const float* sx, const int8_t* W, const float* scale, float* y, int M, int K,
                    int O, hipStream_t st);
 
@@ -90,12 +97,14 @@ struct MoeArgs {
   float* probs_out;
 };
 size_t moe_scratch_size(int T, int D, int E, int K, int I, size_t* offsets);
+// T = 1 with K <= 8 and D, I <= 4096 takes the decode path (routing, then a
+// gate/up GEMV over the routed experts and a down GEMV that combines)
 int launch_moe(const MoeArgs& a, void* scratch, hipStream_t st);
 // The layer in three phases, for callers that act between them (the expert
 // cache): router + top-k + grouping; the expert GEMMs (eslot: expert ->
 // weight slot in a.G/U/Dn and their scales, -1 = skip; null = identity);
 // the combine.  moe_routing gives the device idx [T*K] and counts [E].
-int launch_moe_route(const MoeArgs& a, void* scratch, hipStream_t st);
+int launch_moe_route(const MoeArgs& a, void* scratch, hipStream_t st, bool group = true);
 int launch_moe_experts(const MoeArgs& a, void* scratch, const int* eslot, hipStream_t st);
 int launch_moe_combine(const MoeArgs& a, void* scratch, hipStream_t st);
 void moe_routing(const MoeArgs& a, void* scratch, const int** idx, const int** counts);

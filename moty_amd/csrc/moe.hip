@@ -124,10 +124,11 @@ __device__ __forceinline__ void qrow_row_wave(const float* __restrict__ xr, int 
 }
 
 // Softmax and greedy top-k of one token's logits lg[0..E) (LDS, 16-byte
-// aligned, overwritten with the exponentials) by one wave; writes
-// idx/w[0..K) and, if probs is non-null, probs[0..E).
-__device__ __forceinline__ void route_token_wave(float* lg, int E, int K, int norm, int* __restrict__ idx,
-                                                 float* __restrict__ wout, float* __restrict__ probs) {
+// aligned, overwritten with the exponentials) by one wave; lane kk < K
+// ends with pick kk (*e, *w: expert id and routing weight); probs[0..E)
+// written if non-null.
+__device__ __forceinline__ void route_token_regs(float* lg, int E, int K, int norm, int* e_out, float* w_out,
+                                                 float* __restrict__ probs) {
   constexpr int PV = 4;  // E <= 256
   const int lane = threadIdx.x % MOTY_WAVE;
   float pv[PV];
@@ -190,9 +191,20 @@ __device__ __forceinline__ void route_token_wave(float* lg, int E, int K, int no
     my_w = lane == kk ? wk : my_w;
     ws += wk;  // the normalisation sum, serial over k
   }
+  *e_out = my_e;
+  *w_out = (norm && ws > 0) ? my_w / ws : my_w;
+}
+
+// route_token_regs, then idx/w[0..K) written
+__device__ __forceinline__ void route_token_wave(float* lg, int E, int K, int norm, int* __restrict__ idx,
+                                                 float* __restrict__ wout, float* __restrict__ probs) {
+  int e;
+  float w;
+  route_token_regs(lg, E, K, norm, &e, &w, probs);
+  const int lane = threadIdx.x % MOTY_WAVE;
   if (lane < K) {
-    idx[lane] = my_e;
-    wout[lane] = (norm && ws > 0) ? my_w / ws : my_w;
+    idx[lane] = e;
+    wout[lane] = w;
   }
 }
 
@@ -711,6 +723,278 @@ __global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ y
 }
 
 // ---------------------------------------------------------------------------
+// Decode (T = 1): moty_nn_moe_topk_d1 (nn/moe.c:33-153).  With one token the
+// K routed experts' FFNs are GEMVs over rows nobody else reads, so after the
+// routing (k_router, k_route_topk: the token's int8 row and its K experts)
+// two launches replace the grouping, the two tile GEMMs, the h quantization
+// and the combine:
+//   k_moe_d1_gateup  wave per 4 rows of one routed expert: gate and up rows
+//                    against the token's int8 row, (s*sx)*acc, silu(g)*u
+//                    (nn/moe.c:99-127) -> h [K][I] f32
+//   k_moe_d1_down    each workgroup loads h once, quantizes every expert's row
+//                    into LDS (qrow_i8 per expert, nn/moe.c:129-139), then a
+//                    wave per output row d: the K experts' down dots,
+//                    (ds*sh)*acc (nn/moe.c:146-152), and the weighted sum in
+//                    the reference's order (out = fma(w_k, v_k, out), k in
+//                    top-k order; ascending expert id for nn/moe.c's batch
+//                    order), written once (no per-pair rows, no combine pass).
+constexpr int D1_NW = 4;  // waves per workgroup
+
+__device__ __forceinline__ int4 d1_ldnt16(const int8_t* p) {
+  const v4i v = __builtin_nontemporal_load((const v4i*)p);
+  return int4{v.x, v.y, v.z, v.w};
+}
+
+// Router logits of one token (nn/matmul.c:15-27 -> hw/hw_avx512.h:231-243):
+// a half-wave per expert, lane c carrying FMA chain c (elements c, c+32, ...,
+// s0 for c < 16, s1 for c >= 16) over its whole row loaded up front, then
+// s0 + s1 and the _mm512_reduce_add_ps tree; plus the logit bias.  One wave
+// per workgroup, so the E/2 waves spread over as many CUs.  NPL = D/32.
+template <int NPL>
+__global__ __launch_bounds__(MOTY_WAVE) void k_router_t1(const float* __restrict__ x, const float* __restrict__ Wr,
+                                                         const float* __restrict__ bias, int D, int E,
+                                                         float* __restrict__ logits) {
+  __shared__ __align__(16) float xs[32 * NPL];
+  const int lane = threadIdx.x, c = lane & 31;
+  const int e = blockIdx.x * 2 + (lane >> 5), ec = e < E ? e : E - 1;
+  float w[NPL];
+#pragma unroll
+  for (int j = 0; j < NPL; j++) w[j] = Wr[(int64_t)ec * D + (j * 32 + c < D ? j * 32 + c : 0)];
+  for (int i = lane * 4; i < D; i += MOTY_WAVE * 4) *(float4*)(xs + i) = *(const float4*)(x + i);
+  const float bv = bias ? bias[ec] : 0.f;
+  __syncthreads();
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < NPL; j++)
+    if (j * 32 < D) acc = __fmaf_rn(xs[j * 32 + c], w[j], acc);
+  const float t = acc + __shfl(acc, (lane & 32) + ((c + 16) & 31), 64);  // s0[c] + s1[c]
+  float r = hsum16_half(t, lane & 32);
+  if (bias) r = r + bv;
+  if (c == 0 && e < E) logits[e] = r;
+}
+
+// NC: 1 KiB chunks of a gate/up row (D); lane l takes bytes [c*1024 + 16l, +16).
+// Every wave routes the token itself from the logits (softmax, greedy top-k:
+// the same steps as k_route_topk, a few microseconds less than a launch of its
+// own) and quantizes x in registers (qrow_i8); then the 4 rows of its expert.
+// Workgroup 0's first wave writes idx, w (and the probabilities).
+template <int NC>
+__global__ __launch_bounds__(D1_NW * MOTY_WAVE) void k_moe_d1_gateup(
+    const float* __restrict__ x, const float* __restrict__ logits, int E, int K, int norm,
+    int* __restrict__ idx, float* __restrict__ wout, float* __restrict__ probs,
+    const int8_t* __restrict__ G, const float* __restrict__ GS, const int8_t* __restrict__ U,
+    const float* __restrict__ US, float* __restrict__ h, int D, int I) {
+  __shared__ __align__(16) float lg[D1_NW][256];
+  const int lane = threadIdx.x % MOTY_WAVE, wv = threadIdx.x / MOTY_WAVE;
+  const int gw = blockIdx.x * D1_NW + wv;  // 4-row group over K*I rows
+  const int rpk = (I + 3) / 4;
+  if (gw >= K * rpk) return;  // whole waves; no workgroup barrier in this kernel
+  const int k = gw / rpk, i0 = (gw % rpk) * 4;
+  float4 xv[NC][4];
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    const int kk = c * 1024 + lane * 16;
+#pragma unroll
+    for (int j = 0; j < 4; j++) xv[c][j] = *(const float4*)(x + (kk < D ? kk : 0) + 4 * j);
+  }
+  for (int e = lane; e < E; e += MOTY_WAVE) lg[wv][e] = logits[e];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  int pe;
+  float pw;
+  const bool first = blockIdx.x == 0 && wv == 0;
+  route_token_regs(lg[wv], E, K, norm, &pe, &pw, first ? probs : nullptr);
+  if (first && lane < K) {
+    idx[lane] = pe;
+    wout[lane] = pw;
+  }
+  const int e0 = __builtin_amdgcn_readlane(pe, k);
+  const int e = e0 < 0 ? 0 : e0;  // a round without a candidate: its rows are not used
+  int4 wg[4][NC], wu[4][NC];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int i = i0 + r < I ? i0 + r : I - 1;
+    const int8_t* gr = G + ((int64_t)e * I + i) * D;
+    const int8_t* ur = U + ((int64_t)e * I + i) * D;
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+      const int kk = c * 1024 + lane * 16;
+      wg[r][c] = d1_ldnt16(gr + (kk < D ? kk : 0));
+      wu[r][c] = d1_ldnt16(ur + (kk < D ? kk : 0));
+    }
+  }
+  const int rl = wave_sum_row<4>(lane);
+  const int ir = i0 + rl < I ? i0 + rl : I - 1;
+  const float sg = GS[(int64_t)e * I + ir], su = US[(int64_t)e * I + ir];
+  __builtin_amdgcn_sched_barrier(0);
+  // qrow_i8 of x while the weights fly
+  float amax = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; c++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      xv[c][j] = sel4(c * 1024 + lane * 16 < D, xv[c][j]);
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(xv[c][j].x), fabsf(xv[c][j].y)), fmaxf(fabsf(xv[c][j].z), fabsf(xv[c][j].w))));
+    }
+  amax = wave_max_f32(amax);
+  float sx = amax / 127.f;
+  if (sx < 1e-12f) sx = 1e-12f;
+  const float inv = 1.f / sx;
+  int4 q[NC];
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    int* qp = (int*)&q[c];
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      qp[j] = (int)((uint32_t)(rne_int(xv[c][j].x * inv) & 0xff) | ((uint32_t)(rne_int(xv[c][j].y * inv) & 0xff) << 8) |
+                    ((uint32_t)(rne_int(xv[c][j].z * inv) & 0xff) << 16) |
+                    ((uint32_t)(rne_int(xv[c][j].w * inv) & 0xff) << 24));
+  }
+  int ag[4], au[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    ag[r] = 0;
+    au[r] = 0;
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+      ag[r] = dot16(wg[r][c], q[c], ag[r]);
+      au[r] = dot16(wu[r][c], q[c], au[r]);
+    }
+  }
+  const int a = wave_sum_multi_i32<4>(ag);
+  const int a2 = wave_sum_multi_i32<4>(au);
+  const float v = ref_silu_mul((sg * sx) * (float)a, (su * sx) * (float)a2);
+  if ((lane & 15) == 0 && i0 + rl < I) h[(int64_t)k * I + i0 + rl] = v;
+}
+
+// KC: 1 KiB chunks of a down row (I); RPW output rows per wave; KM >= K
+template <int KC, int RPW, int KM>
+__global__ __launch_bounds__(D1_NW * MOTY_WAVE) void k_moe_d1_down(
+    const int* __restrict__ idx, const float* __restrict__ w, const float* __restrict__ h,
+    const int8_t* __restrict__ Dn, const float* __restrict__ DS, float* __restrict__ out, int D, int I, int K, int E,
+    int order, int* __restrict__ counts) {
+  constexpr int NT = D1_NW * MOTY_WAVE;
+  constexpr int NU = KM * KC * 256;       // float4 units of h (rows padded to KC KiB)
+  constexpr int HJ = (NU + NT - 1) / NT;  // per thread
+  __shared__ __align__(16) int8_t hq_s[KM][KC * 1024];
+  __shared__ unsigned amax_s[KM];
+  __shared__ float sh_s[KM], w_s[KM];
+  __shared__ int e_s[KM], k_s[KM];
+  const int lane = threadIdx.x % MOTY_WAVE, wv = threadIdx.x / MOTY_WAVE;
+  const int d0 = (blockIdx.x * D1_NW + wv) * RPW;
+  // the routed experts in combine order: k order, or ascending expert id
+  // (the K ids of a token are distinct); rank j holds expert e_s[j], whose
+  // h row is k_s[j]
+  if (threadIdx.x < MOTY_WAVE) {
+    const int k = threadIdx.x;
+    const int e = k < K ? idx[k] : 0x7fffffff;
+    int rank = k;
+    if (order == 1) {
+      rank = 0;
+      for (int j = 0; j < K; j++) rank += (__shfl(e, j, 64) < e) ? 1 : 0;
+    }
+    if (k < K) {
+      e_s[rank] = e;
+      k_s[rank] = k;
+      w_s[rank] = w[k];
+    }
+    if (k < KM) amax_s[k] = 0u;
+  }
+  __syncthreads();
+  // every routed expert's h row first (small and cache-resident: it lands
+  // before the weight stream and its quantization overlaps it), then this
+  // wave's down rows of every routed expert (rows clamped, experts past K
+  // repeat rank 0's and are not used; columns past I meet zero codes), with
+  // their row scales
+  float4 hv[HJ];
+#pragma unroll
+  for (int j = 0; j < HJ; j++) {
+    const int u = threadIdx.x + j * NT, row = u / (KC * 256), col = (u % (KC * 256)) * 4;
+    const bool in = row < K && col < I;
+    const float4 v = *(const float4*)(h + (in ? (int64_t)k_s[row] * I + col : 0));
+    hv[j] = sel4(in, v);
+  }
+  int4 wd[RPW][KM][KC];
+  float dsc[RPW][KM];
+#pragma unroll
+  for (int j = 0; j < KM; j++) {
+    const int e0 = e_s[j < K ? j : 0], e = e0 < 0 ? 0 : e0;
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+      const int d = d0 + r < D ? d0 + r : D - 1;
+      const int8_t* dr = Dn + ((int64_t)e * D + d) * I;
+#pragma unroll
+      for (int c = 0; c < KC; c++) {
+        const int kk = c * 1024 + lane * 16;
+        wd[r][j][c] = d1_ldnt16(dr + (kk < I ? kk : 0));
+      }
+      dsc[r][j] = DS[(int64_t)e * D + d];
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < HJ; j++) {
+    const int u = threadIdx.x + j * NT, row = u / (KC * 256);
+    const float4 v = hv[j];
+    // fmaxf drops NaN as the reference's `a > amax` does
+    const float m = fmaxf(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))), 0.f);
+    if (row < K) atomicMax(&amax_s[row], __float_as_uint(m));
+  }
+  __syncthreads();
+  if (threadIdx.x < KM) {
+    float sc = __uint_as_float(amax_s[threadIdx.x]) / 127.f;
+    if (sc < 1e-12f) sc = 1e-12f;
+    sh_s[threadIdx.x] = sc;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < HJ; j++) {
+    const int u = threadIdx.x + j * NT, row = u / (KC * 256), col = (u % (KC * 256)) * 4;
+    if (row < KM) {
+      const float inv = 1.f / sh_s[row];
+      const float4 v = hv[j];
+      *(uint32_t*)(&hq_s[row][col]) =
+          (uint32_t)(rne_int(v.x * inv) & 0xff) | ((uint32_t)(rne_int(v.y * inv) & 0xff) << 8) |
+          ((uint32_t)(rne_int(v.z * inv) & 0xff) << 16) | ((uint32_t)(rne_int(v.w * inv) & 0xff) << 24);
+    }
+  }
+  __syncthreads();
+  if (blockIdx.x == 0 && counts && threadIdx.x < E) {
+    int c = 0;
+    for (int j = 0; j < K; j++) c += e_s[j] == (int)threadIdx.x;
+    counts[threadIdx.x] = c;
+  }
+  // per row: the K experts' dots, (ds*sh)*acc, then the ordered weighted
+  // sum out = fma(w, v, out) from 0 (nn/moe.c:146-152 and 200-202)
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    int acc[KM];
+#pragma unroll
+    for (int j = 0; j < KM; j++) {
+      acc[j] = 0;
+#pragma unroll
+      for (int c = 0; c < KC; c++)
+        acc[j] = dot16(wd[r][j][c], *(const int4*)(&hq_s[j][c * 1024 + lane * 16]), acc[j]);
+    }
+    float o = 0.f;
+#pragma unroll
+    for (int j0 = 0; j0 < KM; j0 += 4) {
+      const int a4[4] = {acc[j0], acc[j0 + 1], acc[j0 + 2], acc[j0 + 3]};
+      const int a = wave_sum_multi_i32<4>(a4);  // lanes 0, 32, 16, 48 hold experts j0 + 0, 1, 2, 3
+      const int tot[4] = {__builtin_amdgcn_readlane(a, 0), __builtin_amdgcn_readlane(a, 32),
+                          __builtin_amdgcn_readlane(a, 16), __builtin_amdgcn_readlane(a, 48)};
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int j = j0 + q;
+        if (j < K && e_s[j] >= 0) o = __fmaf_rn(w_s[j], (dsc[r][j] * sh_s[j]) * (float)tot[q], o);
+      }
+    }
+    if (lane == 0 && d0 + r < D) out[d0 + r] = o;
+  }
+}
+
+// ---------------------------------------------------------------------------
 size_t moe_scratch_size(int T, int D, int E, int K, int I, size_t* offsets) {
   const int64_t P = (int64_t)T * K;
   const int64_t maxt = P / MOE_BM + E + 1;
@@ -767,7 +1051,7 @@ void moe_routing(const MoeArgs& a, void* scratch, const int** idx, const int** c
   *counts = m.counts;
 }
 
-int launch_moe_route(const MoeArgs& a, void* scratch, hipStream_t st) {
+int launch_moe_route(const MoeArgs& a, void* scratch, hipStream_t st, bool group) {
   const int T = a.T, D = a.D, E = a.E, K = a.K, I = a.I;
   if (K < 1 || K > 64 || K > E || E > 256 || (D % 32) || (I % 32) || (D % 4)) return MOTY_EUNSUP;
   const MoeBufs m = moe_bufs(a, scratch);
@@ -797,6 +1081,7 @@ int launch_moe_route(const MoeArgs& a, void* scratch, hipStream_t st) {
   hipLaunchKernelGGL(k_route_topk, dim3((T + TK_TOK - 1) / TK_TOK), dim3(TK_TOK * 128), 0, st, a.x, m.logits, T, D, E,
                      K, a.norm, m.idx, m.w, m.xq, m.sx, a.probs_out);
   LAUNCH_TRY("k_route_topk");
+  if (!group) return MOTY_OK;
   const int mt = moe_mt(a);
   {
     // one workgroup per GR_CHUNK pairs, at most 32 (each one reads all P
@@ -847,8 +1132,61 @@ int launch_moe_combine(const MoeArgs& a, void* scratch, hipStream_t st) {
   return MOTY_OK;
 }
 
+// the decode path's shapes: one token, K <= 8 experts of E <= 256, D and I
+// <= 4 KiB rows (D % 32 == 0 as the routing requires)
+static bool moe_d1(const MoeArgs& a) {
+  return a.T == 1 && a.K >= 1 && a.K <= 8 && a.K <= a.E && a.E <= 256 && a.D <= 4096 && a.I <= 4096 &&
+         a.D % 32 == 0 && a.I % 32 == 0;
+}
+
+static int launch_moe_d1(const MoeArgs& a, void* scratch, hipStream_t st) {
+  const MoeBufs m = moe_bufs(a, scratch);
+  const int D = a.D, I = a.I, K = a.K, E = a.E;
+#define RT(N)                                                                                                \
+  case N:                                                                                                    \
+    hipLaunchKernelGGL((k_router_t1<N>), dim3((E + 1) / 2), dim3(MOTY_WAVE), 0, st, a.x, a.Wr, a.bias, D, E,   \
+                       m.logits);                                                                            \
+    break;
+  switch ((D / 32 + 15) / 16 * 16) {
+    RT(16) RT(32) RT(48) RT(64) RT(80) RT(96) RT(112) RT(128)
+    default: return MOTY_EUNSUP;
+  }
+#undef RT
+  LAUNCH_TRY("k_router_t1");
+  const int nc = (D + 1023) / 1024, kc = (I + 1023) / 1024;
+  const unsigned gu_blocks = (unsigned)((K * ((I + 3) / 4) + D1_NW - 1) / D1_NW);
+#define GU(N)                                                                                                  \
+  case N:                                                                                                      \
+    hipLaunchKernelGGL((k_moe_d1_gateup<N>), dim3(gu_blocks), dim3(D1_NW * MOTY_WAVE), 0, st, a.x, m.logits, E, K, \
+                       a.norm, m.idx, m.w, a.probs_out, a.G, a.GS, a.U, a.US, m.h, D, I);                    \
+    break;
+  switch (nc) {
+    GU(1) GU(2) GU(3) GU(4)
+    default: return MOTY_EUNSUP;
+  }
+#undef GU
+  LAUNCH_TRY("k_moe_d1_gateup");
+  // two rows per wave (one per wave when that leaves fewer than 256
+  // workgroups)
+  const int rpw = D / (2 * D1_NW) >= 256 ? 2 : 1;
+  const unsigned dn_blocks = (unsigned)((D + rpw * D1_NW - 1) / (rpw * D1_NW));
+#define DN(KC, R)                                                                                             \
+  if (kc == KC && rpw == R) {                                                                                 \
+    hipLaunchKernelGGL((k_moe_d1_down<KC, R, 8>), dim3(dn_blocks), dim3(D1_NW * MOTY_WAVE), 0, st, m.idx, m.w,  \
+                       m.h, a.Dn, a.DS, a.out, D, I, K, a.E, a.order, m.counts);                               \
+    LAUNCH_TRY("k_moe_d1_down");                                                                              \
+  }
+  DN(1, 1) DN(1, 2) DN(2, 1) DN(2, 2) DN(3, 1) DN(3, 2) DN(4, 1) DN(4, 2)
+#undef DN
+  if (a.idx_out) HIP_TRY(hipMemcpyAsync(a.idx_out, m.idx, (size_t)K * 4, hipMemcpyDeviceToDevice, st));
+  if (a.w_out) HIP_TRY(hipMemcpyAsync(a.w_out, m.w, (size_t)K * 4, hipMemcpyDeviceToDevice, st));
+  if (a.counts_out) HIP_TRY(hipMemcpyAsync(a.counts_out, m.counts, (size_t)a.E * 4, hipMemcpyDeviceToDevice, st));
+  return MOTY_OK;
+}
+
 int launch_moe(const MoeArgs& a, void* scratch, hipStream_t st) {
   if (a.T <= 0) return MOTY_OK;
+  if (moe_d1(a)) return launch_moe_d1(a, scratch, st);
   int rc = launch_moe_route(a, scratch, st);
   if (!rc) rc = launch_moe_experts(a, scratch, nullptr, st);
   if (!rc) rc = launch_moe_combine(a, scratch, st);

@@ -299,3 +299,17 @@ class MoeLayer:
         if want_routing:
             return y, idx, w, cnt
         return y
+
+
+def wait_errors():
+    """Calls since the last query whose bounded device wait ran out (the
+    one-launch decode FFN); 0 means every output since then is valid."""
+    n = C.c_int(0)
+    check(lib().moty_hip_wait_errors(C.byref(n)), "wait_errors")
+    return n.value
+
+
+def set_ffn1(on):
+    """Route the S = 1 Q8 dense FFN through its one-launch form (on) or the
+    two GEMV launches (off); the results are the same bits."""
+    check(lib().moty_hip_set_ffn1(int(bool(on))), "set_ffn1")

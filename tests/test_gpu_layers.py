@@ -71,6 +71,51 @@ def test_dense_ffn_decode_repeated_and_graph(ops):
             assert same_bits(to_np(o), r), "replay %d" % rep
 
 
+@pytest.mark.parametrize("D,I", [(1024, 3072), (1024, 1024), (2048, 4096), (2048, 2048), (1024, 4096)])
+def test_dense_ffn_q8_one_launch(ops, D, I):
+    # the one-launch decode FFN (workgroups exchanging h through device
+    # memory) against the oracle: several calls in a row on rotating inputs
+    # (the per-workgroup call counters advance), then graph replays with
+    # eager calls between them; no bounded wait may run out
+    say("ffn one-launch", D, I)
+    G, GS = q8(11, (I, D))
+    U, US = q8(12, (I, D))
+    Dn, DS = q8(13, (D, I))
+    xs = [randn(50 + k, (1, D)) * (k + 1) for k in range(3)]
+    xs.append(np.zeros((1, D), np.float32))  # all-zero h: the 1e-12 scale floor
+    ref = [o_dense_ffn_q8(x, G, GS, U, US, Dn, DS) for x in xs]
+    w = [to_dev(a) for a in (G, GS, U, US, Dn, DS)]
+    xd = [to_dev(x) for x in xs]
+    outs = [torch.empty((1, D), device="cuda:0") for _ in xs]
+    ops.set_ffn1(1)
+    try:
+        assert ops.wait_errors() == 0
+        for _ in range(6):
+            for x, o in zip(xd, outs):
+                ops.dense_ffn_q8(x, *w, out=o)
+        for o, r in zip(outs, ref):
+            assert same_bits(to_np(o), r), mismatch(to_np(o), r)
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g):
+                for x, o in zip(xd, outs):
+                    ops.dense_ffn_q8(x, *w, out=o)
+        torch.cuda.current_stream().wait_stream(s)
+        for rep in range(4):
+            for o in outs:
+                o.zero_()
+            g.replay()
+            ops.dense_ffn_q8(xd[0], *w, out=outs[0])
+            torch.cuda.synchronize()
+            for o, r in zip(outs, ref):
+                assert same_bits(to_np(o), r), "replay %d" % rep
+        assert ops.wait_errors() == 0
+    finally:
+        ops.set_ffn1(0)
+
+
 def moe_weights(E, I, D, seed=10):
     G, GS = q8(seed, (E, I, D))
     U, US = q8(seed + 1, (E, I, D))
