@@ -190,7 +190,7 @@ void moty_hip_hw_matmul_i8(float *y, const float *x, const int8_t *q, const floa
 /* moty_matmul_i4_s (nn/nn_matmul.h:66, nn/matmul.c:75-145), per-row int4
  * weights (WF_I4): q4 [O][(I+1)/2] nibbles (even element low) + f32 scale
  * [O].  IDOT4 read from the environment once, as nn/matmul.c:76-77.
- * Served for I % 16 == 0. */
+ * Served for I % 16 == 0 (q4 8-byte, x 16-byte aligned). */
 int moty_hip_matmul_i4_s(float *y, const float *x, const uint8_t *q4, const float *scale, int S, int I, int O);
 /* HwBackend.matmul_i4 slot (hw/hw_backend.h:59-60), void: on failure every
  * y[S*O] is a quiet NaN and moty_hip_last_error() says why. */
@@ -295,11 +295,17 @@ int moty_hip_moe_topk_dev(const MotyHipMoe *m, const float *x, int S, float *out
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  The MoE layer of moty_hip_moe_topk_dev, bit for bit, with its
  * scratch in a fixed 64 MiB device array the library holds per GPU until
- * the process ends (taken at moty_hip_init or the first call on a device);
- * it calls no hipMalloc/hipFree.  Shapes whose scratch exceeds 64 MiB
- * return MOTY_HIP_EINVAL (the OLMoE layer fits up to T = 256 tokens: about
- * 27 MiB).  Every call on one GPU shares that array: calls that overlap on
- * one GPU (several streams or host threads at once) race. */
+ * the process ends.  Its set-up (the array's device address, one event) is
+ * done by moty_hip_init, which the calling thread must have called first
+ * (it allocates; this entry point returns MOTY_HIP_EINVAL otherwise); the
+ * call itself does no hipMalloc/hipFree.  Shapes whose scratch exceeds
+ * 64 MiB return MOTY_HIP_EINVAL (the OLMoE layer fits up to T = 256 tokens:
+ * about 27 MiB).  Every call on one GPU shares that array.  Sequential calls
+ * are ordered on the device even across streams: a call on another stream
+ * than the previous call's waits for that call's work (an event recorded
+ * after each call; not under graph capture, where the caller orders
+ * replays).  Calls that overlap in time on one GPU (several host threads at
+ * once) race. */
 int moty_hip_moe_topk_noalloc_dev(const MotyHipMoe *m, const float *x, int S, float *out, void *stream);
 /* the cached layer with m's router/bias/outputs and x/out on the device;
  * synchronises `stream` once (the routing read-back) */

@@ -62,6 +62,7 @@ static int dev_init(int d) {
     void* fp = nullptr;
     HIP_TRY(hipGetSymbolAddress(&fp, HIP_SYMBOL(scratch)));
     g_dev[d].fixed_scratch = fp;
+    HIP_TRY(hipEventCreateWithFlags(&g_dev[d].fx_ev, hipEventDisableTiming));
     {
       // the one-launch FFN's exchange words (9 copies of I <= 4096 words),
       // per-workgroup call counters and wait-error flag, zeroed once
@@ -125,22 +126,30 @@ static bool capturing(hipStream_t st) {
 }
 
 int scratch_get(Dev* d, size_t bytes, hipStream_t st, void** p) {
-  if (d->scr_used && d->scr_stream != st && !capturing(st) && !capturing(d->scr_stream)) {
-    if (!d->scr_ev) HIP_TRY(hipEventCreateWithFlags(&d->scr_ev, hipEventDisableTiming));
-    // every call queues its work before returning, so recording on the
-    // previous stream now marks the end of the work that used the arena
-    if (hipEventRecord(d->scr_ev, d->scr_stream) == hipSuccess) {
-      HIP_TRY(hipStreamWaitEvent(st, d->scr_ev, 0));
-    } else {
-      (void)hipGetLastError();  // the previous stream is gone: wait for everything instead
-      HIP_TRY(hipDeviceSynchronize());
-    }
-  }
+  if (d->scr_used && d->scr_stream != st && d->scr_ev_ok && !capturing(st))
+    HIP_TRY(hipStreamWaitEvent(st, d->scr_ev, 0));
   int rc = arena_get(d->scratch, bytes, p);
   if (rc) return rc;
   d->scr_stream = st;
   d->scr_used = true;
+  d->scr_pend = true;
   return MOTY_OK;
+}
+
+void scratch_mark(Dev* d) {
+  d->scr_pend = false;
+  d->scr_ev_ok = false;
+  if (capturing(d->scr_stream)) return;
+  if (!d->scr_ev && hipEventCreateWithFlags(&d->scr_ev, hipEventDisableTiming) != hipSuccess) {
+    d->scr_ev = nullptr;
+    return;
+  }
+  // a failed record leaves scr_ev_ok false: the next call on another stream
+  // then runs unordered, so synchronise here instead
+  if (hipEventRecord(d->scr_ev, d->scr_stream) == hipSuccess)
+    d->scr_ev_ok = true;
+  else
+    (void)hipDeviceSynchronize();
 }
 
 // Fingerprint of a host buffer from 64 evenly spaced 16-byte samples (the
@@ -244,7 +253,11 @@ int moty_hip_shutdown(void) {
     d.stream = nullptr;
     if (d.scr_ev) hipEventDestroy(d.scr_ev);
     d.scr_ev = nullptr;
-    d.scr_used = false;
+    d.scr_used = d.scr_pend = d.scr_ev_ok = false;
+    if (d.fx_ev) hipEventDestroy(d.fx_ev);
+    d.fx_ev = nullptr;
+    d.fx_used = d.fx_ev_ok = false;
+    d.fx_stream = nullptr;
     d.scr_stream = nullptr;
     d.ready = false;
   }
@@ -337,7 +350,7 @@ int moty_hip_matmul_i4_grouped_s_dev(float* y, const float* x, const uint8_t* q4
   if (idot4 && gs == 32 && (I % 64) == 0 && I <= 16384) {
     if (S <= 4) return launch_gemv_i4g(x, q4, scale, nullptr, nullptr, y, S, I, O, st);
     void* sp;
-    if ((I % 128) == 0 && !(((uintptr_t)x | (uintptr_t)q4 | (uintptr_t)scale) & 15)) {
+    if (gemm_i4g_h_fits(S, I, O) && !(((uintptr_t)x | (uintptr_t)q4 | (uintptr_t)scale) & 15)) {
       // f16 codes + f16 MFMA: one FMA per output and group in the epilogue
       const size_t hb = al256((size_t)S * I * 2);
       int rc = scratch_get(d, hb + al256((size_t)S * 4), st, &sp);
@@ -367,30 +380,29 @@ int moty_hip_pack_int4_dev(const float* w, uint8_t* q4, float* scale, int O, int
   return launch_pack_i4row(w, q4, scale, O, I, STREAM(stream));
 }
 
-// moty_matmul_i4_s (nn/matmul.c:75-145), per-row int4 weights.  IDOT4: the
-// nibbles expand to int8 codes n - 8 in scratch and the Q8 kernels run the
-// integer dot with the same (scale*sx)*acc epilogue; otherwise the exact
-// f32 path.  I % 16 == 0 (the AVX2 step of the f32 path; other widths stay
-// on the CPU).
+// moty_matmul_i4_s (nn/matmul.c:75-145), per-row int4 weights.  IDOT4:
+// x is quantized per row (qrow_i8) into scratch and k_i4row_idot runs the
+// integer dot straight from the nibbles with the (scale*sx)*acc epilogue;
+// otherwise the exact f32 path.  I % 16 == 0 (the AVX2 step of the f32 path;
+// other widths stay on the CPU); q4 8-byte and x 16-byte aligned.
 int moty_hip_matmul_i4_s_dev(float* y, const float* x, const uint8_t* q4, const float* scale, int S, int I, int O,
                              int idot4, void* stream) {
   CUR(d);
   if (S < 0 || I <= 0 || O < 0 || !y || !x || !q4 || !scale) return set_error("matmul_i4_s: bad arguments"), MOTY_EINVAL;
   if (S == 0 || O == 0) return MOTY_OK;
   if (I % 16) return set_error("matmul_i4_s: I=%d unsupported (I %% 16 == 0)", I), MOTY_EUNSUP;
+  if ((((uintptr_t)q4) & 7) || (((uintptr_t)x) & 15))
+    return set_error("matmul_i4_s: q4 must be 8-byte and x 16-byte aligned"), MOTY_EUNSUP;
   hipStream_t st = STREAM(stream);
   if (!idot4 || I > 16384) return launch_i4row_f32(x, q4, scale, y, S, I, O, st);
-  const size_t bw = al256((size_t)O * I), bx = al256((size_t)S * I);
+  const size_t bx = al256((size_t)S * I);
   void* sp;
-  int rc = scratch_get(d, bw + bx + al256((size_t)S * 4), st, &sp);
+  int rc = scratch_get(d, bx + al256((size_t)S * 4), st, &sp);
   if (rc) return rc;
-  int8_t* w8 = (int8_t*)sp;
-  if ((rc = launch_i4row_to_i8(q4, w8, (int64_t)O * I, st))) return rc;
-  if (S <= GEMV_MAX_S) return launch_gemv_q8(x, w8, scale, nullptr, nullptr, y, S, I, O, st);
-  int8_t* xq = (int8_t*)sp + bw;
-  float* sx = (float*)((char*)sp + bw + bx);
+  int8_t* xq = (int8_t*)sp;
+  float* sx = (float*)((char*)sp + bx);
   if ((rc = launch_qrow_i8(x, xq, sx, nullptr, S, I, I, I, st))) return rc;
-  return launch_gemm_q8(xq, sx, w8, scale, y, S, I, O, st);
+  return launch_i4row_idot(xq, sx, q4, scale, y, S, I, O, st);
 }
 
 int moty_hip_matmul_dev(float* y, const float* x, const float* W, int S, int I, int O, void* stream) {
@@ -534,7 +546,7 @@ int moty_hip_dense_ffn_i4g_dev(float* out, const float* x, int S, const uint8_t*
   if ((D % 32) || (I % 32)) return set_error("dense_ffn_i4g: D=%d I=%d must be multiples of 32", D, I), MOTY_EUNSUP;
   hipStream_t st = STREAM(stream);
   const bool vec = idot4 && (D % 64) == 0 && (I % 64) == 0 && D <= 16384 && I <= 16384;  // both matrices
-  const bool h16 = vec && S > 4 && (D % 128) == 0 && (I % 128) == 0 &&
+  const bool h16 = vec && S > 4 && gemm_i4g_h_fits(S, D, I) && gemm_i4g_h_fits(S, I, D) &&
                    !(((uintptr_t)x | (uintptr_t)gate | (uintptr_t)gs | (uintptr_t)up | (uintptr_t)us |
                       (uintptr_t)down | (uintptr_t)ds) & 15);
   const int W = D > I ? D : I;
@@ -588,8 +600,15 @@ int moty_hip_moe_topk_dev(const MotyHipMoe* m, const float* x, int S, float* out
 }
 
 // The MoE layer of moty_hip_moe_topk_dev on the fixed device scratch array:
-// no allocation of any kind, for callers that cannot allocate.
+// no allocation of any kind, for callers that cannot allocate.  The device
+// must have been set up on this thread by moty_hip_init (which allocates);
+// a call on another stream than the previous one first waits, on the device,
+// for the previous call's work (an event recorded after each call), so
+// sequential calls on different streams do not race.
 int moty_hip_moe_topk_noalloc_dev(const MotyHipMoe* m, const float* x, int S, float* out, void* stream) {
+  if (t_dev < 0 || !g_dev[t_dev].ready)
+    return set_error("moe_topk_noalloc: call moty_hip_init on this thread first (it does the set-up that allocates)"),
+           MOTY_EINVAL;
   CUR(d);
   int rc = moe_check(m, x, out, S, "moe_topk_noalloc");
   if (rc || S == 0) return rc;
@@ -600,9 +619,16 @@ int moty_hip_moe_topk_noalloc_dev(const MotyHipMoe* m, const float* x, int S, fl
               m->E, m->K, m->I, m->D, need, FIXED_SCRATCH_BYTES);
     return MOTY_EINVAL;
   }
-  if (!d->fixed_scratch) return set_error("moe_topk_noalloc: fixed scratch has no device address"), MOTY_EHIP;
-  rc = launch_moe(moe_args(m, x, S, out), d->fixed_scratch, STREAM(stream));
+  if (!d->fixed_scratch || !d->fx_ev)
+    return set_error("moe_topk_noalloc: fixed scratch has no device address"), MOTY_EHIP;
+  hipStream_t st = STREAM(stream);
+  const bool cap = capturing(st);
+  if (d->fx_used && d->fx_stream != st && d->fx_ev_ok && !cap) HIP_TRY(hipStreamWaitEvent(st, d->fx_ev, 0));
+  rc = launch_moe(moe_args(m, x, S, out), d->fixed_scratch, st);
   if (rc == MOTY_EUNSUP) set_error("moe_topk_noalloc: unsupported shape");
+  d->fx_used = true;
+  d->fx_stream = st;
+  d->fx_ev_ok = !cap && hipEventRecord(d->fx_ev, st) == hipSuccess;
   return rc;
 }
 
@@ -700,7 +726,21 @@ static int r4_gate_up(bool q8, const char* what, float* h, const float* x, const
   CUR(d);
   if (D <= 0 || I <= 0 || !h || !x || !gu || !s16) return set_error("%s: bad arguments", what), MOTY_EINVAL;
   if (D % 32 || I % 4) return set_error("%s: D=%d (multiple of 32), I=%d (multiple of 4)", what, D, I), MOTY_EINVAL;
-  const int rc = launch_r4_gate_up_silu(q8, x, gu, s16, h, D, I, STREAM(stream));
+  hipStream_t st = STREAM(stream);
+  int rc = launch_r4_gate_up_silu(q8, x, gu, s16, h, D, I, st);
+  if (rc != MOTY_EUNSUP) return rc;
+  // widths the fused GEMV does not hold in registers (Q8R4 past D = 4096):
+  // the plain R4 matmul over all 2I rows into scratch, then SiLU(g)*u --
+  // the same results, one more pass over 2I floats
+  const size_t bgu = al256((size_t)2 * I * 4), bq = al256((size_t)D), bs = al256((size_t)(D / 32) * 4);
+  void* sp;
+  if ((rc = scratch_get(d, bgu + bq + 2 * bs, st, &sp))) return rc;
+  float* g2 = (float*)sp;
+  int8_t* xq = (int8_t*)((char*)sp + bgu);
+  float* xs = (float*)((char*)sp + bgu + bq);
+  int32_t* xm = (int32_t*)((char*)sp + bgu + bq + bs);
+  if ((rc = launch_r4_matmul(q8, x, gu, s16, g2, 1, D, 2 * I, xq, xs, xm, st)) == MOTY_OK)
+    rc = launch_silu_rows(h, g2, 1, I, st);
   if (rc == MOTY_EUNSUP) set_error("%s: D=%d unsupported", what, D);
   return rc;
 }

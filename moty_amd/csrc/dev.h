@@ -25,14 +25,21 @@ struct Dev {
   int cus = 0;  // compute units
   hipStream_t stream = nullptr;
   Arena scratch, io;
-  // the stream whose queued work last used `scratch`, and an event used to
-  // order a later call on another stream behind that work
+  // the stream whose queued work last used `scratch`, and an event recorded
+  // on it when that call returned (after its work was queued) that orders a
+  // later call on another stream behind that work; scr_pend: a call took the
+  // arena and has not returned yet; scr_ev_ok: scr_ev marks the last use
+  // (false when that use was under graph capture)
   hipStream_t scr_stream = nullptr;
-  bool scr_used = false;
+  bool scr_used = false, scr_pend = false, scr_ev_ok = false;
   hipEvent_t scr_ev = nullptr;
   // device address of this device's copy of the fixed no-allocation
-  // scratch array (api.cpp), taken once at set-up
+  // scratch array (api.cpp), taken once at set-up, and the same ordering
+  // state for it (event created at set-up)
   void* fixed_scratch = nullptr;
+  hipStream_t fx_stream = nullptr;
+  bool fx_used = false, fx_ev_ok = false;
+  hipEvent_t fx_ev = nullptr;
   // one-launch decode FFN: the h exchange words, one call counter per
   // workgroup of its grid (which is always `cus` workgroups) and the
   // bounded-wait error flag; allocated and zeroed at set-up
@@ -52,6 +59,15 @@ int arena_get(Arena& a, size_t bytes, void** p);
 // (calls on one device share the arena, so two streams must not overlap in
 // it).  Streams under graph capture are left unordered.
 int scratch_get(Dev* d, size_t bytes, hipStream_t st, void** p);
+// Called as an entry point returns (ScrGuard): when it took the scratch
+// arena, record scr_ev on its stream, behind the work it queued.
+void scratch_mark(Dev* d);
+struct ScrGuard {
+  Dev* d;
+  ~ScrGuard() {
+    if (d && d->scr_pend) scratch_mark(d);
+  }
+};
 // Stage host x into the transfer arena (device x and y returned), and copy
 // y back and synchronise.
 int stage_io(Dev* d, const void* x, size_t xbytes, size_t ybytes, void** dx, void** dy);
@@ -66,5 +82,6 @@ inline size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
   {                      \
     int _rc = moty::cur(&d); \
     if (_rc) return _rc; \
-  }
+  }                      \
+  moty::ScrGuard _scr_guard{d};
 #define STREAM(s) ((hipStream_t)(s))

@@ -21,7 +21,8 @@ int launch_qrow_f16p(const float* x, uint16_t* xh, float* sx, int S, int I, int 
 // per-row int4 weights (WF_I4, nn/quant.c:34-55) and their expansion to
 // int8 codes n - 8 (I % 16 == 0; n = O * I codes)
 int launch_pack_i4row(const float* w, uint8_t* q4, float* scale, int O, int I, hipStream_t st);
-int launch_i4row_to_i8(const uint8_t* q4, int8_t* q8, int64_t n, hipStream_t st);
+int launch_i4row_idot(const int8_t* xq, const float* sx, const uint8_t* q4, const float* scale, float* y, int S,
+                      int I, int O, hipStream_t st);
 // the exact f32 path of moty_matmul_i4_s (I % 16 == 0)
 int launch_i4row_f32(const float* x, const uint8_t* q4, const float* scale, float* y, int S, int I, int O,
                      hipStream_t st);
@@ -48,6 +49,7 @@ int launch_gemm_i4g(const int8_t* xq, const float* sx, const uint8_t* q4, const 
 // the same GEMM on f16 MFMA over activations from launch_qrow_f16p;
 // q4b/sclb non-null: PAIR, y = silu(x.q4^T) * (x.q4b^T).  MOTY_EUNSUP when
 // I % 128 != 0 or a pointer is not 16-byte aligned
+bool gemm_i4g_h_fits(int M, int I, int O);
 int launch_gemm_i4g_h(const uint16_t* xh, const float* sx, const uint8_t* q4, const float* scl, const uint8_t* q4b,
                       const float* sclb, float* y, int M, int I, int O, hipStream_t st);
 // 1 when launch_gemm_i4g_h runs its 16 x 16 form at this shape: its

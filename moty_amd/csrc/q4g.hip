@@ -771,11 +771,16 @@ static bool gemm_i4g_h_big(int M, int O) { return (int64_t)((M + 127) / 128) * (
 static bool gemm_i4g_h_full(int M, int O) { return (int64_t)((M + 127) / 128) * ((O + 127) / 128) >= 256; }
 int gemm_i4g_h_f8(int M, int O, bool pair) { return !pair && !gemm_i4g_h_big(M, O); }
 
+// the f16 GEMM's 32-bit buffer offsets: activations and nibbles under 4 GiB
+bool gemm_i4g_h_fits(int M, int I, int O) {
+  return (I % 128) == 0 && (int64_t)M * I * 2 < ((int64_t)1 << 32) && (int64_t)O * I / 2 < ((int64_t)1 << 32);
+}
+
 int launch_gemm_i4g_h(const uint16_t* xh, const float* sx, const uint8_t* q4, const float* scl, const uint8_t* q4b,
                       const float* sclb, float* y, int M, int I, int O, hipStream_t st) {
   if ((I % 128) || ((((uintptr_t)xh) | ((uintptr_t)q4) | ((uintptr_t)scl) | ((uintptr_t)q4b) | ((uintptr_t)sclb)) & 15))
     return MOTY_EUNSUP;
-  if ((int64_t)M * I * 2 >= ((int64_t)1 << 32) || (int64_t)O * I / 2 >= ((int64_t)1 << 32)) return MOTY_EUNSUP;
+  if (!gemm_i4g_h_fits(M, I, O)) return MOTY_EUNSUP;
   if (M <= 0 || O <= 0) return MOTY_OK;
   const bool big = gemm_i4g_h_big(M, O);
 #define Q4H(BM, BN, S, WGM, NW, P, T16)                                                                         \
@@ -873,7 +878,7 @@ __global__ __launch_bounds__(256) void k_i4row_f32(const float* __restrict__ x, 
 
 int launch_i4row_f32(const float* x, const uint8_t* q4, const float* scale, float* y, int S, int I, int O,
                      hipStream_t st) {
-  if (I % 16) return MOTY_EUNSUP;
+  if (I % 16 || (((uintptr_t)q4) & 7) || (((uintptr_t)x) & 15)) return MOTY_EUNSUP;
   if (S <= 0 || O <= 0) return MOTY_OK;
   hipLaunchKernelGGL(k_i4row_f32, dim3((O + 255) / 256, S), dim3(256), 0, st, x, q4, scale, y, S, I, O);
   LAUNCH_TRY("k_i4row_f32");

@@ -320,19 +320,13 @@ int launch_pack_i4row(const float* w, uint8_t* q4, float* scale, int O, int I, h
   return MOTY_OK;
 }
 
-// Per-row int4 rows -> int8 rows n - 8 (the codes dot_i4i8 multiplies,
-// hw/hw_scalar.h:14-22), so the Q8 kernels run the integer dot.  I % 16 == 0;
-// thread per 8 input bytes.
-__global__ __launch_bounds__(256) void k_i4row_to_i8(const uint8_t* __restrict__ q4, int8_t* __restrict__ q8,
-                                                     int64_t n8) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n8) return;
-  const uint2 w = *(const uint2*)(q4 + 8 * i);
+// 16 per-row int4 codes (8 bytes, element 2j in the low nibble of byte j)
+// -> the 16 int8 values n - 8 that dot_i4i8 multiplies (hw/hw_scalar.h:14-22).
+__device__ __forceinline__ int4 i4row_expand16(uint2 w) {
   const uint32_t wd[2] = {w.x, w.y};
   uint32_t o[4];
 #pragma unroll
   for (int k = 0; k < 2; k++) {
-    // bytes b0..b3 of wd[k] hold elements 2j (low) and 2j+1 (high)
     const uint32_t lo = wd[k] & 0x0f0f0f0fu, hi = (wd[k] >> 4) & 0x0f0f0f0fu;
     const uint32_t e01 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);  // lo0 hi0 lo1 hi1
     const uint32_t e23 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // lo2 hi2 lo3 hi3
@@ -340,14 +334,46 @@ __global__ __launch_bounds__(256) void k_i4row_to_i8(const uint8_t* __restrict__
     o[2 * k] = (e01 + 0x78787878u) ^ 0x80808080u;
     o[2 * k + 1] = (e23 + 0x78787878u) ^ 0x80808080u;
   }
-  *(uint4*)(q8 + 16 * i) = uint4{o[0], o[1], o[2], o[3]};
+  return int4{(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
 }
 
-int launch_i4row_to_i8(const uint8_t* q4, int8_t* q8, int64_t n, hipStream_t st) {
-  const int64_t n8 = n / 16;  // 8 input bytes (16 codes) per thread
-  if (n8 <= 0) return MOTY_OK;
-  hipLaunchKernelGGL(k_i4row_to_i8, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st, q4, q8, n8);
-  LAUNCH_TRY("k_i4row_to_i8");
+// moty_matmul_i4_s with IDOT4 (nn/matmul.c:75-86, i4_idot_rows :91-99):
+//     y[s*O+o] = scale[o] * sx[s] * (float)dot_i4i8(q4 row o, xq[s], I)
+// straight from the nibbles, no int8 copy of the weights.  A wave owns one
+// row; lane l covers elements [c*1024 + 16l, +16) of chunk c (8 nibble bytes,
+// 512 B per wave-load, coalesced).  Tokens go in blocks of four; a row is
+// re-read once per block, from L2 after the first.  I % 16 == 0 (every
+// covered 16-element run is whole), q4 8-byte and xq 16-byte aligned.
+__global__ __launch_bounds__(256) void k_i4row_idot(const int8_t* __restrict__ xq, const float* __restrict__ sx,
+                                                    const uint8_t* __restrict__ q4, const float* __restrict__ scale,
+                                                    float* __restrict__ y, int S, int I, int O) {
+  const int lane = threadIdx.x % MOTY_WAVE;
+  const int o = blockIdx.x * 4 + threadIdx.x / MOTY_WAVE;
+  if (o >= O) return;
+  const uint8_t* wr = q4 + (int64_t)o * (I / 2);
+  const float so = scale[o];
+  for (int s0 = 0; s0 < S; s0 += 4) {
+    int acc[4] = {0, 0, 0, 0};
+    for (int k = lane * 16; k < I; k += 1024) {
+      const int4 w = i4row_expand16(*(const uint2*)(wr + k / 2));
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        if (s0 + j < S) acc[j] = dot16(w, *(const int4*)(xq + (int64_t)(s0 + j) * I + k), acc[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int a = wave_sum_i32(acc[j]);
+      if (lane == 0 && s0 + j < S) y[(int64_t)(s0 + j) * O + o] = so * sx[s0 + j] * (float)a;
+    }
+  }
+}
+
+int launch_i4row_idot(const int8_t* xq, const float* sx, const uint8_t* q4, const float* scale, float* y, int S,
+                      int I, int O, hipStream_t st) {
+  if (S <= 0 || O <= 0) return MOTY_OK;
+  if (I % 16 || (((uintptr_t)q4) & 7) || (((uintptr_t)xq) & 15)) return MOTY_EUNSUP;
+  hipLaunchKernelGGL(k_i4row_idot, dim3((unsigned)((O + 3) / 4)), dim3(256), 0, st, xq, sx, q4, scale, y, S, I, O);
+  LAUNCH_TRY("k_i4row_idot");
   return MOTY_OK;
 }
 

@@ -243,10 +243,11 @@ def test_pack_int4(ops, O, I):
 
 @pytest.mark.parametrize("idot4", [True, False])
 @pytest.mark.parametrize("S,I,O", [(1, 4096, 256), (3, 1024, 100), (4, 96, 17), (37, 2048, 300), (512, 1024, 1024),
-                                   (9, 16, 5)])
+                                   (9, 16, 5), (2, 2048, 20000), (6, 4096, 12288)])
 def test_matmul_i4_s(ops, idot4, S, I, O):
-    # moty_matmul_i4_s (nn/matmul.c:75-145): int8 GEMV/GEMM over the
-    # expanded codes (IDOT4) or the AVX2-order exact f32 path
+    # moty_matmul_i4_s (nn/matmul.c:75-145): the integer dot straight from
+    # the nibbles (IDOT4) or the AVX2-order exact f32 path; the last two
+    # shapes are large-O weights (no int8 copy of them is made)
     from cpu_libs import o_matmul_i4, o_pack_int4
     say("matmul_i4_s", idot4, S, I, O)
     q4, s = o_pack_int4(randn(O + 2 * I, (O, I), 0.02))
@@ -254,3 +255,20 @@ def test_matmul_i4_s(ops, idot4, S, I, O):
     y = to_np(ops.matmul_i4_s(to_dev(x), to_dev(q4), to_dev(s), idot4))
     y2 = o_matmul_i4(x, q4, s, idot4)
     assert same_bits(y, y2), mismatch(y, y2)
+
+
+@pytest.mark.parametrize("idot4", [True, False])
+def test_matmul_i4_s_misaligned(ops, idot4):
+    # the kernels read 8 nibble bytes per load: a weight view that is not
+    # 8-byte aligned is refused with an error, never read out of line
+    import torch
+    from cpu_libs import o_pack_int4
+    S, I, O = 2, 256, 8
+    say("matmul_i4_s misaligned", idot4)
+    q4, s = o_pack_int4(randn(O + 2 * I, (O, I), 0.02))
+    buf = torch.zeros(O * I // 2 + 1, dtype=torch.uint8, device="cuda")
+    qv = buf[1:].view(O, I // 2)
+    qv.copy_(to_dev(q4))
+    import moty_amd
+    with pytest.raises(moty_amd.MotyHipError, match="aligned"):
+        ops.matmul_i4_s(to_dev(randn(S + I, (S, I))), qv, to_dev(s), idot4)

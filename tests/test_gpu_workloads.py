@@ -170,6 +170,25 @@ def test_c3_i4g_prefill(ops, c3_weights):
     assert same_bits(y, y2), mismatch(y, y2)
 
 
+@pytest.mark.parametrize("M", [1, 256])
+def test_c3_i4g_exact_f32_ffn(ops, c3_weights, M):
+    # the reference's default grouped-int4 path (IDOT4 unset: f32
+    # activations, nn/matmul.c:199-253) through the FFN entry bench.py times
+    # (moty_hip_dense_ffn_i4g_dev, idot4 = 0) at the full C3 shapes.  Every
+    # output row depends only on its own input row, so at M = 256 the oracle
+    # (scalar C) checks a spread of rows of the full-size run.
+    D, I, (gq, gs), (uq, us), (dq, ds) = c3_weights
+    say("C3 i4g exact f32 M=%d" % M)
+    x = randn(85 + M, (M, D))
+    out = to_np(ops.dense_ffn_i4g(to_dev(x), to_dev(gq), to_dev(gs), to_dev(uq), to_dev(us), to_dev(dq),
+                                  to_dev(ds), idot4=False))
+    rows = [0] if M == 1 else [0, 1, 37, 128, 200, 255]
+    xs = x[rows]
+    h2 = o_silu(o_matmul_i4g(xs, gq, gs, False), o_matmul_i4g(xs, uq, us, False))
+    y2 = o_matmul_i4g(h2, dq, ds, False)
+    assert same_bits(out[rows], y2), mismatch(out[rows], y2)
+
+
 # ---------------- C3 shapes in Q4R4 ----------------
 def fast_r4(seed, O, I):
     g = rng(seed)
