@@ -111,14 +111,15 @@ __global__ __launch_bounds__(Q4V_NT) void k_gemv_i4g(const float* __restrict__ x
 // IDOT4 GEMV for decode (S = 1), optionally PAIR (gate + up + SiLU).
 // Workgroup = 4 waves; a wave owns RW consecutive output rows (of W, and of
 // W2 in PAIR mode):
-//   1. it issues every nibble load of its rows first -- lane l takes groups
-//      l, l+64, ... (16 B each, coalesced along the row);
+//   1. it issues the nibble loads of its rows' first PD 64-group chunks --
+//      lane l takes group l of each chunk (16 B, coalesced along the row) --
+//      and each further chunk as the one PD before it is consumed;
 //   2. the workgroup quantizes x into LDS (qrow_i8) while those loads fly;
-//   3. each lane forms its groups' exact integer dots sum (n-8)*x and parks
-//      them, with the group scales, in the wave's LDS slice;
-//   4. one lane per row runs the reference's FMA chain over the groups in
-//      order; y = sx * acc (PAIR: h = silu(g) * u).
-template <int RW, int NGC, bool PAIR, int NT>
+//   3. per chunk, each lane forms its group's exact integer dot sum (n-8)*x
+//      and parks it, with the group scale, in the wave's LDS slice;
+//   4. one lane per row extends the reference's FMA chain over the chunk's
+//      groups in order; y = sx * acc (PAIR: h = silu(g) * u).
+template <int RW, int NGC, bool PAIR, int NT, int PD = NGC>
 __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, const uint8_t* __restrict__ q4,
                                                       const float* __restrict__ scl,
                                                       const uint8_t* __restrict__ q4b,
@@ -131,10 +132,11 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
   __shared__ float red[WAVES];
   __shared__ float sx_s;
   const int lane = threadIdx.x % MOTY_WAVE, wv = threadIdx.x / MOTY_WAVE;
-  const int ng = I / 32, rb = I / 2, ldv = ng + 2;  // ldv even: float2 rows stay 8-byte aligned
+  const int ng = I / 32, rb = I / 2;
+  constexpr int ldv = 66;  // one chunk's 64 groups, padded (even: float4 reads stay aligned)
   int8_t* xq_s = lds;                                                          // [I]
   int* xg8 = (int*)(lds + I);                                                  // [ng] -8 * group sums
-  float2* dv = (float2*)(lds + I + ng * 4) + (size_t)wv * (NM * RW * ldv);      // [NM*RW][ldv] (scale, dot)
+  float2* dv = (float2*)(lds + I + ng * 4) + (size_t)wv * (NM * RW * ldv);      // [NM*RW][ldv] (scale, dot) of one chunk
   const int o0 = (blockIdx.x * WAVES + wv) * RW;
 
   // 1. x (one pass, kept in registers), then every nibble load of this wave
@@ -146,11 +148,13 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
   }
   int4 wb[NM][RW][NGC];
   float wsc[NM][RW][NGC];  // group scales, loaded with the nibbles
-  // chunk-major issue order: chunk c of every row lands before chunk c+1, so
-  // the group dots and FMA chains of chunk c can run while later chunks are
-  // still in flight (the compiler waits only for the chunk it consumes)
-#pragma unroll
-  for (int c = 0; c < NGC; c++)
+  // chunk-major issue order, PD chunks ahead: chunk c of every row is
+  // issued before chunk c+1, and chunk c+PD only when chunk c is consumed,
+  // so each row's data arrives spread over the stream and its FMA chain
+  // (one dependent FMA per group) runs behind it; with every chunk issued
+  // at once a row's whole chain would start after its last byte lands
+  // (the compiler waits only for the chunk it consumes)
+  auto issue = [&](int c) {
 #pragma unroll
     for (int m = 0; m < NM; m++)
 #pragma unroll
@@ -165,6 +169,9 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
         }
         wsc[m][r][c] = __builtin_nontemporal_load((m ? sclb : scl) + o * ng + g);
       }
+  };
+#pragma unroll
+  for (int c = 0; c < PD; c++) issue(c);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int j = 0; j < XV; j++) xr[j] = sel4((threadIdx.x + j * NT) * 4 < I, xr[j]);
@@ -211,6 +218,10 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
   float acc = 0.f;
 #pragma unroll
   for (int c = 0; c < NGC; c++) {
+    if (c + PD < NGC) {
+      issue(c + PD);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     const int g = c * 64 + lane;
     if (g < ng) {
       const int4 x0 = *(const int4*)(xq_s + g * 32);
@@ -224,7 +235,7 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
           const int4 w0 = unpack_nib16_u(uint2{(uint32_t)w.x, (uint32_t)w.y});
           const int4 w1 = unpack_nib16_u(uint2{(uint32_t)w.z, (uint32_t)w.w});
           const int d = dot16(w1, x1, dot16(w0, x0, c8));
-          dv[(m * RW + r) * ldv + g] = float2{wsc[m][r][c], (float)d};
+          dv[(m * RW + r) * ldv + lane] = float2{wsc[m][r][c], (float)d};
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -232,7 +243,7 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     if (lane < NM * RW) {
       const int gend = ng < (c + 1) * 64 ? ng : (c + 1) * 64;
-      const float4* dr = (const float4*)(dv + lane * ldv);
+      const float4* dr = (const float4*)(dv + lane * ldv - c * 64);
       int gg = c * 64;
       for (; gg + 16 <= gend; gg += 16) {
         float4 v[8];
@@ -244,9 +255,13 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
           acc = __fmaf_rn(v[u].z, v[u].w, acc);
         }
       }
-      const float2* d2 = dv + lane * ldv;
+      const float2* d2 = dv + lane * ldv - c * 64;
       for (; gg < gend; gg++) acc = __fmaf_rn(d2[gg].x, d2[gg].y, acc);
     }
+    // the next chunk's dots overwrite the slice: after these reads
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
   const float sxv = sx_s;
   if (PAIR) {
@@ -887,15 +902,15 @@ int launch_i4row_f32(const float* x, const uint8_t* q4, const float* scale, floa
 
 // NT = 256 or 512 threads: wider workgroups amortize the activation row
 // (read once per workgroup) over more weight rows when I is large
-template <int RW, int NGC, bool PAIR, int NT>
+template <int RW, int NGC, bool PAIR, int NT, int PD = NGC>
 static int go_gemv1_i4g(const float* x, const uint8_t* q4, const float* scl, const uint8_t* q4b, const float* sclb,
                         float* y, int I, int O, hipStream_t st) {
   constexpr int NM = PAIR ? 2 : 1;
   const int ng = I / 32;
-  const size_t lds = (size_t)I + (size_t)ng * 4 + (size_t)(NT / MOTY_WAVE) * NM * RW * (ng + 2) * 8;
+  const size_t lds = (size_t)I + (size_t)ng * 4 + (size_t)(NT / MOTY_WAVE) * NM * RW * 66 * 8;
   if (lds > 64 * 1024) return MOTY_EUNSUP;
   const unsigned nb = (unsigned)((O + RW * (NT / MOTY_WAVE) - 1) / (RW * (NT / MOTY_WAVE)));
-  hipLaunchKernelGGL((k_gemv1_i4g<RW, NGC, PAIR, NT>), dim3(nb), dim3(NT), lds, st, x, q4, scl, q4b, sclb, y, I, O);
+  hipLaunchKernelGGL((k_gemv1_i4g<RW, NGC, PAIR, NT, PD>), dim3(nb), dim3(NT), lds, st, x, q4, scl, q4b, sclb, y, I, O);
   LAUNCH_TRY("k_gemv1_i4g");
   return MOTY_OK;
 }
@@ -909,7 +924,7 @@ int launch_gemv_i4g(const float* x, const uint8_t* q4, const float* scl, const u
     const int ngc = (I / 32 + 63) / 64;
     int rc = MOTY_EUNSUP;
     if (q4b) {
-      if (ngc <= 2) rc = go_gemv1_i4g<4, 2, true, 256>(x, q4, scl, q4b, sclb, y, I, O, st);
+      if (ngc <= 2) rc = go_gemv1_i4g<4, 2, true, 256, 1>(x, q4, scl, q4b, sclb, y, I, O, st);
       else if (ngc <= 4) {
         rc = go_gemv1_i4g<2, 4, true, 512>(x, q4, scl, q4b, sclb, y, I, O, st);
         if (rc == MOTY_EUNSUP) rc = go_gemv1_i4g<2, 4, true, 256>(x, q4, scl, q4b, sclb, y, I, O, st);
@@ -924,9 +939,12 @@ int launch_gemv_i4g(const float* x, const uint8_t* q4, const float* scl, const u
       rc = go_gemv1_i4g<4, 4, false, 512>(x, q4, scl, nullptr, nullptr, y, I, O, st);
       if (rc == MOTY_EUNSUP) rc = go_gemv1_i4g<4, 4, false, 256>(x, q4, scl, nullptr, nullptr, y, I, O, st);
     } else if (ngc <= 6) {
-      // 4096 x 12288 (8B down) in a sweep of rows/wave x workgroup size on
-      // MI355X: 2 rows x 256 threads 15.4 us, x 512 threads 15.9, 1 row 16.2
-      rc = go_gemv1_i4g<2, 6, false, 256>(x, q4, scl, nullptr, nullptr, y, I, O, st);
+      // 4096 x 12288 (8B down) in a sweep of rows/wave x workgroup size x
+      // chunks in flight on MI355X, graph replays over rotating weights:
+      // 4 rows x 256 threads, one chunk ahead 8.0 us; two ahead 9.3, all six
+      // 10.9 (the whole row's chains then run after its last byte lands);
+      // 2 rows 9.6 / 10.9; 8 rows x 128 threads 10.1
+      rc = go_gemv1_i4g<4, 6, false, 256, 1>(x, q4, scl, nullptr, nullptr, y, I, O, st);
     } else if (ngc <= 8) {
       rc = go_gemv1_i4g<2, 8, false, 256>(x, q4, scl, nullptr, nullptr, y, I, O, st);
     }
