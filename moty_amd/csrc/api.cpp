@@ -369,6 +369,10 @@ int moty_hip_matmul_i4_grouped_s_dev(float* y, const float* x, const uint8_t* q4
     if (rc) return rc;
     return launch_gemm_i4g(xq, sx, q4, scale, y, S, I, O, st);
   }
+  if (gs == 32 && S == 1) {
+    const int rc = launch_gemv_i4g_xf(x, q4, scale, nullptr, nullptr, y, I, O, st);
+    if (rc != MOTY_EUNSUP) return rc;
+  }
   if (gs == 32 && (I % 32) == 0) return launch_i4g_f32(x, q4, scale, y, S, I, O, st);
   set_error("matmul_i4_grouped_s: gs=%d I=%d unsupported (exact path needs gs == 32, I %% 32 == 0)", gs, I);
   return MOTY_EUNSUP;
@@ -569,6 +573,12 @@ int moty_hip_dense_ffn_i4g_dev(float* out, const float* x, int S, const uint8_t*
   if (vec && S == 1) {
     if ((rc = launch_gemv_i4g(x, gate, gs, up, us, h, 1, D, I, st))) return rc;
     return launch_gemv_i4g(h, down, ds, nullptr, nullptr, out, 1, I, D, st);
+  }
+  if (!idot4 && S == 1 && D <= 12288 && I <= 12288 &&
+      !(((uintptr_t)x | (uintptr_t)gate | (uintptr_t)up | (uintptr_t)down | (uintptr_t)h) & 15)) {
+    // exact f32: gate + up + SiLU in one pass, then down
+    if ((rc = launch_gemv_i4g_xf(x, gate, gs, up, us, h, D, I, st))) return rc;
+    return launch_gemv_i4g_xf(h, down, ds, nullptr, nullptr, out, I, D, st);
   }
   // one matmul_i4_grouped_s each, the path chosen per matrix as the
   // reference does (IDOT4 needs the row length a multiple of 64, <= 16384)

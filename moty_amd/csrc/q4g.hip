@@ -119,7 +119,7 @@ __global__ __launch_bounds__(Q4V_NT) void k_gemv_i4g(const float* __restrict__ x
 //      and parks it, with the group scale, in the wave's LDS slice;
 //   4. one lane per row extends the reference's FMA chain over the chunk's
 //      groups in order; y = sx * acc (PAIR: h = silu(g) * u).
-template <int RW, int NGC, bool PAIR, int NT, int PD = NGC>
+template <int RW, int NGC, bool PAIR, int NT, int PD = NGC, bool XF = false>
 __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, const uint8_t* __restrict__ q4,
                                                       const float* __restrict__ scl,
                                                       const uint8_t* __restrict__ q4b,
@@ -136,7 +136,8 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
   constexpr int ldv = 66;  // one chunk's 64 groups, padded (even: float4 reads stay aligned)
   int8_t* xq_s = lds;                                                          // [I]
   int* xg8 = (int*)(lds + I);                                                  // [ng] -8 * group sums
-  float2* dv = (float2*)(lds + I + ng * 4) + (size_t)wv * (NM * RW * ldv);      // [NM*RW][ldv] (scale, dot) of one chunk
+  float* xf_s = (float*)lds;                                                   // XF: [I] f32
+  float2* dv = (float2*)(lds + (XF ? 4 * I : I + ng * 4)) + (size_t)wv * (NM * RW * ldv);  // [NM*RW][ldv] (scale, dot) of one chunk
   const int o0 = (blockIdx.x * WAVES + wv) * RW;
 
   // 1. x (one pass, kept in registers), then every nibble load of this wave
@@ -175,6 +176,15 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int j = 0; j < XV; j++) xr[j] = sel4((threadIdx.x + j * NT) * 4 < I, xr[j]);
+  if (XF) {
+    // exact f32 activations: x into LDS as it is
+#pragma unroll
+    for (int j = 0; j < XV; j++) {
+      const int i = (threadIdx.x + j * NT) * 4;
+      if (i < I) *(float4*)(xf_s + i) = xr[j];
+    }
+    __syncthreads();
+  } else {
   // 2. qrow_i8 of x into LDS
   float amax = 0.f;
 #pragma unroll
@@ -210,6 +220,7 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
                         dot16(a, int4{0x01010101, 0x01010101, 0x01010101, 0x01010101}, 0));
   }
   __syncthreads();
+  }
   // 3./4. per 64-group chunk: every lane forms its group's exact integer dot
   // for each row and parks (scale, dot) in the wave's LDS slice; then lane
   // j < NM*RW continues the FMA chain of its row (j % RW of matrix j / RW)
@@ -223,7 +234,41 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
       __builtin_amdgcn_sched_barrier(0);
     }
     const int g = c * 64 + lane;
-    if (g < ng) {
+    if (XF && g < ng) {
+      // the reference's exact f32 group sum (nn/matmul.c:222-233, the
+      // AVX-512 form with FMA contraction): t[j] = fma(x[j], w[j],
+      // x[16+j]*w[16+j]), then the 16 -> 8 -> 4 -> 1 reduction tree
+      float xv[32];
+#pragma unroll
+      for (int q = 0; q < 8; q++) *(float4*)(xv + 4 * q) = *(const float4*)(xf_s + g * 32 + 4 * q);
+#pragma unroll
+      for (int m = 0; m < NM; m++)
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+          const int4 w = wb[m][r][c];
+          const uint32_t wd[4] = {(uint32_t)w.x, (uint32_t)w.y, (uint32_t)w.z, (uint32_t)w.w};
+          float wf[32];  // element e = byte e/2, low nibble when e is even, minus 8 (exact)
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const uint32_t lo = wd[q] & 0x0f0f0f0fu, hi = (wd[q] >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+              wf[8 * q + 2 * k] = (float)((lo >> (8 * k)) & 0xffu) - 8.f;
+              wf[8 * q + 2 * k + 1] = (float)((hi >> (8 * k)) & 0xffu) - 8.f;
+            }
+          }
+          float t[16];
+#pragma unroll
+          for (int j = 0; j < 16; j++) t[j] = __fmaf_rn(xv[j], wf[j], xv[16 + j] * wf[16 + j]);
+          float u[8], v[4];
+#pragma unroll
+          for (int j = 0; j < 8; j++) u[j] = t[j + 8] + t[j];
+#pragma unroll
+          for (int j = 0; j < 4; j++) v[j] = u[j + 4] + u[j];
+          dv[(m * RW + r) * ldv + lane] = float2{wsc[m][r][c], (v[0] + v[2]) + (v[1] + v[3])};
+        }
+    }
+    if (!XF && g < ng) {
       const int4 x0 = *(const int4*)(xq_s + g * 32);
       const int4 x1 = *(const int4*)(xq_s + g * 32 + 16);
       const int c8 = xg8[g];
@@ -263,14 +308,15 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
-  const float sxv = sx_s;
+  // XF: y = a (no activation scale)
+  const float sxv = XF ? 0.f : sx_s;
   if (PAIR) {
     const float u = __shfl(acc, (lane + RW) & 63, 64);  // lane r < RW: the up row's chain
     const int o = o0 + lane;
-    if (lane < RW && o < O) y[o] = ref_silu_mul(sxv * acc, sxv * u);
+    if (lane < RW && o < O) y[o] = XF ? ref_silu_mul(acc, u) : ref_silu_mul(sxv * acc, sxv * u);
   } else {
     const int o = o0 + lane;
-    if (lane < RW && o < O) y[o] = sxv * acc;
+    if (lane < RW && o < O) y[o] = XF ? acc : sxv * acc;
   }
 }
 
@@ -902,17 +948,36 @@ int launch_i4row_f32(const float* x, const uint8_t* q4, const float* scale, floa
 
 // NT = 256 or 512 threads: wider workgroups amortize the activation row
 // (read once per workgroup) over more weight rows when I is large
-template <int RW, int NGC, bool PAIR, int NT, int PD = NGC>
+template <int RW, int NGC, bool PAIR, int NT, int PD = NGC, bool XF = false>
 static int go_gemv1_i4g(const float* x, const uint8_t* q4, const float* scl, const uint8_t* q4b, const float* sclb,
                         float* y, int I, int O, hipStream_t st) {
   constexpr int NM = PAIR ? 2 : 1;
   const int ng = I / 32;
-  const size_t lds = (size_t)I + (size_t)ng * 4 + (size_t)(NT / MOTY_WAVE) * NM * RW * 66 * 8;
+  const size_t lds = (XF ? (size_t)I * 4 : (size_t)I + (size_t)ng * 4) + (size_t)(NT / MOTY_WAVE) * NM * RW * 66 * 8;
   if (lds > 64 * 1024) return MOTY_EUNSUP;
   const unsigned nb = (unsigned)((O + RW * (NT / MOTY_WAVE) - 1) / (RW * (NT / MOTY_WAVE)));
-  hipLaunchKernelGGL((k_gemv1_i4g<RW, NGC, PAIR, NT, PD>), dim3(nb), dim3(NT), lds, st, x, q4, scl, q4b, sclb, y, I, O);
+  hipLaunchKernelGGL((k_gemv1_i4g<RW, NGC, PAIR, NT, PD, XF>), dim3(nb), dim3(NT), lds, st, x, q4, scl, q4b, sclb, y, I, O);
   LAUNCH_TRY("k_gemv1_i4g");
   return MOTY_OK;
+}
+
+// The exact-f32 path (IDOT4 unset) for one token: the same workgroup
+// structure with x kept as f32 in LDS and each lane's group sum formed in
+// the reference's float order.  I % 32 == 0, I <= 12288 (x in LDS), 16-byte
+// aligned x and nibbles.  PAIR (q4b): gate + up + SiLU.
+int launch_gemv_i4g_xf(const float* x, const uint8_t* q4, const float* scl, const uint8_t* q4b, const float* sclb,
+                       float* y, int I, int O, hipStream_t st) {
+  if ((I % 32) || I > 12288 || ((((uintptr_t)x) | ((uintptr_t)q4) | ((uintptr_t)q4b)) & 15)) return MOTY_EUNSUP;
+  if (O <= 0) return MOTY_OK;
+  const int ngc = (I / 32 + 63) / 64;
+  if (q4b) {
+    if (ngc <= 2) return go_gemv1_i4g<4, 2, true, 256, 1, true>(x, q4, scl, q4b, sclb, y, I, O, st);
+    if (ngc <= 4) return go_gemv1_i4g<2, 4, true, 256, 1, true>(x, q4, scl, q4b, sclb, y, I, O, st);
+    return go_gemv1_i4g<2, 6, true, 256, 1, true>(x, q4, scl, q4b, sclb, y, I, O, st);
+  }
+  if (ngc <= 2) return go_gemv1_i4g<8, 2, false, 256, 1, true>(x, q4, scl, nullptr, nullptr, y, I, O, st);
+  if (ngc <= 4) return go_gemv1_i4g<4, 4, false, 256, 1, true>(x, q4, scl, nullptr, nullptr, y, I, O, st);
+  return go_gemv1_i4g<4, 6, false, 256, 1, true>(x, q4, scl, nullptr, nullptr, y, I, O, st);
 }
 
 int launch_gemv_i4g(const float* x, const uint8_t* q4, const float* scl, const uint8_t* q4b, const float* sclb,

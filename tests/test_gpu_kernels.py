@@ -165,7 +165,11 @@ def test_gate_up_silu_i4g(ops, D, I):
     assert same_bits(h, g), mismatch(h, g)
 
 
-@pytest.mark.parametrize("S,I,O", [(1, 4096, 256), (3, 96, 40), (16, 1024, 64)])
+@pytest.mark.parametrize("S,I,O", [(1, 4096, 256), (3, 96, 40), (16, 1024, 64),
+                                   # one token: the GEMV form (1..6 chunks of 64 groups, partial
+                                   # chunks, ragged rows), and past its 12288 bound the fallback
+                                   (1, 12288, 100), (1, 8192, 77), (1, 96, 40), (1, 2080, 300), (1, 16384, 20),
+                                   (1, 64, 1000)])
 def test_i4g_f32(ops, S, I, O):
     say("i4g f32", S, I, O)
     w = randn(O + I, (O, I), 0.02)
@@ -209,7 +213,9 @@ def test_silu_and_softmax(ops):
 @pytest.mark.parametrize("S,D,I", [(37, 256, 384), (5, 128, 128), (4, 256, 128), (1, 128, 64), (130, 1024, 640),
                                    (70, 192, 320), (3, 4096, 96), (300, 512, 1280),
                                    # 64 x 192 gate/up tiles, ragged in tokens and rows
-                                   (130, 256, 12416)])
+                                   (130, 256, 12416),
+                                   # one token through the exact-f32 fused gate/up GEMV
+                                   (1, 4096, 1056), (1, 96, 8192), (1, 12288, 2080)])
 def test_dense_ffn_i4g(ops, idot4, S, D, I):
     # nn/ffn.c:26-55 over grouped-int4 Mats: the fused gate/up f16 pass
     # (S > 4, D and I multiples of 128), the int8 GEMM fallback (other
