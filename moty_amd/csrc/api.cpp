@@ -369,8 +369,15 @@ int moty_hip_matmul_i4_grouped_s_dev(float* y, const float* x, const uint8_t* q4
     if (rc) return rc;
     return launch_gemm_i4g(xq, sx, q4, scale, y, S, I, O, st);
   }
-  if (gs == 32 && S == 1) {
-    const int rc = launch_gemv_i4g_xf(x, q4, scale, nullptr, nullptr, y, I, O, st);
+  if (gs == 32 && S <= 4) {
+    // a few tokens: the one-token GEMV per token
+    int rc = MOTY_OK;
+    for (int s = 0; s < S && rc == MOTY_OK; s++)
+      rc = launch_gemv_i4g_xf(x + (int64_t)s * I, q4, scale, nullptr, nullptr, y + (int64_t)s * O, I, O, st);
+    if (rc != MOTY_EUNSUP) return rc;
+  }
+  if (gs == 32 && S > 4) {
+    const int rc = launch_gemm_i4g_xf(x, q4, scale, nullptr, nullptr, y, S, I, O, st);
     if (rc != MOTY_EUNSUP) return rc;
   }
   if (gs == 32 && (I % 32) == 0) return launch_i4g_f32(x, q4, scale, y, S, I, O, st);
@@ -588,8 +595,14 @@ int moty_hip_dense_ffn_i4g_dev(float* out, const float* x, int S, const uint8_t*
       int r = launch_qrow_i8(a, (int8_t*)xq, sx, nullptr, S, K, K, K, st);
       return r ? r : launch_gemm_i4g((const int8_t*)xq, sx, w, ws, o, S, K, N, st);
     }
+    if (S > 4 && launch_gemm_i4g_xf(a, w, ws, nullptr, nullptr, o, S, K, N, st) == MOTY_OK) return MOTY_OK;
     return launch_i4g_f32(a, w, ws, o, S, K, N, st);
   };
+  if (!idot4 && S > 4 && (D % 64) == 0 && !(((uintptr_t)x) & 15) && !(((uintptr_t)gate | (uintptr_t)up) & 7)) {
+    // exact f32, many tokens: gate + up + SiLU in one tiled pass, then down
+    if ((rc = launch_gemm_i4g_xf(x, gate, gs, up, us, h, S, D, I, st))) return rc;
+    return mm(h, down, ds, out, I, D);
+  }
   if ((rc = mm(x, gate, gs, h, D, I))) return rc;
   if ((rc = mm(x, up, us, u, D, I))) return rc;
   if ((rc = launch_silu_mul(h, u, (int64_t)S * I, st))) return rc;

@@ -44,6 +44,9 @@ int launch_gemm_q8(const int8_t* xq, const float* sx, const int8_t* W, const flo
 // q4b/sclb non-null: PAIR mode (S = 1), y = silu(x.q4^T) * (x.q4b^T)
 int launch_gemv_i4g(const float* x, const uint8_t* q4, const float* scl, const uint8_t* q4b, const float* sclb,
                     float* y, int S, int I, int O, hipStream_t st);
+// the exact-f32 path (IDOT4 unset), many tokens (tiled); q4b/sclb non-null: PAIR
+int launch_gemm_i4g_xf(const float* x, const uint8_t* q4, const float* scl, const uint8_t* q4b, const float* sclb,
+                       float* y, int M, int I, int O, hipStream_t st);
 // the exact-f32 path (IDOT4 unset), one token; q4b/sclb non-null: PAIR
 int launch_gemv_i4g_xf(const float* x, const uint8_t* q4, const float* scl, const uint8_t* q4b, const float* sclb,
                        float* y, int I, int O, hipStream_t st);

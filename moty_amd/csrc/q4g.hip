@@ -1043,6 +1043,155 @@ int launch_gemm_i4g(const int8_t* xq, const float* sx, const uint8_t* q4, const 
   return MOTY_OK;
 }
 
+// ---------------------------------------------------------------------------
+// The exact-f32 path (IDOT4 unset) for many tokens, as a tiled GEMM on the
+// vector ALUs (the reference's float order admits no matrix-core form: each
+// product x*w is rounded on its own).  Workgroup tile: 64 tokens x 64 weight
+// rows (PAIR: 32 gate rows and the same 32 up rows), K steps of two groups.
+// Per step the workgroup stages x and the nibbles, expanded once to floats
+// (n - 8, exact), in LDS; thread (tx, ty) owns tokens ty + 16i and tile rows
+// tx + 16j (i, j < 4).  Each group's 32 elements sit in LDS in the order
+// 8*(e % 4) + e / 4, so for jj = 0..3 the eight elements
+// {jj, jj+4, jj+8, jj+12, jj+16, .., jj+28} that reduce to v[jj] of the
+// reference's tree are two 16-byte reads:
+//   t[j] = fma(x[j], w[j], x[16+j]*w[16+j])   (j < 16)
+//   u[j] = t[j+8] + t[j];  v[j] = u[j+4] + u[j];  r = (v0 + v2) + (v1 + v3)
+//   a = fma(r, scale[g], a)                  (groups in ascending order)
+// -- nn/matmul.c:222-233 with FMA contraction, as the one-token kernels.
+constexpr int XF_BT = 64, XF_BO = 64, XF_KE = 64;  // tokens, weight rows, elements per K step
+constexpr int XF_LS = XF_KE + 4;                   // LDS row stride (floats): 16-byte reads conflict-free
+
+__device__ __forceinline__ int xf_pos(int e) { return ((e >> 5) << 5) + 8 * (e & 3) + ((e & 31) >> 2); }
+
+template <bool PAIR>
+__global__ __launch_bounds__(256, 2) void k_gemm_i4g_xf(const float* __restrict__ x, const uint8_t* __restrict__ q4,
+                                                        const float* __restrict__ scl,
+                                                        const uint8_t* __restrict__ q4b,
+                                                        const float* __restrict__ sclb, float* __restrict__ y,
+                                                        int M, int I, int O) {
+  __shared__ __align__(16) float xs[XF_BT * XF_LS];
+  __shared__ __align__(16) float ws[XF_BO * XF_LS];
+  __shared__ float ss[XF_BO][2];
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const int tb = blockIdx.y * XF_BT;
+  constexpr int OR = PAIR ? XF_BO / 2 : XF_BO;  // output rows per tile
+  const int ob = blockIdx.x * OR;
+  const int ng = I / 32, rb = I / 2;
+  // staging roles: x row tid/4, elements 16*(tid%4) .. +16 of the step;
+  // weight row tid/4, nibble bytes 8*(tid%4) .. +8 (elements 16*(tid%4) ..)
+  const int sr = tid >> 2, sq = tid & 3;
+  const int xt = tb + sr < M ? tb + sr : M - 1;
+  const float* xsrc = x + (int64_t)xt * I + 16 * sq;
+  const uint8_t* wsrc;
+  const float* ssrc;
+  {
+    int row = PAIR ? (sr & 31) : sr;
+    int o = ob + row < O ? ob + row : O - 1;
+    const bool up = PAIR && sr >= 32;
+    wsrc = (up ? q4b : q4) + (int64_t)o * rb + 8 * sq;
+    ssrc = (up ? sclb : scl) + (int64_t)o * ng;
+  }
+  float4 px[4];
+  uint2 pw;
+  float psc = 0.f;
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) px[q] = *(const float4*)(xsrc + k0 + 4 * q);
+    pw = *(const uint2*)(wsrc + k0 / 2);
+    if (sq < 2) psc = ssrc[k0 / 32 + sq];
+  };
+  float a[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) a[i][j] = 0.f;
+  gload(0);
+  for (int k0 = 0; k0 < I; k0 += XF_KE) {
+    __syncthreads();  // the previous step's reads are done
+    {
+      const float* pv = (const float*)px;
+#pragma unroll
+      for (int e = 0; e < 16; e++) xs[sr * XF_LS + xf_pos(16 * sq + e)] = pv[e];
+      const uint32_t wd[2] = {pw.x, pw.y};
+#pragma unroll
+      for (int b = 0; b < 8; b++) {
+        const uint32_t byte = (wd[b >> 2] >> (8 * (b & 3))) & 0xffu;
+        ws[sr * XF_LS + xf_pos(16 * sq + 2 * b)] = (float)(byte & 15u) - 8.f;
+        ws[sr * XF_LS + xf_pos(16 * sq + 2 * b + 1)] = (float)(byte >> 4) - 8.f;
+      }
+      if (sq < 2) ss[sr][sq] = psc;
+    }
+    __syncthreads();
+    if (k0 + XF_KE < I) gload(k0 + XF_KE);
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+      float w02[4][4], v[4][4];
+#pragma unroll
+      for (int h = 0; h < 4; h++) {
+        const int jj = h == 0 ? 0 : (h == 1 ? 2 : (h == 2 ? 1 : 3));  // v0, v2, then v1, v3
+        float X[4][8], W[4][8];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          *(float4*)&X[i][0] = *(const float4*)(xs + (ty + 16 * i) * XF_LS + 32 * g + 8 * jj);
+          *(float4*)&X[i][4] = *(const float4*)(xs + (ty + 16 * i) * XF_LS + 32 * g + 8 * jj + 4);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          *(float4*)&W[j][0] = *(const float4*)(ws + (tx + 16 * j) * XF_LS + 32 * g + 8 * jj);
+          *(float4*)&W[j][4] = *(const float4*)(ws + (tx + 16 * j) * XF_LS + 32 * g + 8 * jj + 4);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            // t at j = jj, jj+4, jj+8, jj+12: slots 0..3, partners in slots 4..7
+            float t[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) t[k] = __fmaf_rn(X[i][k], W[j][k], X[i][k + 4] * W[j][k + 4]);
+            const float vv = (t[3] + t[1]) + (t[2] + t[0]);  // u[jj+4] + u[jj]
+            if (h == 0 || h == 2) v[i][j] = vv;
+            else if (h == 1) w02[i][j] = v[i][j] + vv;  // v0 + v2
+            else a[i][j] = __fmaf_rn(w02[i][j] + (v[i][j] + vv), ss[tx + 16 * j][g], a[i][j]);
+          }
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int t = tb + ty + 16 * i;
+    if (t >= M) continue;
+    if (PAIR) {
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const int o = ob + tx + 16 * j;
+        if (o < O) y[(int64_t)t * O + o] = ref_silu_mul(a[i][j], a[i][j + 2]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int o = ob + tx + 16 * j;
+        if (o < O) y[(int64_t)t * O + o] = a[i][j];
+      }
+    }
+  }
+}
+
+// many tokens, exact f32: I % 64 == 0, 16-byte aligned x and 8-byte aligned
+// nibbles; PAIR (q4b): y = silu(gate) * up
+int launch_gemm_i4g_xf(const float* x, const uint8_t* q4, const float* scl, const uint8_t* q4b, const float* sclb,
+                       float* y, int M, int I, int O, hipStream_t st) {
+  if ((I % XF_KE) || (((uintptr_t)x) & 15) || ((((uintptr_t)q4) | ((uintptr_t)q4b)) & 7)) return MOTY_EUNSUP;
+  if (M <= 0 || O <= 0) return MOTY_OK;
+  const int orow = q4b ? XF_BO / 2 : XF_BO;
+  dim3 grid((O + orow - 1) / orow, (M + XF_BT - 1) / XF_BT);
+  if (q4b)
+    hipLaunchKernelGGL(k_gemm_i4g_xf<true>, grid, dim3(256), 0, st, x, q4, scl, q4b, sclb, y, M, I, O);
+  else
+    hipLaunchKernelGGL(k_gemm_i4g_xf<false>, grid, dim3(256), 0, st, x, q4, scl, q4b, sclb, y, M, I, O);
+  LAUNCH_TRY("k_gemm_i4g_xf");
+  return MOTY_OK;
+}
+
 int launch_i4g_f32(const float* x, const uint8_t* q4, const float* scl, float* y, int S, int I, int O,
                    hipStream_t st) {
   if (I % 32) return MOTY_EUNSUP;
