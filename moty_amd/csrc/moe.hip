@@ -532,7 +532,14 @@ __global__ __launch_bounds__(MOTY_WAVE * MT * NW) void k_moe_gemm(
   __shared__ __align__(16) int8_t sA[BM * MG_LS];
   __shared__ __align__(16) int8_t sB[BROWS * MG_LS];
   __shared__ float s_act[BM];
-  const int tile = blockIdx.y;
+  // XCD-aware placement (workgroups go round-robin over the 8 XCDs): the
+  // N-tiles of one M-tile share an XCD, so its activation rows are pulled
+  // into one L2 instead of eight.  Workgroup L runs M-tile 8*(j / nn) + L%8,
+  // N-tile j % nn, with j = L / 8 and nn N-tiles.
+  const int nn = (N + 32 * NW - 1) / (32 * NW);
+  const int jx = blockIdx.x >> 3;
+  const int tile = 8 * (jx / nn) + (blockIdx.x & 7);
+  const int ntile = jx % nn;
   if (tile >= ntiles[0]) return;
   const int2 tm = tiles[tile];
   const int e = tm.x, mb = tm.y;
@@ -544,7 +551,7 @@ __global__ __launch_bounds__(MOTY_WAVE * MT * NW) void k_moe_gemm(
   const int tid = threadIdx.x, lane = tid % MOTY_WAVE, wv = tid / MOTY_WAVE;
   const int sub = wv / NW, wn = wv % NW;  // this wave: sub-tile, 32-row N slice
   const int r32 = lane & 31, h = lane >> 5;
-  const int nb0 = blockIdx.x * BN;
+  const int nb0 = ntile * BN;
   const int msub = mb + 64 * sub;
   const bool one = (nseg - msub) > 0;   // the sub-tile's halves have rows (wave-uniform)
   const bool two = (nseg - msub) > 32;
@@ -1101,21 +1108,24 @@ int launch_moe_experts(const MoeArgs& a, void* scratch, const int* eslot, hipStr
   const MoeBufs m = moe_bufs(a, scratch);
   const int P = a.T * a.K, mt = moe_mt(a);
   const int maxt = P / (64 * mt) + E + 1;
+  // one workgroup per (M-tile, 128-row N-tile), M-tiles padded to a
+  // multiple of the 8 XCDs (the kernel maps workgroup -> tile XCD-aware)
+  const int maxt8 = (maxt + 7) / 8 * 8;
   if (mt == 2)
-    hipLaunchKernelGGL((k_moe_gemm<true, 2, 4>), dim3((I + 127) / 128, maxt), dim3(512), 0, st, m.tiles, m.ntiles,
-                       m.offs, m.slot_tok, m.xq, m.sx, a.G, a.GS, a.U, a.US, m.h, I, D, eslot);
+    hipLaunchKernelGGL((k_moe_gemm<true, 2, 4>), dim3((unsigned)(((I + 127) / 128) * maxt8)), dim3(512), 0, st,
+                       m.tiles, m.ntiles, m.offs, m.slot_tok, m.xq, m.sx, a.G, a.GS, a.U, a.US, m.h, I, D, eslot);
   else
-    hipLaunchKernelGGL((k_moe_gemm<true, 1, 4>), dim3((I + 127) / 128, maxt), dim3(256), 0, st, m.tiles, m.ntiles,
-                       m.offs, m.slot_tok, m.xq, m.sx, a.G, a.GS, a.U, a.US, m.h, I, D, eslot);
+    hipLaunchKernelGGL((k_moe_gemm<true, 1, 4>), dim3((unsigned)(((I + 127) / 128) * maxt8)), dim3(256), 0, st,
+                       m.tiles, m.ntiles, m.offs, m.slot_tok, m.xq, m.sx, a.G, a.GS, a.U, a.US, m.h, I, D, eslot);
   LAUNCH_TRY("k_moe_gemm<gateup>");
   int rc = launch_qrow_i8(m.h, m.hq, m.sh, nullptr, P, I, I, I, st);
   if (rc) return rc;
   if (mt == 2)
-    hipLaunchKernelGGL((k_moe_gemm<false, 2, 4>), dim3((D + 127) / 128, maxt), dim3(512), 0, st, m.tiles, m.ntiles,
-                       m.offs, m.slot_tok, m.hq, m.sh, a.Dn, a.DS, nullptr, nullptr, m.y, D, I, eslot);
+    hipLaunchKernelGGL((k_moe_gemm<false, 2, 4>), dim3((unsigned)(((D + 127) / 128) * maxt8)), dim3(512), 0, st,
+                       m.tiles, m.ntiles, m.offs, m.slot_tok, m.hq, m.sh, a.Dn, a.DS, nullptr, nullptr, m.y, D, I, eslot);
   else
-    hipLaunchKernelGGL((k_moe_gemm<false, 1, 4>), dim3((D + 127) / 128, maxt), dim3(256), 0, st, m.tiles, m.ntiles,
-                       m.offs, m.slot_tok, m.hq, m.sh, a.Dn, a.DS, nullptr, nullptr, m.y, D, I, eslot);
+    hipLaunchKernelGGL((k_moe_gemm<false, 1, 4>), dim3((unsigned)(((D + 127) / 128) * maxt8)), dim3(256), 0, st,
+                       m.tiles, m.ntiles, m.offs, m.slot_tok, m.hq, m.sh, a.Dn, a.DS, nullptr, nullptr, m.y, D, I, eslot);
   LAUNCH_TRY("k_moe_gemm<down>");
   return MOTY_OK;
 }
