@@ -339,8 +339,8 @@ def bench_c2(c, steps, warmup):
     q, k, v, gate and up share their input, so their rows are stored
     concatenated (the fused-rows layout of moty_mat_fuse_rows,
     nn/mat.c:32-68, and of the fused gate_up of nn/ffn.c:28-37) and run as
-    one GEMM; o and down run on their own inputs.  One activation
-    quantization per distinct input."""
+    one GEMM; o and down run on their own inputs.  The three distinct
+    inputs are quantized in one launch (moty_hip_qrow_i8_multi_dev)."""
     torch, ops = c.torch, c.ops
     M = 512
     shapes = [("q", 2048, 1024), ("k", 1024, 1024), ("v", 1024, 1024), ("gate", 3072, 1024), ("up", 3072, 1024),
@@ -356,12 +356,16 @@ def bench_c2(c, steps, warmup):
     xq = {I: torch.empty((M, I), dtype=torch.int8, device="cuda:0") for I in xs}
     sx = {I: torch.empty(M, device="cuda:0") for I in xs}
     lib = ops.lib()
+    import ctypes as C
+    keys = (1024, 2048, 3072)
+    arr = lambda vals: (C.c_void_p * 3)(*vals)
+    qjobs = (arr([xs[I].data_ptr() for I in keys]), arr([xq[I].data_ptr() for I in keys]),
+             arr([sx[I].data_ptr() for I in keys]), (C.c_int * 3)(M, M, M), (C.c_int * 3)(*keys))
 
     def step(ws):
         def f():
-            for I in xs:  # one activation quantization per distinct input
-                ops.check(lib.moty_hip_qrow_i8_dev(ops._p(xs[I]), ops._p(xq[I]), ops._p(sx[I]), None, M, I,
-                                                   ops._stream()), "qrow")
+            # the three distinct inputs quantized in one launch
+            ops.check(lib.moty_hip_qrow_i8_multi_dev(3, *qjobs, ops._stream()), "qrow_multi")
             for I, (q, s) in zip((1024, 2048, 3072), ws):
                 ops.matmul_q8_preq(xq[I], sx[I], q, s, out=ys[I])
         return f

@@ -200,6 +200,14 @@ void moty_hip_hw_matmul_i4(float *y, const float *x, const uint8_t *q4, const fl
 /* qrow_i8 over S rows (hw/hw_quant.h:9-16): q [S][I], sx [S]; xg [S][I/32]
  * group sums when non-NULL (I % 32 == 0). */
 int moty_hip_qrow_i8_dev(const float *x, int8_t *q, float *sx, int32_t *xg, int S, int I, void *stream);
+/* qrow_i8 of up to 4 independent row sets in one launch (job j: x[j] [S[j]][I[j]]
+ * -> q[j], sx[j]; I[j] <= 4096, I[j] % 16 == 0, dense 16-byte aligned rows).
+ * No counterpart in the reference, which quantizes inside each
+ * moty_matmul_q_s call (nn/matmul.c:29-36): for callers that run several
+ * prefill GEMMs whose inputs are all ready, so that their quantizations
+ * pay one launch. */
+int moty_hip_qrow_i8_multi_dev(int n, const float *const *x, int8_t *const *q, float *const *sx, const int *S,
+                               const int *I, void *stream);
 /* moty_quantize_rows (nn/quant.c:12-33) */
 int moty_hip_quantize_rows_dev(const float *w, int8_t *q, float *scale, int O, int I, int bits, void *stream);
 /* moty_pack_int4_grouped (nn/quant.c:57-83); gs % 16 == 0 as the reference requires */

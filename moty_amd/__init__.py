@@ -78,6 +78,7 @@ SIGNATURES = {
     "moty_hip_pack_int4_dev": (I32, [P, P, P, I32, I32, P]),
     "moty_hip_matmul_i4_s_dev": (I32, [P, P, P, P, I32, I32, I32, I32, P]),
     "moty_hip_qrow_i8_dev": (I32, [P, P, P, P, I32, I32, P]),
+    "moty_hip_qrow_i8_multi_dev": (I32, [I32, P, P, P, P, P, P]),
     "moty_hip_quantize_rows_dev": (I32, [P, P, P, I32, I32, I32, P]),
     "moty_hip_pack_int4_grouped_dev": (I32, [P, P, P, I32, I32, I32, P]),
     "moty_hip_matmul_q_s_dev": (I32, [P, P, P, P, I32, I32, I32, P]),

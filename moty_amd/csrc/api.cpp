@@ -288,6 +288,28 @@ int moty_hip_set_ffn1(int on) {
 
 // ---------------- device-pointer entry points ----------------
 
+int moty_hip_qrow_i8_multi_dev(int n, const float* const* x, int8_t* const* q, float* const* sx, const int* S,
+                               const int* I, void* stream) {
+  CUR(d);
+  if (n < 1 || n > QROW_MAX_JOBS || !x || !q || !sx || !S || !I)
+    return set_error("qrow_i8_multi: bad arguments (1 <= n <= %d)", QROW_MAX_JOBS), MOTY_EINVAL;
+  QrowJobs jb = {};
+  jb.n = n;
+  for (int j = 0; j < n; j++) {
+    if (S[j] < 0 || I[j] <= 0 || (S[j] > 0 && (!x[j] || !q[j] || !sx[j])))
+      return set_error("qrow_i8_multi: bad job %d", j), MOTY_EINVAL;
+    jb.x[j] = x[j];
+    jb.q[j] = q[j];
+    jb.sx[j] = sx[j];
+    jb.S[j] = S[j];
+    jb.I[j] = I[j];
+  }
+  const int rc = launch_qrow_multi(jb, STREAM(stream));
+  if (rc == MOTY_EUNSUP)
+    set_error("qrow_i8_multi: every job needs I <= 4096, I %% 16 == 0 and 16-byte aligned x and q");
+  return rc;
+}
+
 int moty_hip_qrow_i8_dev(const float* x, int8_t* q, float* sx, int32_t* xg, int S, int I, void* stream) {
   CUR(d);
   if (S < 0 || I <= 0 || !x || !q || !sx) return set_error("qrow_i8: bad arguments"), MOTY_EINVAL;

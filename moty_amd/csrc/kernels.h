@@ -12,6 +12,17 @@ constexpr int GEMV_MAX_S = 4;  // token rows served by the decode GEMVs
 constexpr int MOE_BM = 64;     // slots per M-tile of the grouped MoE GEMMs
 constexpr int MOE_NBUF = 15;   // MoE scratch sub-buffers
 
+// several qrow_i8 jobs (dense rows, I <= 4096, I % 16 == 0) in one launch
+constexpr int QROW_MAX_JOBS = 4;
+struct QrowJobs {
+  const float* x[QROW_MAX_JOBS];
+  int8_t* q[QROW_MAX_JOBS];
+  float* sx[QROW_MAX_JOBS];
+  int S[QROW_MAX_JOBS], I[QROW_MAX_JOBS];
+  int b0[QROW_MAX_JOBS + 1];  // first workgroup of each job (set by the launcher)
+  int n;
+};
+int launch_qrow_multi(QrowJobs jb, hipStream_t st);
 int launch_qrow_i8(const float* x, int8_t* q, float* sx, int32_t* xg, int S, int I, int64_t ldx, int64_t ldq,
                    hipStream_t st);
 // qrow_i8 with f16 codes in the k-permuted fragment order of the f16-MFMA

@@ -182,6 +182,79 @@ __global__ void k_pack_i4g(const float* __restrict__ w, uint8_t* __restrict__ q4
   }
 }
 
+// Several qrow_i8 jobs in one launch (each I <= 4096, I % 16 == 0, rows
+// dense, 16-byte aligned): workgroups [b0[j], b0[j+1]) take job j, four rows
+// each, one wave per row with the arithmetic of k_qrow_wave.  Only the
+// chunks a job's rows have are loaded (the branch is wave-uniform).
+__global__ __launch_bounds__(256) void k_qrow_multi(QrowJobs jb) {
+  int j = 0;
+#pragma unroll
+  for (int i = 1; i < QROW_MAX_JOBS; i++)
+    if (i < jb.n && (int)blockIdx.x >= jb.b0[i]) j = i;
+  const int S = jb.S[j], I = jb.I[j];
+  const int lane = threadIdx.x % MOTY_WAVE;
+  int64_t row = (int64_t)(blockIdx.x - jb.b0[j]) * 4 + threadIdx.x / MOTY_WAVE;
+  const bool live = row < S;
+  row = live ? row : S - 1;
+  const float* xr = jb.x[j] + row * I;
+  const int nc = (I + 1023) / 1024;
+  float4 v[4][4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const int k = c * 1024 + lane * 16;
+    if (c < nc) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) v[c][q] = *(const float4*)(xr + (k < I ? k : 0) + 4 * q);
+    }
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const bool ok = c < nc && c * 1024 + lane * 16 < I;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      v[c][q] = sel4(ok, v[c][q]);
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[c][q].x), fabsf(v[c][q].y)), fmaxf(fabsf(v[c][q].z), fabsf(v[c][q].w))));
+    }
+  }
+  amax = wave_max_f32(amax);
+  float s = amax / 127.f;
+  if (s < 1e-12f) s = 1e-12f;
+  const float inv = 1.f / s;
+  if (!live) return;
+  if (lane == 0) jb.sx[j][row] = s;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const int k = c * 1024 + lane * 16;
+    if (c >= nc || k >= I) continue;
+    int4 o;
+    int* op = (int*)&o;
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+      op[q] = (int)((uint32_t)(rne_int(v[c][q].x * inv) & 0xff) | ((uint32_t)(rne_int(v[c][q].y * inv) & 0xff) << 8) |
+                    ((uint32_t)(rne_int(v[c][q].z * inv) & 0xff) << 16) |
+                    ((uint32_t)(rne_int(v[c][q].w * inv) & 0xff) << 24));
+    *(int4*)(jb.q[j] + row * I + k) = o;
+  }
+}
+
+int launch_qrow_multi(QrowJobs jb, hipStream_t st) {
+  if (jb.n < 1 || jb.n > QROW_MAX_JOBS) return MOTY_EINVAL;
+  int nb = 0;
+  for (int j = 0; j < jb.n; j++) {
+    if (jb.S[j] < 0 || jb.I[j] <= 0 || jb.I[j] > 4096 || (jb.I[j] % 16)) return MOTY_EUNSUP;
+    if (jb.S[j] > 0 && (!jb.x[j] || !jb.q[j] || !jb.sx[j] || ((((uintptr_t)jb.x[j]) | ((uintptr_t)jb.q[j])) & 15)))
+      return MOTY_EUNSUP;
+    jb.b0[j] = nb;
+    nb += (jb.S[j] + 3) / 4;
+  }
+  for (int j = jb.n; j <= QROW_MAX_JOBS; j++) jb.b0[j] = nb;
+  if (nb == 0) return MOTY_OK;
+  hipLaunchKernelGGL(k_qrow_multi, dim3((unsigned)nb), dim3(256), 0, st, jb);
+  LAUNCH_TRY("k_qrow_multi");
+  return MOTY_OK;
+}
+
 int launch_qrow_i8(const float* x, int8_t* q, float* sx, int32_t* xg, int S, int I, int64_t ldx,
                    int64_t ldq, hipStream_t st) {
   if (S <= 0) return MOTY_OK;

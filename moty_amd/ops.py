@@ -35,6 +35,19 @@ def qrow_i8(x, group_sums=False):
     return q, sx, xg
 
 
+def qrow_i8_multi(xs):
+    """qrow_i8 of up to four row sets in one launch: returns [(q, sx), ...]."""
+    _dev(*xs)
+    n = len(xs)
+    outs = [(torch.empty(x.shape, dtype=torch.int8, device=x.device),
+             torch.empty(x.shape[0], dtype=torch.float32, device=x.device)) for x in xs]
+    arr = lambda vals: (C.c_void_p * n)(*vals)
+    check(lib().moty_hip_qrow_i8_multi_dev(n, arr([x.data_ptr() for x in xs]), arr([q.data_ptr() for q, _ in outs]),
+                                           arr([s.data_ptr() for _, s in outs]), (C.c_int * n)(*[x.shape[0] for x in xs]),
+                                           (C.c_int * n)(*[x.shape[1] for x in xs]), _stream()), "qrow_i8_multi")
+    return outs
+
+
 def quantize_rows(w, bits=8):
     """nn/quant.c:12-33: (q int8 [O,I], scale [O])."""
     _dev(w)

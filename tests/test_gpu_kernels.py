@@ -67,6 +67,22 @@ def test_qrow_i8(ops, S, I):
         assert (to_np(xg) == q2.reshape(S, -1, 32).astype(np.int32).sum(-1)).all()
 
 
+@pytest.mark.parametrize("jobs", [[(512, 1024), (512, 2048), (512, 3072)], [(1, 16)], [(0, 64), (5, 4096)],
+                                  [(3, 48), (7, 2000), (9, 3072), (130, 1008)]])
+def test_qrow_i8_multi(ops, jobs):
+    """Several row sets in one launch, each against the oracle's qrow_i8."""
+    say("qrow multi", jobs)
+    xs = [randn(S * I + j, (S, I)) * 3 for j, (S, I) in enumerate(jobs)]
+    if xs[-1].size:
+        xs[-1][0, :5] = [0.0, -0.0, 1e-30, 5.5, -5.5]
+    outs = ops.qrow_i8_multi([to_dev(x) for x in xs])
+    for x, (q, sx) in zip(xs, outs):
+        if not x.size:
+            continue
+        q2, sx2 = o_qrow(x)
+        assert same_bits(to_np(sx), sx2) and same_bits(to_np(q), q2)
+
+
 @pytest.mark.parametrize("S,I", [(1, 1024), (5, 4096), (3, 48), (7, 2000), (9, 3072), (4, 5008), (6, 1030)])
 def test_qrow_i8_rows(ops, S, I):
     """Without group sums: rows of I <= 4096 (I % 16 == 0) take the
