@@ -437,7 +437,8 @@ def bench_c3(c, steps, warmup):
                                              out=y)
         t, n = c.time_steps([step_f32(w) for w in copies], max(4, steps // (8 if M == 1 else 64)), 4)
         res["M%d_exact_f32" % M] = {"ms_per_step": t * 1e3, "steps": n, "timing": dict(c.last),
-                                    "hbm": roofline("hbm", algo / t / 1e9, HBM_PEAK_GBS, "GB/s"),
+                                    "hbm": roofline("hbm", algo / t / 1e9, HBM_PEAK_GBS, "GB/s",
+                                                    pmc_traffic("hbm_traffic_pmc", "c3_M%d_exact_f32_step" % M)),
                                     "vector_f32": roofline("valu", 2 * M * 3 * I * D / t / 1e12, F32_PEAK_TFLOPS,
                                                            "TFLOP/s")}
     return {"workload": "C3 8B-dense FFN, grouped int4 g32, D=4096, I=12288, M=1 and M=256: IDOT4=1 (int8 "
