@@ -297,3 +297,41 @@ def test_matmul_i4_s_misaligned(ops, idot4):
     import moty_amd
     with pytest.raises(moty_amd.MotyHipError, match="aligned"):
         ops.matmul_i4_s(to_dev(randn(S + I, (S, I))), qv, to_dev(s), idot4)
+
+
+@pytest.mark.parametrize("S", [1, 9])
+def test_i4g_f32_unaligned_activations(ops, S):
+    # the exact-f32 GEMV / tiled GEMM read x in 16-byte units: an activation
+    # view that is only 4-byte aligned takes the lane-per-output kernel, same bits
+    I, O = 1024, 72
+    say("i4g f32 unaligned x", S)
+    q4, s = o_pack_int4_grouped(randn(O + I, (O, I), 0.02))
+    x = randn(S + 5 * I, (S, I))
+    buf = torch.zeros(S * I + 1, dtype=torch.float32, device="cuda")
+    xv = buf[1:].view(S, I)
+    xv.copy_(to_dev(x))
+    y = to_np(ops.matmul_i4_grouped_s(xv, to_dev(q4), to_dev(s), 32, False))
+    y2 = o_matmul_i4g(x, q4, s, False)
+    assert same_bits(y, y2), mismatch(y, y2)
+
+
+def test_qrow_i8_multi_refuses(ops):
+    # job counts outside 1..4, rows past 4096 elements or not a multiple of
+    # 16, and unaligned rows are refused with an error, never run
+    import ctypes as C
+    import moty_amd
+    say("qrow multi refuses")
+    x = torch.zeros((2, 4112), dtype=torch.float32, device="cuda")
+    with pytest.raises(moty_amd.MotyHipError, match="4096"):
+        ops.qrow_i8_multi([x])
+    with pytest.raises(moty_amd.MotyHipError, match="4096"):
+        ops.qrow_i8_multi([torch.zeros((2, 40), dtype=torch.float32, device="cuda")])
+    buf = torch.zeros(2 * 64 + 1, dtype=torch.float32, device="cuda")
+    with pytest.raises(moty_amd.MotyHipError, match="aligned"):
+        ops.qrow_i8_multi([buf[1:].view(2, 64)])
+    with pytest.raises(moty_amd.MotyHipError, match="bad arguments"):
+        ops.qrow_i8_multi([torch.zeros((1, 64), dtype=torch.float32, device="cuda")] * 5)
+    lib = moty_amd.lib()
+    z = (C.c_void_p * 1)()
+    n = (C.c_int * 1)(1)
+    assert lib.moty_hip_qrow_i8_multi_dev(0, z, z, z, n, n, None) != 0
