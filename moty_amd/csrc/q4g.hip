@@ -250,11 +250,14 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
           float wf[32];  // element e = byte e/2, low nibble when e is even, minus 8 (exact)
 #pragma unroll
           for (int q = 0; q < 4; q++) {
-            const uint32_t lo = wd[q] & 0x0f0f0f0fu, hi = (wd[q] >> 4) & 0x0f0f0f0fu;
+            // n - 8 as signed bytes ((n + 0x78) ^ 0x80, carry-free), each
+            // then converted from its byte position
+            const uint32_t lo = ((wd[q] & 0x0f0f0f0fu) + 0x78787878u) ^ 0x80808080u;
+            const uint32_t hi = (((wd[q] >> 4) & 0x0f0f0f0fu) + 0x78787878u) ^ 0x80808080u;
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-              wf[8 * q + 2 * k] = (float)((lo >> (8 * k)) & 0xffu) - 8.f;
-              wf[8 * q + 2 * k + 1] = (float)((hi >> (8 * k)) & 0xffu) - 8.f;
+              wf[8 * q + 2 * k] = (float)(int8_t)(lo >> (8 * k));
+              wf[8 * q + 2 * k + 1] = (float)(int8_t)(hi >> (8 * k));
             }
           }
           float t[16];
