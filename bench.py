@@ -79,23 +79,27 @@ class Ctx:
         return self.ops.pack_int4_grouped(w, 32)
 
     def time_steps(self, fns, steps, warmup, replays=7):
-        """Time exactly `steps` steps: step k runs fns[k % len(fns)] (the
-        weight copies rotate), captured into one HIP graph; `warmup` steps
-        from a second graph run just before it on the same stream, so the
-        timed graph is queued while the GPU is still busy and no launch gap
-        enters the timed region.  Each of `replays` rounds, on a stream of
-        its own, times the warm-up graph alone between two HIP events, then
-        the warm-up and timed graphs together between two more; the K steps'
-        time is the difference, so the fixed cost of an event pair around a
-        graph launch cancels instead of being spread over the K steps (at the
-        driver's K = 20 it added 0.45 us to each 5.7 us C1 step).  The result
-        is the median round's seconds per step (self.last holds the round
-        count, the spread and the raw warm-up + timed figure).  Returns
-        (seconds per step, steps timed)."""
+        """Time exactly `steps` steps, `replays` times: step k of a run
+        calls one fns[i] (each fn a step over its own weight copy).  Every
+        round r captures three HIP graphs over consecutive copies: warm-up A
+        (`warmup` steps), warm-up B (`warmup` steps) and the K timed steps;
+        round r starts where round r-1 ended, so with enough copies no copy
+        is touched twice within the Infinity Cache's reach.  After one
+        untimed replay of every graph (the first replay uploads it), each
+        round times A alone between two HIP events, then B followed by the
+        timed graph between two more: B's graph is queued behind the events
+        while the GPU is still busy, and A and B do the same work on cold
+        copies, so the difference is the time the K steps add, with the fixed
+        cost of an event pair around a graph launch (about 9 us on MI355X,
+        0.45 us per C1 step at the driver's K = 20) cancelled.  The result is
+        the median round's seconds per step (self.last holds the round count,
+        the spread and the raw B + timed figure).  Returns (seconds per step,
+        steps timed)."""
         torch = self.torch
         n = len(fns)
         steps = max(1, int(steps))
         warmup = max(1, int(warmup))
+        replays = max(1, int(replays))
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
@@ -110,30 +114,24 @@ class Ctx:
                 for k in range(count):
                     fns[(first + k) % n]()
             return g
-        timed = capture(0, steps)
-        # the warm-up steps run the copies that precede copy 0 in cyclic
-        # order, ending with copy n-1: every timed copy is then either
-        # untouched by the warm-up or was touched at its start, with the
-        # rest of the rotation (more than the 256 MB Infinity Cache) after it
-        warm = capture((-warmup) % n, warmup)
-        ts = []
+        rounds = []
+        per = 2 * warmup + steps
+        for r in range(replays):
+            b = r * per
+            rounds.append((capture(b, warmup), capture(b + warmup, warmup), capture(b + 2 * warmup, steps)))
+        ts, raw = [], []
         with torch.cuda.stream(s):
-            warm.replay()  # first replay of each graph uploads it
-            timed.replay()
+            for gs in rounds:
+                for g in gs:
+                    g.replay()
             torch.cuda.synchronize()
-            raw = []
-            for _ in range(max(1, replays)):
+            for wa, wb, timed in rounds:
                 ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
-                # the warm-up alone between two events, then the warm-up and
-                # the K timed steps between two events: the difference is the
-                # time the K steps add, with the fixed cost of an event pair
-                # around a graph launch (about 9 us on MI355X, 0.45 us per
-                # step at K = 20) cancelled
                 ev[0].record(s)
-                warm.replay()
+                wa.replay()
                 ev[1].record(s)
                 ev[2].record(s)
-                warm.replay()
+                wb.replay()
                 timed.replay()
                 ev[3].record(s)
                 torch.cuda.synchronize()
@@ -141,11 +139,13 @@ class Ctx:
                 twk = ev[2].elapsed_time(ev[3]) / 1e3
                 ts.append((twk - tw) / steps)
                 raw.append(twk)
+        del rounds
         ts.sort()
         raw.sort()
         med = ts[len(ts) // 2]
         self.last = {"replays": len(ts), "spread_us": [round(ts[0] * 1e6, 3), round(ts[-1] * 1e6, 3)],
-                     "method": "median over replays of (warm-up + K steps) - (warm-up alone), each between HIP events",
+                     "method": "per round: (warm-up B + K steps) - (warm-up A), each between HIP events, over "
+                               "copies no earlier round touched when the copies allow; median over rounds",
                      "warm_plus_timed_us_median": round(raw[len(raw) // 2] * 1e6, 1)}
         return med, steps
 
@@ -186,7 +186,11 @@ def bench_c1(c, steps, warmup):
     D, I = 1024, 3072
     wbytes = 3 * D * I + (2 * I + D) * 4           # int8 weights + f32 row scales
     algo = wbytes + 2 * D * 4                      # + x in, out
-    ncopy = n_copies(wbytes)
+    # 4.8 GB of copies: the Infinity Cache keeps some lines of the copies
+    # written last at set-up, so a 1.2 GB rotation (133 copies) read part of
+    # its bytes from there (5.59 against 5.92 us per step at 266 copies and
+    # 5.88 at 532)
+    ncopy = n_copies(wbytes, target=4800 << 20)
     g = c.gen(0, 1)
     copies = [c.q8((I, D), g) + c.q8((I, D), g) + c.q8((D, I), g) for _ in range(ncopy)]
     x = c.randn((1, D), c.gen(0, 2))
@@ -477,7 +481,7 @@ def bench_q8_gemv_sizes(c, steps, warmup):
     for O, I in ((4096, 4096), (12288, 4096)):
         wbytes = O * I + O * 4
         g = c.gen(7, O)
-        copies = [c.q8((O, I), g) for _ in range(n_copies(wbytes))]
+        copies = [c.q8((O, I), g) for _ in range(n_copies(wbytes, target=4800 << 20))]
         x = c.randn((1, I), c.gen(7, 1))
         res["_cpu"]["gemv_%dx%d" % (O, I)] = (x, copies[0], wbytes + (I + O) * 4)
         y = torch.empty((1, O), device="cuda:0")
@@ -489,7 +493,7 @@ def bench_q8_gemv_sizes(c, steps, warmup):
     D, I = 4096, 12288
     wbytes = 2 * (I * D + I * 4)
     g = c.gen(7, 2)
-    copies = [c.q8((I, D), g) + c.q8((I, D), g) for _ in range(n_copies(wbytes))]
+    copies = [c.q8((I, D), g) + c.q8((I, D), g) for _ in range(n_copies(wbytes, target=4800 << 20))]
     x = c.randn((1, D), c.gen(7, 3))
     h = torch.empty((1, I), device="cuda:0")
     t, n = c.time_steps([lambda w=w: ops.gate_up_silu_q8(x, w[0], w[1], w[2], w[3], out=h) for w in copies],

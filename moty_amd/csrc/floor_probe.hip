@@ -145,7 +145,9 @@ extern "C" int moty_probe_floor(float* out) {
   PT(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
   int* o;
   PT(hipMalloc(&o, 256));
-  const int NCP = 133;
+  // 512 copies (5 GB): every graph below touches the first 266, and the
+  // Infinity Cache keeps some lines of the last ones the memset wrote
+  const int NCP = 512;
   const size_t MAXB = 10u << 20;
   int8_t* big;
   PT(hipMalloc(&big, NCP * MAXB));
