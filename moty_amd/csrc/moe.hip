@@ -738,13 +738,13 @@ __global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ y
 //   k_moe_d1_gateup  wave per 4 rows of one routed expert: gate and up rows
 //                    against the token's int8 row, (s*sx)*acc, silu(g)*u
 //                    (nn/moe.c:99-127) -> h [K][I] f32
-//   k_moe_d1_down    each workgroup loads h once, quantizes every expert's row
-//                    into LDS (qrow_i8 per expert, nn/moe.c:129-139), then a
-//                    wave per output row d: the K experts' down dots,
-//                    (ds*sh)*acc (nn/moe.c:146-152), and the weighted sum in
-//                    the reference's order (out = fma(w_k, v_k, out), k in
-//                    top-k order; ascending expert id for nn/moe.c's batch
-//                    order), written once (no per-pair rows, no combine pass).
+//   k_moe_d1_down_ew a wave per routed expert and RPW output rows: the
+//                    expert's h row quantized in registers (qrow_i8,
+//                    nn/moe.c:129-139), its down dots, (ds*sh)*acc
+//                    (nn/moe.c:146-152); then the weighted sum in the
+//                    reference's order (out = fma(w_k, v_k, out), k in top-k
+//                    order; ascending expert id for nn/moe.c's batch order),
+//                    written once (no per-pair rows, no combine pass).
 constexpr int D1_NW = 4;  // waves per workgroup
 
 __device__ __forceinline__ int4 d1_ldnt16(const int8_t* p) {
@@ -875,129 +875,126 @@ __global__ __launch_bounds__(D1_NW * MOTY_WAVE) void k_moe_d1_gateup(
   if ((lane & 15) == 0 && i0 + rl < I) h[(int64_t)k * I + i0 + rl] = v;
 }
 
-// KC: 1 KiB chunks of a down row (I); RPW output rows per wave; KM >= K
+// The decode down projection, one wave per routed expert: workgroup = KM
+// waves over RPW output rows; wave j takes the expert of combine rank j,
+// loads that expert's h row and its RPW down rows, quantizes the h row in
+// registers (a wave max is the row's amax: qrow_i8 with no workgroup
+// barrier), forms its RPW dots and (ds*sh)*acc, and parks them in LDS; after
+// one barrier the first wave runs the ordered weighted sum per row.  A wave
+// thus holds one h row and RPW weight rows in flight, not every expert's:
+// against one workgroup quantizing all K rows of h for 2 rows per wave, the
+// decode MoE at the C4 shape 23.8 -> 21.4 us per token (RPW 8; 4: 22.0,
+// 16: 22.3).
 template <int KC, int RPW, int KM>
-__global__ __launch_bounds__(D1_NW * MOTY_WAVE) void k_moe_d1_down(
+__global__ __launch_bounds__(KM * MOTY_WAVE) void k_moe_d1_down_ew(
     const int* __restrict__ idx, const float* __restrict__ w, const float* __restrict__ h,
     const int8_t* __restrict__ Dn, const float* __restrict__ DS, float* __restrict__ out, int D, int I, int K, int E,
     int order, int* __restrict__ counts) {
-  constexpr int NT = D1_NW * MOTY_WAVE;
-  constexpr int NU = KM * KC * 256;       // float4 units of h (rows padded to KC KiB)
-  constexpr int HJ = (NU + NT - 1) / NT;  // per thread
-  __shared__ __align__(16) int8_t hq_s[KM][KC * 1024];
-  __shared__ unsigned amax_s[KM];
-  __shared__ float sh_s[KM], w_s[KM];
-  __shared__ int e_s[KM], k_s[KM];
-  const int lane = threadIdx.x % MOTY_WAVE, wv = threadIdx.x / MOTY_WAVE;
-  const int d0 = (blockIdx.x * D1_NW + wv) * RPW;
-  // the routed experts in combine order: k order, or ascending expert id
-  // (the K ids of a token are distinct); rank j holds expert e_s[j], whose
-  // h row is k_s[j]
-  if (threadIdx.x < MOTY_WAVE) {
-    const int k = threadIdx.x;
-    const int e = k < K ? idx[k] : 0x7fffffff;
-    int rank = k;
-    if (order == 1) {
-      rank = 0;
-      for (int j = 0; j < K; j++) rank += (__shfl(e, j, 64) < e) ? 1 : 0;
-    }
-    if (k < K) {
-      e_s[rank] = e;
-      k_s[rank] = k;
-      w_s[rank] = w[k];
-    }
-    if (k < KM) amax_s[k] = 0u;
+  __shared__ float val_s[KM][RPW];
+  const int lane = threadIdx.x % MOTY_WAVE, j = threadIdx.x / MOTY_WAVE;
+  const int d0 = blockIdx.x * RPW;
+  // the expert of combine rank j: rank k = k (top-k order) or the number of
+  // smaller expert ids (ascending order; a token's K ids are distinct)
+  const int ek = lane < K ? idx[lane] : 0x7fffffff;
+  int rank = lane;
+  if (order == 1) {
+    rank = 0;
+    for (int q = 0; q < K; q++) rank += (__shfl(ek, q, 64) < ek) ? 1 : 0;
   }
-  __syncthreads();
-  // every routed expert's h row first (small and cache-resident: it lands
-  // before the weight stream and its quantization overlaps it), then this
-  // wave's down rows of every routed expert (rows clamped, experts past K
-  // repeat rank 0's and are not used; columns past I meet zero codes), with
-  // their row scales
-  float4 hv[HJ];
+  const unsigned long long hit = __ballot(lane < K && rank == j);
+  const bool live = j < K && hit != 0ull;
+  const int kj = live ? (int)__builtin_ctzll(hit) : 0;  // h row of this rank
+  const int e0 = __shfl(ek, kj, 64);
+  const bool use = live && e0 >= 0;
+  const int e = use ? e0 : 0;
+  const float wj = w[kj];
+  // loads: the h row, then the RPW down rows and their scales
+  float4 hv[KC][4];
 #pragma unroll
-  for (int j = 0; j < HJ; j++) {
-    const int u = threadIdx.x + j * NT, row = u / (KC * 256), col = (u % (KC * 256)) * 4;
-    const bool in = row < K && col < I;
-    const float4 v = *(const float4*)(h + (in ? (int64_t)k_s[row] * I + col : 0));
-    hv[j] = sel4(in, v);
-  }
-  int4 wd[RPW][KM][KC];
-  float dsc[RPW][KM];
+  for (int c = 0; c < KC; c++) {
+    const int kk = c * 1024 + lane * 16;
 #pragma unroll
-  for (int j = 0; j < KM; j++) {
-    const int e0 = e_s[j < K ? j : 0], e = e0 < 0 ? 0 : e0;
-#pragma unroll
-    for (int r = 0; r < RPW; r++) {
-      const int d = d0 + r < D ? d0 + r : D - 1;
-      const int8_t* dr = Dn + ((int64_t)e * D + d) * I;
-#pragma unroll
-      for (int c = 0; c < KC; c++) {
-        const int kk = c * 1024 + lane * 16;
-        wd[r][j][c] = d1_ldnt16(dr + (kk < I ? kk : 0));
-      }
-      dsc[r][j] = DS[(int64_t)e * D + d];
-    }
+    for (int q = 0; q < 4; q++) hv[c][q] = *(const float4*)(h + (int64_t)kj * I + (kk < I ? kk : 0) + 4 * q);
   }
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int j = 0; j < HJ; j++) {
-    const int u = threadIdx.x + j * NT, row = u / (KC * 256);
-    const float4 v = hv[j];
-    // fmaxf drops NaN as the reference's `a > amax` does
-    const float m = fmaxf(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))), 0.f);
-    if (row < K) atomicMax(&amax_s[row], __float_as_uint(m));
-  }
-  __syncthreads();
-  if (threadIdx.x < KM) {
-    float sc = __uint_as_float(amax_s[threadIdx.x]) / 127.f;
-    if (sc < 1e-12f) sc = 1e-12f;
-    sh_s[threadIdx.x] = sc;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < HJ; j++) {
-    const int u = threadIdx.x + j * NT, row = u / (KC * 256), col = (u % (KC * 256)) * 4;
-    if (row < KM) {
-      const float inv = 1.f / sh_s[row];
-      const float4 v = hv[j];
-      *(uint32_t*)(&hq_s[row][col]) =
-          (uint32_t)(rne_int(v.x * inv) & 0xff) | ((uint32_t)(rne_int(v.y * inv) & 0xff) << 8) |
-          ((uint32_t)(rne_int(v.z * inv) & 0xff) << 16) | ((uint32_t)(rne_int(v.w * inv) & 0xff) << 24);
-    }
-  }
-  __syncthreads();
-  if (blockIdx.x == 0 && counts && threadIdx.x < E) {
-    int c = 0;
-    for (int j = 0; j < K; j++) c += e_s[j] == (int)threadIdx.x;
-    counts[threadIdx.x] = c;
-  }
-  // per row: the K experts' dots, (ds*sh)*acc, then the ordered weighted
-  // sum out = fma(w, v, out) from 0 (nn/moe.c:146-152 and 200-202)
+  int4 wd[RPW][KC];
 #pragma unroll
   for (int r = 0; r < RPW; r++) {
-    int acc[KM];
+    const int d = d0 + r < D ? d0 + r : D - 1;
+    const int8_t* dr = Dn + ((int64_t)e * D + d) * I;
 #pragma unroll
-    for (int j = 0; j < KM; j++) {
-      acc[j] = 0;
-#pragma unroll
-      for (int c = 0; c < KC; c++)
-        acc[j] = dot16(wd[r][j][c], *(const int4*)(&hq_s[j][c * 1024 + lane * 16]), acc[j]);
+    for (int c = 0; c < KC; c++) {
+      const int kk = c * 1024 + lane * 16;
+      wd[r][c] = d1_ldnt16(dr + (kk < I ? kk : 0));
     }
+  }
+  constexpr int RS = RPW < 4 ? RPW : 4;  // rows per wave sum
+  const int rl = wave_sum_row<RS>(lane);
+  float dsc[RPW / RS];
+#pragma unroll
+  for (int t = 0; t < RPW / RS; t++) dsc[t] = DS[(int64_t)e * D + (d0 + t * RS + rl < D ? d0 + t * RS + rl : D - 1)];
+  __builtin_amdgcn_sched_barrier(0);
+  // qrow_i8 of the h row in registers (fmaxf drops NaN as the reference's
+  // `a > amax` does)
+  float amax = 0.f;
+#pragma unroll
+  for (int c = 0; c < KC; c++)
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      hv[c][q] = sel4(c * 1024 + lane * 16 < I, hv[c][q]);
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(hv[c][q].x), fabsf(hv[c][q].y)), fmaxf(fabsf(hv[c][q].z), fabsf(hv[c][q].w))));
+    }
+  amax = wave_max_f32(amax);
+  float sh = amax / 127.f;
+  if (sh < 1e-12f) sh = 1e-12f;
+  const float inv = 1.f / sh;
+  int4 hq[KC];
+#pragma unroll
+  for (int c = 0; c < KC; c++) {
+    int* qp = (int*)&hq[c];
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+      qp[q] = (int)((uint32_t)(rne_int(hv[c][q].x * inv) & 0xff) | ((uint32_t)(rne_int(hv[c][q].y * inv) & 0xff) << 8) |
+                    ((uint32_t)(rne_int(hv[c][q].z * inv) & 0xff) << 16) |
+                    ((uint32_t)(rne_int(hv[c][q].w * inv) & 0xff) << 24));
+  }
+  int acc[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    acc[r] = 0;
+#pragma unroll
+    for (int c = 0; c < KC; c++) acc[r] = dot16(wd[r][c], hq[c], acc[r]);
+  }
+#pragma unroll
+  for (int t = 0; t < RPW / RS; t++) {
+    int part[RS];
+#pragma unroll
+    for (int q = 0; q < RS; q++) part[q] = acc[t * RS + q];
+    const int a = wave_sum_multi_i32<RS>(part);
+    if ((lane & (MOTY_WAVE / RS - 1)) == 0) val_s[j][t * RS + rl] = (dsc[t] * sh) * (float)a;
+  }
+  if (blockIdx.x == 0 && j == 0 && counts) {
+    for (int x = lane; x < E; x += MOTY_WAVE) {
+      int cnt = 0;
+      for (int q = 0; q < K; q++) cnt += __shfl(ek, q, 64) == x;
+      counts[x] = cnt;
+    }
+  }
+  // each wave's weight of its rank, for the combine
+  __shared__ float w_s[KM];
+  __shared__ int u_s[KM];
+  if (lane == 0) {
+    w_s[j] = wj;
+    u_s[j] = use ? 1 : 0;
+  }
+  __syncthreads();
+  // the ordered weighted sum out = fma(w, v, out) from 0 (nn/moe.c:146-152
+  // and 200-202), one lane per row
+  if (j == 0 && lane < RPW && d0 + lane < D) {
     float o = 0.f;
 #pragma unroll
-    for (int j0 = 0; j0 < KM; j0 += 4) {
-      const int a4[4] = {acc[j0], acc[j0 + 1], acc[j0 + 2], acc[j0 + 3]};
-      const int a = wave_sum_multi_i32<4>(a4);  // lanes 0, 32, 16, 48 hold experts j0 + 0, 1, 2, 3
-      const int tot[4] = {__builtin_amdgcn_readlane(a, 0), __builtin_amdgcn_readlane(a, 32),
-                          __builtin_amdgcn_readlane(a, 16), __builtin_amdgcn_readlane(a, 48)};
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const int j = j0 + q;
-        if (j < K && e_s[j] >= 0) o = __fmaf_rn(w_s[j], (dsc[r][j] * sh_s[j]) * (float)tot[q], o);
-      }
-    }
-    if (lane == 0 && d0 + r < D) out[d0 + r] = o;
+    for (int q = 0; q < KM; q++)
+      if (q < K && u_s[q]) o = __fmaf_rn(w_s[q], val_s[q][lane], o);
+    out[d0 + lane] = o;
   }
 }
 
@@ -1176,18 +1173,17 @@ static int launch_moe_d1(const MoeArgs& a, void* scratch, hipStream_t st) {
   }
 #undef GU
   LAUNCH_TRY("k_moe_d1_gateup");
-  // two rows per wave (one per wave when that leaves fewer than 256
-  // workgroups)
-  const int rpw = D / (2 * D1_NW) >= 256 ? 2 : 1;
-  const unsigned dn_blocks = (unsigned)((D + rpw * D1_NW - 1) / (rpw * D1_NW));
-#define DN(KC, R)                                                                                             \
+  // eight output rows per workgroup of one wave per routed expert (four
+  // for rows of 3-4 KiB)
+  const int rpw = kc <= 2 ? 8 : 4;
+#define DE(KC, R)                                                                                             \
   if (kc == KC && rpw == R) {                                                                                 \
-    hipLaunchKernelGGL((k_moe_d1_down<KC, R, 8>), dim3(dn_blocks), dim3(D1_NW * MOTY_WAVE), 0, st, m.idx, m.w,  \
+    hipLaunchKernelGGL((k_moe_d1_down_ew<KC, R, 8>), dim3((D + R - 1) / R), dim3(8 * MOTY_WAVE), 0, st, m.idx, m.w, \
                        m.h, a.Dn, a.DS, a.out, D, I, K, a.E, a.order, m.counts);                               \
-    LAUNCH_TRY("k_moe_d1_down");                                                                              \
+    LAUNCH_TRY("k_moe_d1_down_ew");                                                                            \
   }
-  DN(1, 1) DN(1, 2) DN(2, 1) DN(2, 2) DN(3, 1) DN(3, 2) DN(4, 1) DN(4, 2)
-#undef DN
+  DE(1, 8) DE(2, 8) DE(3, 4) DE(4, 4)
+#undef DE
   if (a.idx_out) HIP_TRY(hipMemcpyAsync(a.idx_out, m.idx, (size_t)K * 4, hipMemcpyDeviceToDevice, st));
   if (a.w_out) HIP_TRY(hipMemcpyAsync(a.w_out, m.w, (size_t)K * 4, hipMemcpyDeviceToDevice, st));
   if (a.counts_out) HIP_TRY(hipMemcpyAsync(a.counts_out, m.counts, (size_t)a.E * 4, hipMemcpyDeviceToDevice, st));
