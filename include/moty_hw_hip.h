@@ -297,7 +297,8 @@ int moty_hip_pack_q8r4_dev(const float *w, int8_t *q8, uint16_t *s16, int O, int
 int moty_hip_gguf_dequant_dev(int dtype, const void *raw, int64_t numel, float *out, void *stream);
 int moty_hip_gguf_repack_q4_0_dev(const uint8_t *blocks, uint8_t *q4, float *qs, int64_t O, int64_t I,
                                   void *stream);
-/* the MoE layer, all pointers in m and x/out on the device */
+/* the MoE layer, all pointers in m and x/out on the device; x, out, router
+ * and g/u/d 16-byte aligned (MOTY_HIP_EUNSUP otherwise) */
 int moty_hip_moe_topk_dev(const MotyHipMoe *m, const float *x, int S, float *out, void *stream);
 /* No counterpart in the reference: for callers that cannot allocate (code
  * under HIP graph capture, tight serving loops, harnesses that forbid

@@ -536,6 +536,12 @@ static int moe_check(const MotyHipMoe* m, const float* x, float* out, int S, con
     set_error("%s: D=%d I=%d E=%d unsupported (D, I multiples of 32, E <= 256)", what, m->D, m->I, m->E);
     return MOTY_EUNSUP;
   }
+  // the kernels move x, out, the router and the expert rows in 16-byte units
+  if (S > 0 && ((((uintptr_t)x) | ((uintptr_t)out) | ((uintptr_t)m->router) | ((uintptr_t)m->g) |
+                 ((uintptr_t)m->u) | ((uintptr_t)m->d)) & 15)) {
+    set_error("%s: x, out, router and the g/u/d expert tensors must be 16-byte aligned", what);
+    return MOTY_EUNSUP;
+  }
   return MOTY_OK;
 }
 

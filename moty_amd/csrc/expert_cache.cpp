@@ -342,6 +342,9 @@ int moty_hip_moe_topk_cached_dev(const MotyHipMoe* m, MotyHipExpertCache* c, voi
   if ((D % 32) || (I % 32) || E > 256)
     return set_error("moe_topk_cached: D=%d I=%d E=%d unsupported (D, I multiples of 32, E <= 256)", D, I, E),
            MOTY_EUNSUP;
+  // the kernels move x, out and the router rows in 16-byte units
+  if ((((uintptr_t)x) | ((uintptr_t)out) | ((uintptr_t)m->router)) & 15)
+    return set_error("moe_topk_cached: x, out and router must be 16-byte aligned"), MOTY_EUNSUP;
   int rc = ec_check(c, 0, fn, "moe_topk_cached");
   if (rc) return rc;
   if ((rc = ec_alloc(c, I, D))) return rc;

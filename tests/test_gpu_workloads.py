@@ -229,3 +229,19 @@ def test_c3_i4g_dense_ffn(ops, c3_weights, M):
     h = o_silu(o_matmul_i4g(x, gq, gs, True), o_matmul_i4g(x, uq, us, True))
     y2 = o_matmul_i4g(h, dq, ds, True)
     assert same_bits(y, y2), mismatch(y, y2)
+
+
+def test_moe_refuses_unaligned(ops):
+    # the MoE kernels move x, out, the router and the expert rows in 16-byte
+    # units: a 4-byte-aligned activation view is refused, never read
+    import moty_amd
+    E, K, I, D = 8, 2, 64, 96
+    say("moe unaligned")
+    ex = fast_moe_weights(E, I, D, seed=90)
+    Wr = randn(91, (E, D), 0.02)
+    L = moe_layer(ops, Wr, ex, K, 1, moty_amd.ORDER_EXPERT)
+    buf = torch.zeros(2 * D + 1, dtype=torch.float32, device="cuda")
+    xv = buf[1:].view(2, D)
+    xv.copy_(to_dev(randn(92, (2, D))))
+    with pytest.raises(moty_amd.MotyHipError, match="16-byte aligned"):
+        L(xv)
