@@ -288,6 +288,17 @@ int moty_hip_set_ffn1(int on) {
 
 // ---------------- device-pointer entry points ----------------
 
+// the kernels move activations and weight rows in 16-byte units: pointers
+// that are not 16-byte aligned are refused rather than read out of line
+static int need_al16(const char* what, const void* a, const void* b, const void* c = nullptr,
+                     const void* e = nullptr) {
+  if ((((uintptr_t)a) | ((uintptr_t)b) | ((uintptr_t)c) | ((uintptr_t)e)) & 15) {
+    set_error("%s: activations and weights must be 16-byte aligned", what);
+    return MOTY_EUNSUP;
+  }
+  return MOTY_OK;
+}
+
 int moty_hip_qrow_i8_multi_dev(int n, const float* const* x, int8_t* const* q, float* const* sx, const int* S,
                                const int* I, void* stream) {
   CUR(d);
@@ -335,6 +346,7 @@ int moty_hip_matmul_q8_preq_dev(float* y, const int8_t* xq, const float* sx, con
                                 int S, int I, int O, void* stream) {
   CUR(d);
   if (S < 0 || I <= 0 || O < 0) return set_error("matmul_q8_preq: bad shape"), MOTY_EINVAL;
+  if (S > 0 && O > 0 && need_al16("matmul_q8_preq", xq, q)) return MOTY_EUNSUP;
   int rc = launch_gemm_q8(xq, sx, q, scale, y, S, I, O, STREAM(stream));
   if (rc == MOTY_EUNSUP) set_error("matmul_q8_preq: I=%d must be a multiple of 16", I);
   return rc;
@@ -345,6 +357,7 @@ int moty_hip_matmul_q_s_dev(float* y, const float* x, const int8_t* q, const flo
   CUR(d);
   if (S < 0 || I <= 0 || O < 0 || !y || !x || !q || !scale) return set_error("matmul_q_s: bad arguments"), MOTY_EINVAL;
   if (S == 0 || O == 0) return MOTY_OK;
+  if (need_al16("matmul_q_s", x, q)) return MOTY_EUNSUP;
   if (I > 16384 || (I % 16)) {
     set_error("matmul_q_s: I=%d unsupported (needs I %% 16 == 0, I <= 16384)", I);
     return MOTY_EUNSUP;
@@ -370,6 +383,7 @@ int moty_hip_matmul_i4_grouped_s_dev(float* y, const float* x, const uint8_t* q4
   if (S == 0 || O == 0) return MOTY_OK;
   hipStream_t st = STREAM(stream);
   if (idot4 && gs == 32 && (I % 64) == 0 && I <= 16384) {
+    if (need_al16("matmul_i4_grouped_s", x, q4)) return MOTY_EUNSUP;
     if (S <= 4) return launch_gemv_i4g(x, q4, scale, nullptr, nullptr, y, S, I, O, st);
     void* sp;
     if (gemm_i4g_h_fits(S, I, O) && !(((uintptr_t)x | (uintptr_t)q4 | (uintptr_t)scale) & 15)) {
@@ -472,6 +486,7 @@ int moty_hip_gate_up_silu_q8_dev(float* h, const float* x, int S, const int8_t* 
     set_error("gate_up_silu_q8: S=%d D=%d unsupported (S <= %d, D %% 16 == 0)", S, D, GEMV_MAX_S);
     return MOTY_EUNSUP;
   }
+  if (need_al16("gate_up_silu_q8", x, gate, up)) return MOTY_EUNSUP;
   return launch_gemv_q8(x, gate, gs, up, us, h, S, D, I, STREAM(stream));
 }
 
@@ -480,6 +495,7 @@ int moty_hip_gate_up_silu_i4g_dev(float* h, const float* x, const uint8_t* gate,
   CUR(d);
   if (D <= 0 || I <= 0 || !h || !x || !gate || !gs || !up || !us)
     return set_error("gate_up_silu_i4g: bad arguments"), MOTY_EINVAL;
+  if (need_al16("gate_up_silu_i4g", x, gate, up)) return MOTY_EUNSUP;
   int rc = launch_gemv_i4g(x, gate, gs, up, us, h, 1, D, I, STREAM(stream));
   if (rc == MOTY_EUNSUP) set_error("gate_up_silu_i4g: D=%d unsupported (D %% 64 == 0, D <= 16384)", D);
   return rc;
@@ -491,6 +507,7 @@ int moty_hip_dense_ffn_q8_dev(float* out, const float* x, int S, const int8_t* g
   CUR(d);
   if (S < 0 || D <= 0 || I <= 0) return set_error("dense_ffn_q8: bad shape"), MOTY_EINVAL;
   if (S == 0) return MOTY_OK;
+  if (need_al16("dense_ffn_q8", x, gate, up, down)) return MOTY_EUNSUP;
   if ((D % 16) || (I % 16) || D > 16384 || I > 16384) {
     set_error("dense_ffn_q8: D=%d I=%d unsupported", D, I);
     return MOTY_EUNSUP;
@@ -583,6 +600,8 @@ int moty_hip_dense_ffn_i4g_dev(float* out, const float* x, int S, const uint8_t*
     return set_error("dense_ffn_i4g: bad arguments"), MOTY_EINVAL;
   if (S == 0) return MOTY_OK;
   if ((D % 32) || (I % 32)) return set_error("dense_ffn_i4g: D=%d I=%d must be multiples of 32", D, I), MOTY_EUNSUP;
+  // the exact-f32 path falls back to byte-granular kernels; IDOT4 needs alignment
+  if (idot4 && need_al16("dense_ffn_i4g", x, gate, up, down)) return MOTY_EUNSUP;
   hipStream_t st = STREAM(stream);
   const bool vec = idot4 && (D % 64) == 0 && (I % 64) == 0 && D <= 16384 && I <= 16384;  // both matrices
   const bool h16 = vec && S > 4 && gemm_i4g_h_fits(S, D, I) && gemm_i4g_h_fits(S, I, D) &&
@@ -720,6 +739,7 @@ static int r4_dev(bool q8, const char* what, float* y, const float* x, const uin
   CUR(d);
   int rc = r4_check(what, S, I, O, y, x, q, s16);
   if (rc || S == 0 || O == 0) return rc;
+  if (need_al16(what, x, q)) return MOTY_EUNSUP;
   void* sp = nullptr;
   int8_t* xq = nullptr;
   float* xs = nullptr;
@@ -777,6 +797,7 @@ static int r4_gate_up(bool q8, const char* what, float* h, const float* x, const
   CUR(d);
   if (D <= 0 || I <= 0 || !h || !x || !gu || !s16) return set_error("%s: bad arguments", what), MOTY_EINVAL;
   if (D % 32 || I % 4) return set_error("%s: D=%d (multiple of 32), I=%d (multiple of 4)", what, D, I), MOTY_EINVAL;
+  if (need_al16(what, x, gu)) return MOTY_EUNSUP;
   hipStream_t st = STREAM(stream);
   int rc = launch_r4_gate_up_silu(q8, x, gu, s16, h, D, I, st);
   if (rc != MOTY_EUNSUP) return rc;
@@ -814,6 +835,7 @@ static int r4_ffn(bool q8, const char* what, float* out, const float* x, int S, 
     return set_error("%s: bad arguments", what), MOTY_EINVAL;
   if (D % 32 || I % 32) return set_error("%s: D=%d, I=%d must be multiples of 32", what, D, I), MOTY_EINVAL;
   if (S == 0) return MOTY_OK;
+  if (need_al16(what, x, gu, dn)) return MOTY_EUNSUP;
   hipStream_t st = STREAM(stream);
   // scratch: h [S][I] | gu [S][2I] | activation codes for the GEMMs
   const int W = D > I ? D : I;

@@ -335,3 +335,18 @@ def test_qrow_i8_multi_refuses(ops):
     z = (C.c_void_p * 1)()
     n = (C.c_int * 1)(1)
     assert lib.moty_hip_qrow_i8_multi_dev(0, z, z, z, n, n, None) != 0
+
+
+def test_q8_refuses_unaligned_weights(ops):
+    # the Q8 GEMV/GEMM read weight rows in 16-byte units: a weight view one
+    # byte off is refused with an error, never read out of line
+    import moty_amd
+    I, O = 1024, 64
+    say("q8 unaligned weights")
+    q, s = o_quantize_rows(randn(O + I, (O, I), 0.02))
+    buf = torch.zeros(O * I + 1, dtype=torch.int8, device="cuda")
+    qv = buf[1:].view(O, I)
+    qv.copy_(to_dev(q))
+    for S in (1, 8):
+        with pytest.raises(moty_amd.MotyHipError, match="16-byte aligned"):
+            ops.matmul_q_s(to_dev(randn(S + I, (S, I))), qv, to_dev(s))
