@@ -261,7 +261,7 @@ def bench_moe(c, cfg, T, E, K, I, D, norm, order, steps, warmup, bias=None, labe
     active = int((cnt > 0).sum())
     algo = 3 * active * I * D + active * (2 * I + D) * 4 + E * D * 4 + 2 * T * D * 4
     ops_int = 2 * T * K * 3 * I * D
-    t, n = c.time_steps([lambda L=L: L(x, out=out) for L in layers], max(8, steps // 16), max(4, warmup // 16))
+    t, n = c.time_steps([lambda L=L: L(x, out=out) for L in layers], max(16, steps // 16), max(4, warmup // 16))
     gbs = algo / t / 1e9
     return {
         "workload": label, "tokens_per_s": T / t, "ms_per_layer": t * 1e3, "steps": n, "timing": dict(c.last),
@@ -442,7 +442,7 @@ def bench_c3(c, steps, warmup):
             # moty_nn_dense_ffn over WF_I4G Mats: gate + up + SiLU in one
             # pass (a GEMV at M = 1, the f16-MFMA GEMM at M = 256), then down
             return lambda: ops.dense_ffn_i4g(x, w[0][0], w[0][1], w[1][0], w[1][1], w[2][0], w[2][1], out=y)
-        t, n = c.time_steps([step(w) for w in copies], max(8, steps // (8 if M == 1 else 16)), 8)
+        t, n = c.time_steps([step(w) for w in copies], max(32 if M == 1 else 8, steps // (8 if M == 1 else 16)), 8)
         ops_int = 2 * M * 3 * I * D
         algo = wbytes + M * (D + I + I + D) * 4
         tr = pmc_traffic("hbm_traffic_pmc", "c3_M%d_step" % M)
@@ -459,7 +459,7 @@ def bench_c3(c, steps, warmup):
         def step_f32(w):
             return lambda: ops.dense_ffn_i4g(x, w[0][0], w[0][1], w[1][0], w[1][1], w[2][0], w[2][1], idot4=False,
                                              out=y)
-        t, n = c.time_steps([step_f32(w) for w in copies], max(4, steps // (8 if M == 1 else 64)), 4)
+        t, n = c.time_steps([step_f32(w) for w in copies], max(32 if M == 1 else 4, steps // (8 if M == 1 else 64)), 4)
         res["M%d_exact_f32" % M] = {"ms_per_step": t * 1e3, "steps": n, "timing": dict(c.last),
                                     "hbm": roofline("hbm", algo / t / 1e9, HBM_PEAK_GBS, "GB/s",
                                                     pmc_traffic("hbm_traffic_pmc", "c3_M%d_exact_f32_step" % M)),
@@ -524,7 +524,7 @@ def bench_c3_r4(c, steps, warmup):
         res["_cpu"]["x"][M] = x
         y = torch.empty((M, D), device="cuda:0")
         t, n = c.time_steps([lambda w=w: ops.dense_ffn_r4(x, w[0], w[1], w[2], w[3], I, out=y) for w in copies],
-                            max(8, steps // (8 if M == 1 else 16)), 8)
+                            max(32 if M == 1 else 8, steps // (8 if M == 1 else 16)), 8)
         ops_int = 2 * M * 3 * I * D
         algo = wbytes + M * (D + D) * 4
         tr = pmc_traffic("hbm_traffic_pmc", "c3r4_M%d_step" % M)
