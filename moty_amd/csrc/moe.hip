@@ -882,7 +882,7 @@ __global__ __launch_bounds__(D1_NW * MOTY_WAVE) void k_moe_d1_gateup(
   if ((lane & 15) == 0 && i0 + rl < I) h[(int64_t)k * I + i0 + rl] = v;
 }
 
-// The decode down projection, one wave per routed expert: workgroup = KM
+// The decode down projection, one wave per routed expert: workgroup = K <= KM
 // waves over RPW output rows; wave j takes the expert of combine rank j,
 // loads that expert's h row and its RPW down rows, quantizes the h row in
 // registers (a wave max is the row's amax: qrow_i8 with no workgroup
@@ -1185,7 +1185,7 @@ static int launch_moe_d1(const MoeArgs& a, void* scratch, hipStream_t st) {
   const int rpw = kc <= 2 ? 8 : 4;
 #define DE(KC, R)                                                                                             \
   if (kc == KC && rpw == R) {                                                                                 \
-    hipLaunchKernelGGL((k_moe_d1_down_ew<KC, R, 8>), dim3((D + R - 1) / R), dim3(8 * MOTY_WAVE), 0, st, m.idx, m.w, \
+    hipLaunchKernelGGL((k_moe_d1_down_ew<KC, R, 8>), dim3((D + R - 1) / R), dim3(K * MOTY_WAVE), 0, st, m.idx, m.w, \
                        m.h, a.Dn, a.DS, a.out, D, I, K, a.E, a.order, m.counts);                               \
     LAUNCH_TRY("k_moe_d1_down_ew");                                                                            \
   }
