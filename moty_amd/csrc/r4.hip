@@ -142,7 +142,11 @@ __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, con
   int8_t* xq_s = lds;
   float* xs_s = (float*)(lds + S_ * I);
   int* xm_s = (int*)(xs_s + S_ * nb);
-  float2* op_s = (float2*)(xm_s + S_ * nb) + (size_t)bw * (4 * NM * S_ * nb);
+  // operand rows padded to an even length past nb: the four rows of a
+  // block that lanes 4g..4g+3 write land in distinct banks (rows nb apart
+  // shared banks: 8-16 % of LDS cycles in bank conflicts)
+  const int ldo = nb + 2 - (nb & 1);
+  float2* op_s = (float2*)(xm_s + S_ * nb) + (size_t)bw * (4 * NM * S_ * ldo);
   int blk = blockIdx.x * BPW + bw;
   const bool live = blk < O4;
   blk = live ? blk : O4 - 1;
@@ -229,7 +233,7 @@ __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, con
   // priority over the parts that only form group sums
   if (KS > 1 && part == 0) __builtin_amdgcn_s_setprio(3);
   const bool chain = part == 0 && lane < 4 * NM * S_;
-  const float2* opc = op_s + (lane < 4 * NM * S_ ? lane : 0) * nb;  // lane = (m*4 + r)*S_ + t
+  const float2* opc = op_s + (lane < 4 * NM * S_ ? lane : 0) * ldo;  // lane = (m*4 + r)*S_ + t
   const bool even = (nb & 1) == 0;  // 16-byte reads of two groups' operands stay aligned
   float acc = 0.f;
 #pragma unroll
@@ -254,7 +258,7 @@ __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, con
           sacc = dot16(r4_lo(wc[m][k]), *(const int4*)xg, dot16(r4_hi(wc[m][k]), *(const int4*)(xg + 16), 0));
           sacc -= 8 * xm_s[t * nb + gc];
         }
-        if (ok && h == 0) op_s[((m * 4 + r) * S_ + t) * nb + g] = float2{(float)sacc, dd * xs_s[t * nb + gc]};
+        if (ok && h == 0) op_s[((m * 4 + r) * S_ + t) * ldo + g] = float2{(float)sacc, dd * xs_s[t * nb + gc]};
       }
     }
     if (KS > 1 && part != 0) {
@@ -306,7 +310,8 @@ __global__ __launch_bounds__(NT) void k_r4_gemv(const float* __restrict__ x, con
 template <int S_, int NT, bool PAIR, int KS>
 static size_t r4_gemv_lds(int I) {
   const int nb = I / 32;
-  return (size_t)S_ * I + (size_t)S_ * nb * 8 + (size_t)(NT / MOTY_WAVE / KS) * 4 * (PAIR ? 2 : 1) * S_ * nb * 8;
+  const int ldo = nb + 2 - (nb & 1);
+  return (size_t)S_ * I + (size_t)S_ * nb * 8 + (size_t)(NT / MOTY_WAVE / KS) * 4 * (PAIR ? 2 : 1) * S_ * ldo * 8;
 }
 
 template <bool Q8, int S_, int IC, int NT, bool PAIR, int KS>
