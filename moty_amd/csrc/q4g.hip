@@ -136,8 +136,9 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
   constexpr int ldv = 66;  // one chunk's 64 groups, padded (even: float4 reads stay aligned)
   int8_t* xq_s = lds;                                                          // [I]
   int* xg8 = (int*)(lds + I);                                                  // [ng] -8 * group sums
-  float* xf_s = (float*)lds;                                                   // XF: [I] f32
-  float2* dv = (float2*)(lds + (XF ? 4 * I : I + ng * 4)) + (size_t)wv * (NM * RW * ldv);  // [NM*RW][ldv] (scale, dot) of one chunk
+  float* xf_s = (float*)lds;  // XF: [ng][36] f32 -- each group's 32 values, rows padded to 144 B so
+                              // the lanes' 16-byte reads of their groups spread over the banks
+  float2* dv = (float2*)(lds + (XF ? 4 * ng * 36 : I + ng * 4)) + (size_t)wv * (NM * RW * ldv);  // [NM*RW][ldv] (scale, dot) of one chunk
   const int o0 = (blockIdx.x * WAVES + wv) * RW;
 
   // 1. x (one pass, kept in registers), then every nibble load of this wave
@@ -181,7 +182,7 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
 #pragma unroll
     for (int j = 0; j < XV; j++) {
       const int i = (threadIdx.x + j * NT) * 4;
-      if (i < I) *(float4*)(xf_s + i) = xr[j];
+      if (i < I) *(float4*)(xf_s + (i >> 5) * 36 + (i & 31)) = xr[j];
     }
     __syncthreads();
   } else {
@@ -240,7 +241,7 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
       // x[16+j]*w[16+j]), then the 16 -> 8 -> 4 -> 1 reduction tree
       float xv[32];
 #pragma unroll
-      for (int q = 0; q < 8; q++) *(float4*)(xv + 4 * q) = *(const float4*)(xf_s + g * 32 + 4 * q);
+      for (int q = 0; q < 8; q++) *(float4*)(xv + 4 * q) = *(const float4*)(xf_s + g * 36 + 4 * q);
 #pragma unroll
       for (int m = 0; m < NM; m++)
 #pragma unroll
@@ -956,7 +957,7 @@ static int go_gemv1_i4g(const float* x, const uint8_t* q4, const float* scl, con
                         float* y, int I, int O, hipStream_t st) {
   constexpr int NM = PAIR ? 2 : 1;
   const int ng = I / 32;
-  const size_t lds = (XF ? (size_t)I * 4 : (size_t)I + (size_t)ng * 4) + (size_t)(NT / MOTY_WAVE) * NM * RW * 66 * 8;
+  const size_t lds = (XF ? (size_t)ng * 36 * 4 : (size_t)I + (size_t)ng * 4) + (size_t)(NT / MOTY_WAVE) * NM * RW * 66 * 8;
   if (lds > 64 * 1024) return MOTY_EUNSUP;
   const unsigned nb = (unsigned)((O + RW * (NT / MOTY_WAVE) - 1) / (RW * (NT / MOTY_WAVE)));
   hipLaunchKernelGGL((k_gemv1_i4g<RW, NGC, PAIR, NT, PD, XF>), dim3(nb), dim3(NT), lds, st, x, q4, scl, q4b, sclb, y, I, O);
