@@ -259,6 +259,9 @@ int moty_hip_shutdown(void) {
     d.fx_used = d.fx_ev_ok = false;
     d.fx_stream = nullptr;
     d.scr_stream = nullptr;
+    if (d.f1_xh) hipFree(d.f1_xh);  // one block: exchange words, counters, flag
+    d.f1_xh = nullptr;
+    d.f1_epoch = d.f1_err = nullptr;
     d.ready = false;
   }
   t_dev = -1;
