@@ -174,7 +174,21 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_gemm_q8_dma(const int8_
   const int kg = wv / NW, w = wv % NW;
   const int wm = w / WGN, wn = w % WGN;
   const int r32 = lane & 31, h = lane >> 5;
-  const int mb = blockIdx.y * BM, nb = blockIdx.x * BN;
+  int bx = blockIdx.x, by = blockIdx.y;
+  {
+    // workgroups go round-robin over the 8 XCDs by linear id: give XCD x a
+    // (gy/2) x (gx/4) block of tiles, so its L2 pulls in half the
+    // activation rows and a quarter of the weight rows (row-major order
+    // gave each XCD every activation row and an eighth of the weights)
+    const int gx = gridDim.x, gy = gridDim.y;
+    if (gx % 4 == 0 && gy % 2 == 0) {
+      const int lin = by * gx + bx, x = lin & 7, j = lin >> 3;
+      const int bw = gx / 4;
+      bx = (x & 3) * bw + j % bw;
+      by = (x >> 2) * (gy / 2) + j / bw;
+    }
+  }
+  const int mb = by * BM, nb = bx * BN;
   const int8_t* src[NI];
 #pragma unroll
   for (int i = 0; i < NI; i++) {
