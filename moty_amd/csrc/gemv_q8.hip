@@ -370,7 +370,10 @@ static int launch_1(const float* x, const int8_t* W, const float* scale, const i
   int rpw = 4;
   while (rpw > 1 && (O + rpw - 1) / rpw < 256) rpw >>= 1;
   const int waves = (O + rpw - 1) / rpw;
-  const int nw = waves > 768 ? 4 : (waves + 255) / 256;  // one workgroup per CU, up to 4 waves each
+  // up to one workgroup per CU, of up to 4 waves; from 768 waves on, 4
+  // (C1's gate/up, 768 waves: FFN step 5.85 us against 5.90 with 3-wave
+  // workgroups on every CU, 5.96 with 2, 5.90 with 1)
+  const int nw = waves >= 768 ? 4 : (waves + 255) / 256;
   const unsigned nb = (unsigned)((waves + nw - 1) / nw);
   // a long weight stream: the shared-activation kernel (activation row
   // first, quantized once per workgroup, fewer registers per wave) in
