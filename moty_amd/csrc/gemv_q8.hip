@@ -376,20 +376,25 @@ static int launch_1(const float* x, const int8_t* W, const float* scale, const i
   const int nw = waves >= 768 ? 4 : (waves + 255) / 256;
   const unsigned nb = (unsigned)((waves + nw - 1) / nw);
   // a long weight stream: the shared-activation kernel (activation row
-  // first, quantized once per workgroup, fewer registers per wave) in
-  // 8-wave workgroups, one row per wave (two past 8192 rows: plain matrices
-  // only) -- the best of a rows/wave x waves/workgroup sweep on MI355X over
-  // 4096x4096, 12288x4096 and the fused 2 x 12288x4096; a short one: the
-  // per-wave kernel, whose activation and weight latencies overlap
+  // quantized once per workgroup into LDS, fewer registers per wave), the
+  // weight loads issued before the activation row lands: two rows per wave
+  // for plain matrices, one for the fused gate/up pair; 8-wave workgroups
+  // from 4096 waves on, else 4.  From a sweep of rows/wave x waves/workgroup
+  // x issue order on MI355X (graph replays over rotating weights): 4096 x
+  // 4096 4.26 us against 4.64 for 8 waves of one row with the row awaited
+  // first, 12288 x 4096 9.65 against 10.06 (2 rows, 8 waves, awaited), the
+  // fused 2 x 12288 x 4096 17.2 against 17.7
   if ((int64_t)O * I * (PAIR ? 2 : 1) >= ((int64_t)16 << 20)) {
     constexpr int NWL = (4 * NC) % 8 == 0 ? 8 : 4;  // whole float4 of the row per thread
-    const int r = (!PAIR && O > 8192) ? 2 : 1;
-    const unsigned nbl = (unsigned)(((O + r - 1) / r + NWL - 1) / NWL);
-    if (r == 2)
-      hipLaunchKernelGGL((k_gemv1_q8_lds<NC, 2, PAIR, NWL>), dim3(nbl), dim3(NWL * MOTY_WAVE), 0, st, x, W, scale,
-                         W2, scale2, y, I, O);
+    const int lwaves = PAIR ? O : (O + 1) / 2;
+    const bool wide = lwaves >= 4096;
+    const unsigned nbl = (unsigned)((lwaves + (wide ? NWL : 4) - 1) / (wide ? NWL : 4));
+    constexpr int R = PAIR ? 1 : 2;
+    if (wide)
+      hipLaunchKernelGGL((k_gemv1_q8_lds<NC, R, PAIR, NWL, true>), dim3(nbl), dim3(NWL * MOTY_WAVE), 0, st, x, W,
+                         scale, W2, scale2, y, I, O);
     else
-      hipLaunchKernelGGL((k_gemv1_q8_lds<NC, 1, PAIR, NWL>), dim3(nbl), dim3(NWL * MOTY_WAVE), 0, st, x, W, scale,
+      hipLaunchKernelGGL((k_gemv1_q8_lds<NC, R, PAIR, 4, true>), dim3(nbl), dim3(4 * MOTY_WAVE), 0, st, x, W, scale,
                          W2, scale2, y, I, O);
     LAUNCH_TRY("k_gemv1_q8_lds");
     return MOTY_OK;

@@ -126,7 +126,9 @@ Q8_CASES = [(1, 1024, 3072), (1, 3072, 1024), (1, 3072, 2000), (1, 4096, 1500), 
             # few tiles: K split over four wave groups (K blocks 4, 5, 16)
             (17, 512, 50), (40, 640, 96), (130, 2048, 200),
             # S = 1 past 16 MiB of weights: the shared-activation GEMV, full and ragged
-            (1, 4096, 4096), (1, 3088, 5500), (1, 1040, 16200)]
+            (1, 4096, 4096), (1, 3088, 5500), (1, 1040, 16200),
+            # ... with 4096 or more waves of two rows: 8-wave workgroups
+            (1, 4096, 8200)]
 
 
 @pytest.mark.parametrize("S,I,O", Q8_CASES)

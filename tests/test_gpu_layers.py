@@ -24,7 +24,7 @@ def q8(seed, shape):
 
 @pytest.mark.parametrize("S,D,I", [(1, 1024, 3072), (4, 1024, 3072), (9, 256, 512), (1, 64, 32), (1, 2048, 6144),
                                    (1, 4096, 2048), (1, 3088, 2800),
-                                   (1, 4096, 1024), (1, 1040, 2000)])
+                                   (1, 4096, 1024), (1, 1040, 2000), (1, 4096, 4096)])
 def test_dense_ffn_q8(ops, S, D, I):
     say("dense_ffn", S, D, I)
     G, GS = q8(1, (I, D))
