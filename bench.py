@@ -214,7 +214,7 @@ def bench_c1(c, steps, warmup):
         "workload": "C1 Qwen3-0.6B FFN decode, Q8_0 (fused gate/up GEMV + SiLU, down GEMV), S=1, D=1024, I=3072",
         "gbs": algo / t / 1e9, "ms_per_step": t * 1e3, "steps": n, "algo_bytes": algo,
         "weight_copies": ncopy, "x": x, "w0": copies[0], "timing": rep,
-        "kernel": {"name": "k_gemv1_q8<1,4,PAIR,3> gate+up+SiLU", "us": tg * 1e6, "algo_bytes": gu_algo,
+        "kernel": {"name": "k_gemv1_q8<1,4,PAIR,4> gate+up+SiLU", "us": tg * 1e6, "algo_bytes": gu_algo,
                    "gbs": gu_algo / tg / 1e9},
         "one_launch_us": round(t1 * 1e6, 3),
     }
