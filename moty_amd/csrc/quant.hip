@@ -153,6 +153,95 @@ __global__ __launch_bounds__(NT) void k_quantize_rows(const float* __restrict__ 
   }
 }
 
+// The same for rows of I % 4 == 0, I <= 4 * NT * NV (16-byte aligned rows):
+// the row is read once, by 16-byte loads kept in registers, and written as
+// 4-byte words -- one pass over HBM where the kernel above reads every
+// element twice with 4-byte loads and writes single bytes.
+template <int NT, int NV>
+__global__ __launch_bounds__(NT) void k_quantize_rows_v(const float* __restrict__ w, int8_t* __restrict__ q,
+                                                        float* __restrict__ scale, int I, int bits) {
+  __shared__ float red[NT / MOTY_WAVE];
+  const int64_t row = blockIdx.x;
+  const float* wr = w + row * (int64_t)I;
+  int8_t* qr = q + row * (int64_t)I;
+  const int qmax = (1 << (bits - 1)) - 1;
+  float4 v[NV];
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const int i = (threadIdx.x + j * NT) * 4;
+    v[j] = i < I ? *(const float4*)(wr + i) : float4{0.f, 0.f, 0.f, 0.f};
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+  }
+  amax = block_max<NT>(amax, red);
+  float s = amax / (float)qmax;
+  if (s < 1e-8f) s = 1e-8f;
+  if (threadIdx.x == 0) scale[row] = s;
+  auto q1 = [&](float x) {
+    int c = rne_int(x / s);
+    c = c > qmax ? qmax : c;
+    c = c < -qmax - 1 ? -qmax - 1 : c;
+    return (uint32_t)c & 0xffu;
+  };
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const int i = (threadIdx.x + j * NT) * 4;
+    if (i < I) *(uint32_t*)(qr + i) = q1(v[j].x) | (q1(v[j].y) << 8) | (q1(v[j].z) << 16) | (q1(v[j].w) << 24);
+  }
+}
+
+// Group-32 packing for I % 32 == 0 (16-byte aligned w, q4): a workgroup of
+// NT threads takes NT consecutive groups -- a contiguous NT * 128 bytes of w
+// -- into LDS by 16-byte loads, each thread then packs its own group as
+// k_pack_i4g does and writes its 16 code bytes and its scale.  Group g
+// sits at word 33 * g in LDS, so the lanes reading element j of their
+// groups hit different banks.
+template <int NT>
+__global__ __launch_bounds__(NT) void k_pack_i4g32(const float* __restrict__ w, uint8_t* __restrict__ q4,
+                                                   float* __restrict__ scale, int64_t ngt) {
+  __shared__ float ws[NT * 33];
+  const int64_t g0 = (int64_t)blockIdx.x * NT;
+  const int ng = ngt - g0 < NT ? (int)(ngt - g0) : NT;
+  const float* src = w + g0 * 32;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const int u = threadIdx.x + j * NT;  // float4 unit of the block
+    if (u < ng * 8) {
+      const float4 t = *(const float4*)(src + 4 * u);
+      float* d = ws + (u >> 3) * 33 + (u & 7) * 4;
+      d[0] = t.x;
+      d[1] = t.y;
+      d[2] = t.z;
+      d[3] = t.w;
+    }
+  }
+  __syncthreads();
+  if ((int)threadIdx.x >= ng) return;
+  const float* gw = ws + threadIdx.x * 33;
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(gw[i]));
+  float s = amax / 7.f;
+  if (s < 1e-8f) s = 1e-8f;
+  const int64_t g = g0 + threadIdx.x;
+  scale[g] = s;
+  uint32_t out[4];
+#pragma unroll
+  for (int b = 0; b < 4; b++) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      int v0 = rne_int(gw[8 * b + 2 * k] / s);
+      v0 = v0 > 7 ? 7 : (v0 < -8 ? -8 : v0);
+      int v1 = rne_int(gw[8 * b + 2 * k + 1] / s);
+      v1 = v1 > 7 ? 7 : (v1 < -8 ? -8 : v1);
+      word |= (uint32_t)((v0 + 8) | ((v1 + 8) << 4)) << (8 * k);
+    }
+    out[b] = word;
+  }
+  *(uint4*)(q4 + g * 16) = uint4{out[0], out[1], out[2], out[3]};
+}
+
 // One thread per (row, group).  Odd trailing elements pair with a zero code.
 __global__ void k_pack_i4g(const float* __restrict__ w, uint8_t* __restrict__ q4, float* __restrict__ scale,
                            int O, int I, int gs) {
@@ -452,6 +541,18 @@ int launch_i4row_idot(const int8_t* xq, const float* sx, const uint8_t* q4, cons
 
 int launch_quantize_rows(const float* w, int8_t* q, float* scale, int O, int I, int bits, hipStream_t st) {
   if (O <= 0) return MOTY_OK;
+  if ((I % 4) == 0 && I <= 16384 && !(((uintptr_t)w) & 15) && !(((uintptr_t)q) & 3)) {
+    // one pass in registers: float4 units per thread as the row needs
+    const int nv = (I / 4 + 255) / 256;
+#define QV(NV)                                                                                             \
+  if (nv <= NV) {                                                                                           \
+    hipLaunchKernelGGL((k_quantize_rows_v<256, NV>), dim3(O), dim3(256), 0, st, w, q, scale, I, bits);       \
+    LAUNCH_TRY("k_quantize_rows_v");                                                                        \
+    return MOTY_OK;                                                                                         \
+  }
+    QV(1) QV(2) QV(4) QV(8) QV(16)
+#undef QV
+  }
   hipLaunchKernelGGL(k_quantize_rows<256>, dim3(O), dim3(256), 0, st, w, q, scale, I, bits);
   LAUNCH_TRY("k_quantize_rows");
   return MOTY_OK;
@@ -461,6 +562,12 @@ int launch_pack_i4g(const float* w, uint8_t* q4, float* scale, int O, int I, int
   const int ng = (I + gs - 1) / gs;
   const int64_t n = (int64_t)O * ng;
   if (n <= 0) return MOTY_OK;
+  if (gs == 32 && (I % 32) == 0 && !(((uintptr_t)w) & 15) && !(((uintptr_t)q4) & 15)) {
+    // rows are whole groups: the groups of the matrix are consecutive 128-byte runs of w
+    hipLaunchKernelGGL(k_pack_i4g32<256>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, w, q4, scale, n);
+    LAUNCH_TRY("k_pack_i4g32");
+    return MOTY_OK;
+  }
   hipLaunchKernelGGL(k_pack_i4g, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, w, q4, scale, O, I, gs);
   LAUNCH_TRY("k_pack_i4g");
   return MOTY_OK;

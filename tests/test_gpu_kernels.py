@@ -100,19 +100,30 @@ def test_qrow_zero_row(ops):
     assert (to_np(sx) == np.float32(1e-12)).all() and not to_np(q).any()
 
 
-@pytest.mark.parametrize("O,I", [(64, 1024), (7, 33), (3, 3072)])
-def test_quantize_rows(ops, O, I):
-    say("quantize_rows", O, I)
+# I % 4 == 0 and I <= 16384: one pass in registers (1, 2, 4, 8 or 16 float4
+# per thread); other rows: the two-pass kernel.  A zero row takes s = 1e-8.
+@pytest.mark.parametrize("O,I", [(64, 1024), (7, 33), (3, 3072), (5, 16384), (2, 20000), (9, 4100), (4, 12),
+                                 (3, 8190)])
+@pytest.mark.parametrize("bits", [8, 4])
+def test_quantize_rows(ops, O, I, bits):
+    say("quantize_rows", O, I, bits)
     w = randn(O + I, (O, I), 0.02)
-    q, s = ops.quantize_rows(to_dev(w))
-    q2, s2 = o_quantize_rows(w)
+    w[0, :5] = [0.0, 1e-30, -0.07, 0.07, 0.035]
+    if O > 2:
+        w[1] = 0.0
+    q, s = ops.quantize_rows(to_dev(w), bits)
+    q2, s2 = o_quantize_rows(w, bits)
     assert same_bits(to_np(q), q2) and same_bits(to_np(s), s2)
 
 
-@pytest.mark.parametrize("O,I,gs", [(64, 4096, 32), (5, 31, 16), (8, 100, 32)])
+# gs = 32 with I % 32 == 0: one workgroup per 256 consecutive groups staged
+# through LDS (full and ragged last workgroup); other shapes: one thread per group
+@pytest.mark.parametrize("O,I,gs", [(64, 4096, 32), (5, 31, 16), (8, 100, 32), (300, 1024, 32), (3, 96, 32),
+                                    (1, 32, 32), (7, 12288, 32), (4, 64, 16)])
 def test_pack_int4_grouped(ops, O, I, gs):
     say("pack_i4g", O, I, gs)
     w = randn(O * 7 + I, (O, I), 0.02)
+    w[0, :gs] = 0.0  # an all-zero group: s = 1e-8
     q4, s = ops.pack_int4_grouped(to_dev(w), gs)
     q42, s2 = o_pack_int4_grouped(w, gs)
     assert same_bits(to_np(q4), q42) and same_bits(to_np(s), s2)
