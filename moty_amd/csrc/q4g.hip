@@ -107,6 +107,22 @@ __global__ __launch_bounds__(Q4V_NT) void k_gemv_i4g(const float* __restrict__ x
   }
 }
 
+// v_cvt_off_f32_i4 of byte K of w: the signed nibble in bits [8K, 8K+4)
+// divided by 16 (exact), one SDWA-selected conversion
+template <int K>
+__device__ __forceinline__ float cvt_off_b(uint32_t w) {
+  float r;
+  if (K == 0)
+    asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(w));
+  else if (K == 1)
+    asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(r) : "v"(w));
+  else if (K == 2)
+    asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(w));
+  else
+    asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(r) : "v"(w));
+  return r;
+}
+
 // ---------------------------------------------------------------------------
 // IDOT4 GEMV for decode (S = 1), optionally PAIR (gate + up + SiLU).
 // Workgroup = 4 waves; a wave owns RW consecutive output rows (of W, and of
@@ -177,12 +193,22 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int j = 0; j < XV; j++) xr[j] = sel4((threadIdx.x + j * NT) * 4 < I, xr[j]);
+  // XF: x into LDS as 16 x (exact) when every |x| < 2^123 -- then the
+  // nibbles convert as (n - 8) / 16 and each product, hence each rounding,
+  // is the reference's -- else as it is, for the full-width conversion
+  bool x16 = false;
   if (XF) {
-    // exact f32 activations: x into LDS as it is
+    bool big = false;
+#pragma unroll
+    for (int j = 0; j < XV; j++)
+      big |= fmaxf(fmaxf(fabsf(xr[j].x), fabsf(xr[j].y)), fmaxf(fabsf(xr[j].z), fabsf(xr[j].w))) >= 0x1p123f;
+    x16 = !__syncthreads_or(big);
 #pragma unroll
     for (int j = 0; j < XV; j++) {
       const int i = (threadIdx.x + j * NT) * 4;
-      if (i < I) *(float4*)(xf_s + (i >> 5) * 36 + (i & 31)) = xr[j];
+      float4 v = xr[j];
+      if (x16) v = float4{16.f * v.x, 16.f * v.y, 16.f * v.z, 16.f * v.w};
+      if (i < I) *(float4*)(xf_s + (i >> 5) * 36 + (i & 31)) = v;
     }
     __syncthreads();
   } else {
@@ -249,16 +275,34 @@ __global__ __launch_bounds__(NT) void k_gemv1_i4g(const float* __restrict__ x, c
           const int4 w = wb[m][r][c];
           const uint32_t wd[4] = {(uint32_t)w.x, (uint32_t)w.y, (uint32_t)w.z, (uint32_t)w.w};
           float wf[32];  // element e = byte e/2, low nibble when e is even, minus 8 (exact)
+          if (x16) {
+            // (n - 8) / 16: n ^ 8 is n - 8 as a signed nibble, and
+            // v_cvt_off_f32_i4 gives a signed nibble / 16 from the low
+            // 4 bits of its byte-selected operand
 #pragma unroll
-          for (int q = 0; q < 4; q++) {
-            // n - 8 as signed bytes ((n + 0x78) ^ 0x80, carry-free), each
-            // then converted from its byte position
-            const uint32_t lo = ((wd[q] & 0x0f0f0f0fu) + 0x78787878u) ^ 0x80808080u;
-            const uint32_t hi = (((wd[q] >> 4) & 0x0f0f0f0fu) + 0x78787878u) ^ 0x80808080u;
+            for (int q = 0; q < 4; q++) {
+              const uint32_t a = wd[q] ^ 0x88888888u, b = a >> 4;
+              wf[8 * q + 0] = cvt_off_b<0>(a);
+              wf[8 * q + 1] = cvt_off_b<0>(b);
+              wf[8 * q + 2] = cvt_off_b<1>(a);
+              wf[8 * q + 3] = cvt_off_b<1>(b);
+              wf[8 * q + 4] = cvt_off_b<2>(a);
+              wf[8 * q + 5] = cvt_off_b<2>(b);
+              wf[8 * q + 6] = cvt_off_b<3>(a);
+              wf[8 * q + 7] = cvt_off_b<3>(b);
+            }
+          } else {
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-              wf[8 * q + 2 * k] = (float)(int8_t)(lo >> (8 * k));
-              wf[8 * q + 2 * k + 1] = (float)(int8_t)(hi >> (8 * k));
+            for (int q = 0; q < 4; q++) {
+              // n - 8 as signed bytes ((n + 0x78) ^ 0x80, carry-free),
+              // each then converted from its byte position
+              const uint32_t lo = ((wd[q] & 0x0f0f0f0fu) + 0x78787878u) ^ 0x80808080u;
+              const uint32_t hi = (((wd[q] >> 4) & 0x0f0f0f0fu) + 0x78787878u) ^ 0x80808080u;
+#pragma unroll
+              for (int k = 0; k < 4; k++) {
+                wf[8 * q + 2 * k] = (float)(int8_t)(lo >> (8 * k));
+                wf[8 * q + 2 * k + 1] = (float)(int8_t)(hi >> (8 * k));
+              }
             }
           }
           float t[16];

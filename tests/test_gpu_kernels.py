@@ -312,6 +312,35 @@ def test_matmul_i4_s_misaligned(ops, idot4):
         ops.matmul_i4_s(to_dev(randn(S + I, (S, I))), qv, to_dev(s), idot4)
 
 
+@pytest.mark.parametrize("case", ["denormal", "large", "huge", "inf"])
+@pytest.mark.parametrize("S", [1, 3])
+def test_i4g_f32_activation_extremes(ops, S, case):
+    # the one-token GEMV holds x as 16 x (nibbles as (n - 8) / 16) while
+    # every |x| < 2^123, else x as it is: both must give the reference's bits,
+    # with denormal, large (2^122), huge (2^126: the fallback) and infinite
+    # activations
+    I, O = 2048, 96
+    say("i4g f32 extremes", S, case)
+    q4, s = o_pack_int4_grouped(randn(O + I, (O, I), 0.02))
+    x = randn(S + 11 * I, (S, I))
+    if case == "denormal":
+        x[:, ::3] *= np.float32(1e-40)
+    elif case == "large":
+        x[:, 5] = np.float32(2.0 ** 122)
+    elif case == "huge":
+        x[:, 7] = np.float32(2.0 ** 126)
+        x[:, 9] = np.float32(-3e38)
+    else:
+        x[:, 3] = np.float32(np.inf)
+    y = to_np(ops.matmul_i4_grouped_s(to_dev(x), to_dev(q4), to_dev(s), 32, False))
+    y2 = o_matmul_i4g(x, q4, s, False)
+    # NaNs (inf * 0 and inf - inf) compare as NaNs: the host and the GPU
+    # make default NaNs with different sign bits
+    nan = np.isnan(y2)
+    assert (np.isnan(y) == nan).all()
+    assert same_bits(np.where(nan, 0, y).astype(np.float32), np.where(nan, 0, y2).astype(np.float32)), mismatch(y, y2)
+
+
 @pytest.mark.parametrize("S", [1, 9])
 def test_i4g_f32_unaligned_activations(ops, S):
     # the exact-f32 GEMV / tiled GEMM read x in 16-byte units: an activation
