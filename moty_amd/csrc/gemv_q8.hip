@@ -247,21 +247,21 @@ __global__ __launch_bounds__(NW * MOTY_WAVE) void k_gemv1_q8(const float* __rest
   if ((lane & (MOTY_WAVE / RPW - 1)) == 0 && o < O) y[o] = v;
 }
 
-// S = 1, I <= 4096, large matrices (the weight stream is long enough for
-// its queueing to matter).  The workgroup loads the activation row once
-// (thread t takes float4 units t, t + NT, ...) and waits for it before any weight
-// load is issued: queued behind the weight stream, in the CU's load path
-// and in L2, it would arrive with the weights.  Then it streams its
-// weights: wave w owns
-// RPW rows, lane l reads bytes [c*1024 + 16l, +16) of each 1 KiB chunk c,
-// with non-temporal loads (read once, kept out of the caches' way).  While
-// they fly the row is quantized (qrow_i8 bit for bit: the row's amax from a
-// wave max and an LDS exchange across the waves) into LDS, from where each
-// lane takes exactly the 16 codes per chunk its dot needs.
-// XF: the weight loads are issued right after the activation loads, without
-// waiting for them -- for short weight streams, where the activation row is
-// as large as a wave's weights (C1's down: 12 KiB of h against 3 KiB per
-// row) and is better loaded once per workgroup than once per wave.
+// S = 1, I <= 4096: large matrices, and plain rows of 3-4 KiB whose
+// activation row is as large as a wave's weights (C1's down: 12 KiB of h
+// against 3 KiB per row), so better loaded once per workgroup than once per
+// wave.  The workgroup loads the activation row once (thread t takes float4
+// units t, t + NT, ...); wave w owns RPW rows, lane l reads bytes
+// [c*1024 + 16l, +16) of each 1 KiB chunk c, with non-temporal loads (read
+// once, kept out of the caches' way).  While they fly the row is quantized
+// (qrow_i8 bit for bit: the row's amax from a wave max and an LDS exchange
+// across the waves) into LDS, from where each lane takes exactly the 16
+// codes per chunk its dot needs.
+// XF (every launch below): the weight loads are issued right behind the
+// activation loads.  Without it the workgroup waits for the row first,
+// which an earlier one-row-per-wave form needed (its row, queued behind the
+// weight stream, arrived 3.5 us into a 10 us kernel) and which measured
+// slower for every launch shape used now.
 template <int NC, int RPW, bool PAIR, int NW, bool XF = false>
 __global__ __launch_bounds__(NW * MOTY_WAVE) void k_gemv1_q8_lds(const float* __restrict__ x, const int8_t* __restrict__ W,
                                                       const float* __restrict__ scale,
