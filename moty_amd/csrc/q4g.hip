@@ -1025,7 +1025,8 @@ int launch_gemv_i4g_xf(const float* x, const uint8_t* q4, const float* scl, cons
   }
   if (ngc <= 2) return go_gemv1_i4g<8, 2, false, 256, 1, true>(x, q4, scl, nullptr, nullptr, y, I, O, st);
   if (ngc <= 4) return go_gemv1_i4g<4, 4, false, 256, 1, true>(x, q4, scl, nullptr, nullptr, y, I, O, st);
-  return go_gemv1_i4g<4, 6, false, 256, 1, true>(x, q4, scl, nullptr, nullptr, y, I, O, st);
+  // 2 rows per wave (4096 x 12288: 10.6 -> 10.2 us against 4)
+  return go_gemv1_i4g<2, 6, false, 256, 1, true>(x, q4, scl, nullptr, nullptr, y, I, O, st);
 }
 
 int launch_gemv_i4g(const float* x, const uint8_t* q4, const float* scl, const uint8_t* q4b, const float* sclb,
