@@ -631,7 +631,7 @@ int moty_hip_dense_ffn_i4g_dev(float* out, const float* x, int S, const uint8_t*
     if ((rc = launch_gemv_i4g(x, gate, gs, up, us, h, 1, D, I, st))) return rc;
     return launch_gemv_i4g(h, down, ds, nullptr, nullptr, out, 1, I, D, st);
   }
-  if (!idot4 && S == 1 && D <= 12288 && I <= 12288 &&
+  if (!idot4 && S == 1 && D <= 16384 && I <= 16384 &&
       !(((uintptr_t)x | (uintptr_t)gate | (uintptr_t)up | (uintptr_t)down | (uintptr_t)h) & 15)) {
     // exact f32: gate + up + SiLU in one pass, then down
     if ((rc = launch_gemv_i4g_xf(x, gate, gs, up, us, h, D, I, st))) return rc;
@@ -646,6 +646,14 @@ int moty_hip_dense_ffn_i4g_dev(float* out, const float* x, int S, const uint8_t*
       return r ? r : launch_gemm_i4g((const int8_t*)xq, sx, w, ws, o, S, K, N, st);
     }
     if (S > 4 && launch_gemm_i4g_xf(a, w, ws, nullptr, nullptr, o, S, K, N, st) == MOTY_OK) return MOTY_OK;
+    if (S <= 4) {
+      // exact f32, a few tokens: the one-token GEMV per token (it refuses
+      // what it cannot take before launching anything)
+      int r = MOTY_OK;
+      for (int s = 0; s < S && r == MOTY_OK; s++)
+        r = launch_gemv_i4g_xf(a + (int64_t)s * K, w, ws, nullptr, nullptr, o + (int64_t)s * N, K, N, st);
+      if (r != MOTY_EUNSUP) return r;
+    }
     return launch_i4g_f32(a, w, ws, o, S, K, N, st);
   };
   if (!idot4 && S > 4 && (D % 64) == 0 && !(((uintptr_t)x) & 15) && !(((uintptr_t)gate | (uintptr_t)up) & 7)) {

@@ -1001,7 +1001,20 @@ static int go_gemv1_i4g(const float* x, const uint8_t* q4, const float* scl, con
   constexpr int NM = PAIR ? 2 : 1;
   const int ng = I / 32;
   const size_t lds = (XF ? (size_t)ng * 36 * 4 : (size_t)I + (size_t)ng * 4) + (size_t)(NT / MOTY_WAVE) * NM * RW * 66 * 8;
-  if (lds > 64 * 1024) return MOTY_EUNSUP;
+  if (lds > 150 * 1024) return MOTY_EUNSUP;  // within the CU's 160 KiB, static arrays included
+  if (lds > 64 * 1024) {
+    // past 64 KiB of dynamic LDS: raise the instance's allowance to what
+    // this launch needs (kept when larger)
+    static size_t allowed = 0;
+    if (lds > allowed) {
+      if (hipFuncSetAttribute((const void*)&k_gemv1_i4g<RW, NGC, PAIR, NT, PD, XF>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+        (void)hipGetLastError();  // leave no error for a later call to find
+        return MOTY_EUNSUP;
+      }
+      allowed = lds;
+    }
+  }
   const unsigned nb = (unsigned)((O + RW * (NT / MOTY_WAVE) - 1) / (RW * (NT / MOTY_WAVE)));
   hipLaunchKernelGGL((k_gemv1_i4g<RW, NGC, PAIR, NT, PD, XF>), dim3(nb), dim3(NT), lds, st, x, q4, scl, q4b, sclb, y, I, O);
   LAUNCH_TRY("k_gemv1_i4g");
@@ -1010,23 +1023,26 @@ static int go_gemv1_i4g(const float* x, const uint8_t* q4, const float* scl, con
 
 // The exact-f32 path (IDOT4 unset) for one token: the same workgroup
 // structure with x kept as f32 in LDS and each lane's group sum formed in
-// the reference's float order.  I % 32 == 0, I <= 12288 (x in LDS), 16-byte
-// aligned x and nibbles.  PAIR (q4b): gate + up + SiLU.
+// the reference's float order.  I % 32 == 0, I <= 16384 (x in LDS: past
+// 12288 more than 64 KiB of it), 16-byte aligned x and nibbles.  PAIR (q4b):
+// gate + up + SiLU.
 int launch_gemv_i4g_xf(const float* x, const uint8_t* q4, const float* scl, const uint8_t* q4b, const float* sclb,
                        float* y, int I, int O, hipStream_t st) {
-  if ((I % 32) || I > 12288 || ((((uintptr_t)x) | ((uintptr_t)q4) | ((uintptr_t)q4b)) & 15)) return MOTY_EUNSUP;
+  if ((I % 32) || I > 16384 || ((((uintptr_t)x) | ((uintptr_t)q4) | ((uintptr_t)q4b)) & 15)) return MOTY_EUNSUP;
   if (O <= 0) return MOTY_OK;
   const int ngc = (I / 32 + 63) / 64;
   if (q4b) {
     // 2 gate + 2 up rows per wave (C3 M = 1 exact-f32 FFN 25.7 -> 25.2 us against 4 + 4)
     if (ngc <= 2) return go_gemv1_i4g<2, 2, true, 256, 1, true>(x, q4, scl, q4b, sclb, y, I, O, st);
     if (ngc <= 4) return go_gemv1_i4g<2, 4, true, 256, 1, true>(x, q4, scl, q4b, sclb, y, I, O, st);
-    return go_gemv1_i4g<2, 6, true, 256, 1, true>(x, q4, scl, q4b, sclb, y, I, O, st);
+    if (ngc <= 6) return go_gemv1_i4g<2, 6, true, 256, 1, true>(x, q4, scl, q4b, sclb, y, I, O, st);
+    return go_gemv1_i4g<2, 8, true, 256, 1, true>(x, q4, scl, q4b, sclb, y, I, O, st);
   }
   if (ngc <= 2) return go_gemv1_i4g<8, 2, false, 256, 1, true>(x, q4, scl, nullptr, nullptr, y, I, O, st);
   if (ngc <= 4) return go_gemv1_i4g<4, 4, false, 256, 1, true>(x, q4, scl, nullptr, nullptr, y, I, O, st);
   // 2 rows per wave (4096 x 12288: 10.6 -> 10.2 us against 4)
-  return go_gemv1_i4g<2, 6, false, 256, 1, true>(x, q4, scl, nullptr, nullptr, y, I, O, st);
+  if (ngc <= 6) return go_gemv1_i4g<2, 6, false, 256, 1, true>(x, q4, scl, nullptr, nullptr, y, I, O, st);
+  return go_gemv1_i4g<2, 8, false, 256, 1, true>(x, q4, scl, nullptr, nullptr, y, I, O, st);
 }
 
 int launch_gemv_i4g(const float* x, const uint8_t* q4, const float* scl, const uint8_t* q4b, const float* sclb,

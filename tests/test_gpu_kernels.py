@@ -195,9 +195,11 @@ def test_gate_up_silu_i4g(ops, D, I):
 
 
 @pytest.mark.parametrize("S,I,O", [(1, 4096, 256), (3, 96, 40), (16, 1024, 64),
-                                   # one token: the GEMV form (1..6 chunks of 64 groups, partial
-                                   # chunks, ragged rows), and past its 12288 bound the fallback
+                                   # one token: the GEMV form (1..8 chunks of 64 groups, partial
+                                   # chunks, ragged rows; past 12288 more than 64 KiB of LDS), and
+                                   # past its 16384 bound the fallback
                                    (1, 12288, 100), (1, 8192, 77), (1, 96, 40), (1, 2080, 300), (1, 16384, 20),
+                                   (1, 14336, 300), (2, 16384, 64), (1, 16416, 10),
                                    (1, 64, 1000),
                                    # 2..4 tokens: the GEMV per token; more: the tiled GEMM (64 x 64
                                    # tiles, ragged in tokens and rows; I % 64 != 0 falls back)
@@ -247,7 +249,10 @@ def test_silu_and_softmax(ops):
                                    # 64 x 192 gate/up tiles, ragged in tokens and rows
                                    (130, 256, 12416),
                                    # one token through the exact-f32 fused gate/up GEMV
-                                   (1, 4096, 1056), (1, 96, 8192), (1, 12288, 2080)])
+                                   (1, 4096, 1056), (1, 96, 8192), (1, 12288, 2080),
+                                   # rows past 12288 (more than 64 KiB of x in LDS), and 2-4
+                                   # tokens through the per-token GEMV
+                                   (1, 1024, 14336), (1, 16384, 96), (3, 1024, 2048), (4, 14336, 64)])
 def test_dense_ffn_i4g(ops, idot4, S, D, I):
     # nn/ffn.c:26-55 over grouped-int4 Mats: the fused gate/up f16 pass
     # (S > 4, D and I multiples of 128), the int8 GEMM fallback (other
