@@ -1003,16 +1003,21 @@ static int go_gemv1_i4g(const float* x, const uint8_t* q4, const float* scl, con
   const size_t lds = (XF ? (size_t)ng * 36 * 4 : (size_t)I + (size_t)ng * 4) + (size_t)(NT / MOTY_WAVE) * NM * RW * 66 * 8;
   if (lds > 150 * 1024) return MOTY_EUNSUP;  // within the CU's 160 KiB, static arrays included
   if (lds > 64 * 1024) {
-    // past 64 KiB of dynamic LDS: raise the instance's allowance to what
-    // this launch needs (kept when larger)
-    static size_t allowed = 0;
-    if (lds > allowed) {
+    // past 64 KiB of dynamic LDS: raise the instance's allowance on this
+    // device to what this launch needs (kept when larger)
+    static size_t allowed[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+      (void)hipGetLastError();
+      return MOTY_EUNSUP;
+    }
+    if (lds > allowed[dev]) {
       if (hipFuncSetAttribute((const void*)&k_gemv1_i4g<RW, NGC, PAIR, NT, PD, XF>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
         (void)hipGetLastError();  // leave no error for a later call to find
         return MOTY_EUNSUP;
       }
-      allowed = lds;
+      allowed[dev] = lds;
     }
   }
   const unsigned nb = (unsigned)((O + RW * (NT / MOTY_WAVE) - 1) / (RW * (NT / MOTY_WAVE)));
