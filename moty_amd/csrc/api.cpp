@@ -408,14 +408,14 @@ int moty_hip_matmul_i4_grouped_s_dev(float* y, const float* x, const uint8_t* q4
     if (rc) return rc;
     return launch_gemm_i4g(xq, sx, q4, scale, y, S, I, O, st);
   }
-  if (gs == 32 && S <= 4) {
+  if (gs == 32 && S <= XF_GEMV_MAX_S) {
     // a few tokens: the one-token GEMV per token
     int rc = MOTY_OK;
     for (int s = 0; s < S && rc == MOTY_OK; s++)
       rc = launch_gemv_i4g_xf(x + (int64_t)s * I, q4, scale, nullptr, nullptr, y + (int64_t)s * O, I, O, st);
     if (rc != MOTY_EUNSUP) return rc;
   }
-  if (gs == 32 && S > 4) {
+  if (gs == 32 && S > XF_GEMV_MAX_S) {
     const int rc = launch_gemm_i4g_xf(x, q4, scale, nullptr, nullptr, y, S, I, O, st);
     if (rc != MOTY_EUNSUP) return rc;
   }
@@ -631,11 +631,16 @@ int moty_hip_dense_ffn_i4g_dev(float* out, const float* x, int S, const uint8_t*
     if ((rc = launch_gemv_i4g(x, gate, gs, up, us, h, 1, D, I, st))) return rc;
     return launch_gemv_i4g(h, down, ds, nullptr, nullptr, out, 1, I, D, st);
   }
-  if (!idot4 && S == 1 && D <= 16384 && I <= 16384 &&
+  if (!idot4 && S <= XF_GEMV_MAX_S && D <= 16384 && I <= 16384 &&
       !(((uintptr_t)x | (uintptr_t)gate | (uintptr_t)up | (uintptr_t)down | (uintptr_t)h) & 15)) {
-    // exact f32: gate + up + SiLU in one pass, then down
-    if ((rc = launch_gemv_i4g_xf(x, gate, gs, up, us, h, D, I, st))) return rc;
-    return launch_gemv_i4g_xf(h, down, ds, nullptr, nullptr, out, I, D, st);
+    // exact f32, per token: gate + up + SiLU in one pass, then down (the
+    // shapes fit, so no launch is refused after the first)
+    for (int s = 0; s < S; s++) {
+      if ((rc = launch_gemv_i4g_xf(x + (int64_t)s * D, gate, gs, up, us, h + (int64_t)s * I, D, I, st))) return rc;
+      if ((rc = launch_gemv_i4g_xf(h + (int64_t)s * I, down, ds, nullptr, nullptr, out + (int64_t)s * D, I, D, st)))
+        return rc;
+    }
+    return MOTY_OK;
   }
   // one matmul_i4_grouped_s each, the path chosen per matrix as the
   // reference does (IDOT4 needs the row length a multiple of 64, <= 16384)
@@ -645,8 +650,8 @@ int moty_hip_dense_ffn_i4g_dev(float* out, const float* x, int S, const uint8_t*
       int r = launch_qrow_i8(a, (int8_t*)xq, sx, nullptr, S, K, K, K, st);
       return r ? r : launch_gemm_i4g((const int8_t*)xq, sx, w, ws, o, S, K, N, st);
     }
-    if (S > 4 && launch_gemm_i4g_xf(a, w, ws, nullptr, nullptr, o, S, K, N, st) == MOTY_OK) return MOTY_OK;
-    if (S <= 4) {
+    if (S > XF_GEMV_MAX_S && launch_gemm_i4g_xf(a, w, ws, nullptr, nullptr, o, S, K, N, st) == MOTY_OK) return MOTY_OK;
+    if (S <= XF_GEMV_MAX_S) {
       // exact f32, a few tokens: the one-token GEMV per token (it refuses
       // what it cannot take before launching anything)
       int r = MOTY_OK;
@@ -656,7 +661,8 @@ int moty_hip_dense_ffn_i4g_dev(float* out, const float* x, int S, const uint8_t*
     }
     return launch_i4g_f32(a, w, ws, o, S, K, N, st);
   };
-  if (!idot4 && S > 4 && (D % 64) == 0 && !(((uintptr_t)x) & 15) && !(((uintptr_t)gate | (uintptr_t)up) & 7)) {
+  if (!idot4 && S > XF_GEMV_MAX_S && (D % 64) == 0 && !(((uintptr_t)x) & 15) &&
+      !(((uintptr_t)gate | (uintptr_t)up) & 7)) {
     // exact f32, many tokens: gate + up + SiLU in one tiled pass, then down
     if ((rc = launch_gemm_i4g_xf(x, gate, gs, up, us, h, S, D, I, st))) return rc;
     return mm(h, down, ds, out, I, D);

@@ -59,6 +59,10 @@ int launch_gemv_i4g(const float* x, const uint8_t* q4, const float* scl, const u
 int launch_gemm_i4g_xf(const float* x, const uint8_t* q4, const float* scl, const uint8_t* q4b, const float* sclb,
                        float* y, int M, int I, int O, hipStream_t st);
 // the exact-f32 path (IDOT4 unset), one token; q4b/sclb non-null: PAIR
+// Exact-f32 grouped int4: token counts up to this run the one-token GEMV per
+// token rather than the 64-token tiled GEMM (12288 x 4096: 10.3 us per token
+// against 278 us for any tile of up to 64 tokens; they meet near 27).
+constexpr int XF_GEMV_MAX_S = 24;
 int launch_gemv_i4g_xf(const float* x, const uint8_t* q4, const float* scl, const uint8_t* q4b, const float* sclb,
                        float* y, int I, int O, hipStream_t st);
 int launch_gemm_i4g(const int8_t* xq, const float* sx, const uint8_t* q4, const float* scl, float* y, int M, int I,

@@ -201,9 +201,10 @@ def test_gate_up_silu_i4g(ops, D, I):
                                    (1, 12288, 100), (1, 8192, 77), (1, 96, 40), (1, 2080, 300), (1, 16384, 20),
                                    (1, 14336, 300), (2, 16384, 64), (1, 16416, 10),
                                    (1, 64, 1000),
-                                   # 2..4 tokens: the GEMV per token; more: the tiled GEMM (64 x 64
+                                   # 2..24 tokens: the GEMV per token; more: the tiled GEMM (64 x 64
                                    # tiles, ragged in tokens and rows; I % 64 != 0 falls back)
-                                   (4, 2048, 100), (65, 4096, 130), (256, 1088, 70), (7, 128, 33), (5, 96, 40)])
+                                   (4, 2048, 100), (65, 4096, 130), (256, 1088, 70), (7, 128, 33),
+                                   (24, 1024, 96), (25, 1024, 96), (40, 128, 33), (5, 96, 40)])
 def test_i4g_f32(ops, S, I, O):
     say("i4g f32", S, I, O)
     w = randn(O + I, (O, I), 0.02)
