@@ -408,14 +408,15 @@ int moty_hip_matmul_i4_grouped_s_dev(float* y, const float* x, const uint8_t* q4
     if (rc) return rc;
     return launch_gemm_i4g(xq, sx, q4, scale, y, S, I, O, st);
   }
-  if (gs == 32 && S <= XF_GEMV_MAX_S) {
+  const bool per_token = S <= 4 || xf_gemv_per_token(S, I, O);
+  if (gs == 32 && per_token) {
     // a few tokens: the one-token GEMV per token
     int rc = MOTY_OK;
     for (int s = 0; s < S && rc == MOTY_OK; s++)
       rc = launch_gemv_i4g_xf(x + (int64_t)s * I, q4, scale, nullptr, nullptr, y + (int64_t)s * O, I, O, st);
     if (rc != MOTY_EUNSUP) return rc;
   }
-  if (gs == 32 && S > XF_GEMV_MAX_S) {
+  if (gs == 32 && S > 4) {
     const int rc = launch_gemm_i4g_xf(x, q4, scale, nullptr, nullptr, y, S, I, O, st);
     if (rc != MOTY_EUNSUP) return rc;
   }
@@ -631,7 +632,8 @@ int moty_hip_dense_ffn_i4g_dev(float* out, const float* x, int S, const uint8_t*
     if ((rc = launch_gemv_i4g(x, gate, gs, up, us, h, 1, D, I, st))) return rc;
     return launch_gemv_i4g(h, down, ds, nullptr, nullptr, out, 1, I, D, st);
   }
-  if (!idot4 && S <= XF_GEMV_MAX_S && D <= 16384 && I <= 16384 &&
+  const bool xf_tok = S <= 4 || (xf_gemv_per_token(S, D, 2 * I) && xf_gemv_per_token(S, I, D));
+  if (!idot4 && xf_tok && D <= 16384 && I <= 16384 &&
       !(((uintptr_t)x | (uintptr_t)gate | (uintptr_t)up | (uintptr_t)down | (uintptr_t)h) & 15)) {
     // exact f32, per token: gate + up + SiLU in one pass, then down (the
     // shapes fit, so no launch is refused after the first)
@@ -650,8 +652,9 @@ int moty_hip_dense_ffn_i4g_dev(float* out, const float* x, int S, const uint8_t*
       int r = launch_qrow_i8(a, (int8_t*)xq, sx, nullptr, S, K, K, K, st);
       return r ? r : launch_gemm_i4g((const int8_t*)xq, sx, w, ws, o, S, K, N, st);
     }
-    if (S > XF_GEMV_MAX_S && launch_gemm_i4g_xf(a, w, ws, nullptr, nullptr, o, S, K, N, st) == MOTY_OK) return MOTY_OK;
-    if (S <= XF_GEMV_MAX_S) {
+    const bool tok = S <= 4 || xf_gemv_per_token(S, K, N);
+    if (!tok && launch_gemm_i4g_xf(a, w, ws, nullptr, nullptr, o, S, K, N, st) == MOTY_OK) return MOTY_OK;
+    if (tok) {
       // exact f32, a few tokens: the one-token GEMV per token (it refuses
       // what it cannot take before launching anything)
       int r = MOTY_OK;
@@ -661,7 +664,7 @@ int moty_hip_dense_ffn_i4g_dev(float* out, const float* x, int S, const uint8_t*
     }
     return launch_i4g_f32(a, w, ws, o, S, K, N, st);
   };
-  if (!idot4 && S > XF_GEMV_MAX_S && (D % 64) == 0 && !(((uintptr_t)x) & 15) &&
+  if (!idot4 && !xf_tok && S > 4 && (D % 64) == 0 && !(((uintptr_t)x) & 15) &&
       !(((uintptr_t)gate | (uintptr_t)up) & 7)) {
     // exact f32, many tokens: gate + up + SiLU in one tiled pass, then down
     if ((rc = launch_gemm_i4g_xf(x, gate, gs, up, us, h, S, D, I, st))) return rc;

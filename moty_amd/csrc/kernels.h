@@ -59,10 +59,16 @@ int launch_gemv_i4g(const float* x, const uint8_t* q4, const float* scl, const u
 int launch_gemm_i4g_xf(const float* x, const uint8_t* q4, const float* scl, const uint8_t* q4b, const float* sclb,
                        float* y, int M, int I, int O, hipStream_t st);
 // the exact-f32 path (IDOT4 unset), one token; q4b/sclb non-null: PAIR
-// Exact-f32 grouped int4: token counts up to this run the one-token GEMV per
-// token rather than the 64-token tiled GEMM (12288 x 4096: 10.3 us per token
-// against 278 us for any tile of up to 64 tokens; they meet near 27).
-constexpr int XF_GEMV_MAX_S = 24;
+// Exact-f32 grouped int4, S tokens through an O x I matrix: the one-token
+// GEMV once per token, or the 64-token tiled GEMM?  The tiled GEMM's time
+// follows its K loop, not the token or row count (about 66 ns per element
+// of I: 69 us at I = 1024, 270-280 us at 4096 for 256 to 12288 rows); the
+// GEMV's is about 4 us plus the matrix bytes at 5 TB/s per token (measured
+// on MI355X: 4.2 us at 1024 x 1024, 10.3 at 12288 x 4096).
+inline bool xf_gemv_per_token(int S, int I, int O) {
+  const double gemv_us = 4.0 + ((double)O * I * 0.625) / 5.0e6, gemm_us = 0.066 * I;
+  return S <= 64 && S * gemv_us < gemm_us;
+}
 int launch_gemv_i4g_xf(const float* x, const uint8_t* q4, const float* scl, const uint8_t* q4b, const float* sclb,
                        float* y, int I, int O, hipStream_t st);
 int launch_gemm_i4g(const int8_t* xq, const float* sx, const uint8_t* q4, const float* scl, float* y, int M, int I,
