@@ -641,9 +641,9 @@ class CpuRef:
         self.kind = "reference" if self.r is not None else "port"
         self.cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
 
-    def out(self, value, unit, sample, runs, cores=None):
+    def out(self, value, unit, sample, runs, cores=None, warm=3):
         return {"value": value, "unit": unit, "cores": cores or self.cores, "kind": self.kind,
-                "sample": "%s; median of %d runs after 3 warm-ups" % (sample, runs)}
+                "sample": "%s; median of %d runs after %d warm-up%s" % (sample, runs, warm, "" if warm == 1 else "s")}
 
     def q_s(self, y, x, q, s):
         S, I = x.shape
@@ -698,6 +698,9 @@ def cpu_c1(cr, c1, budget):
     return cr.out(round(c1["algo_bytes"] / t / 1e9, 2), "GB/s", "C1 decode FFN (3 matmul_q_s + silu_mul)", n)
 
 
+MOE_WARM = 1  # warm-up runs of a CPU MoE layer (each is a whole layer)
+
+
 def cpu_moe(cr, r, T_sample, order, norm, budget, nmin=20, skew=None, cap=0):
     """r: a bench_moe result (its first weight copy and inputs); skew: hot
     expert ids whose logits the inputs lift by +2.0 (the reference's batch
@@ -712,7 +715,7 @@ def cpu_moe(cr, r, T_sample, order, norm, budget, nmin=20, skew=None, cap=0):
     ws = [t.cpu().numpy() for t in lay.keep[1:7]]
     out = np.empty((T_sample, lay.D), np.float32)
     t, n = cpu_med(lambda: cr.moe(out, xs, Wr, ws, lay.E, lay.K, lay.I, lay.D, order, norm, cap), budget,
-                   nmin=nmin, warm=1)
+                   nmin=nmin, warm=MOE_WARM)
     return T_sample / t, n
 
 
@@ -843,12 +846,12 @@ def cpu_baseline(c1, c4, extra, budget):
     cr = CpuRef()
     out = cpu_c1(cr, c1, min(3.0, budget))
     if c4 is not None:
-        tpo, n1 = cpu_moe(cr, c4, 64, "olmoe", 0, budget, nmin=3)
+        tpo, n1 = cpu_moe(cr, c4, 256, "olmoe", 0, budget, nmin=3)
         tpb, n2 = cpu_moe(cr, c4, 256, "batch", 1, budget)
         out["moe"] = cr.out(round(tpb, 1), "tokens/s", "C4 OLMoE layer through moe_batch_core (nn/moe.c:159-205), "
-                            "all 256 tokens", n2)
+                            "all 256 tokens", n2, warm=MOE_WARM)
         out["moe"]["olmoe_per_token"] = cr.out(round(tpo, 1), "tokens/s", "the olmoe engine's per-token moe() "
-                                               "(engines/olmoe.c:219-244) on the first 64 of the 256 tokens", n1)
+                                               "(engines/olmoe.c:219-244), all 256 tokens", n1, warm=MOE_WARM)
     for r in extra:
         w = r.get("workload", "")
         try:
@@ -866,17 +869,19 @@ def cpu_baseline(c1, c4, extra, budget):
                 r["cpu_baseline"] = cpu_moe_d1(cr, r, budget)
             elif w.startswith("C5"):
                 sk = "skewed" in w
-                tp, n = cpu_moe(cr, r, 134, "batch", 1, budget, skew=np.arange(0, 128, 16) if sk else None)
-                r["cpu_baseline"] = cr.out(round(tp, 1), "tokens/s", "C5 layer through moe_batch_core on the first "
-                                           "134 of the 1072 tokens (1/8 of the batch)%s" % (
+                tp, n = cpu_moe(cr, r, 1072, "batch", 1, budget, nmin=3,
+                                skew=np.arange(0, 128, 16) if sk else None)
+                r["cpu_baseline"] = cr.out(round(tp, 1), "tokens/s", "C5 layer through moe_batch_core, all 1072 "
+                                           "tokens of the batch%s" % (
                                                "; skew as +2.0 on the hot experts' logits through x and the router"
-                                               if sk else ""), n)
+                                               if sk else ""), n, warm=MOE_WARM)
             elif w.startswith("C4 MoE layer shape through the device expert cache") and c4 is not None:
                 res = {}
                 for cap in (64, 32):
                     tp, n = cpu_moe(cr, c4, 256, "batch", 1, budget / 2, cap=cap, nmin=5)
                     res["cap%d" % cap] = cr.out(round(tp, 1), "tokens/s", "C4 batch layer over the reference's "
-                                                "ExpertCache (runtime/moecache.c) with %d slots, all 256 tokens" % cap, n)
+                                                "ExpertCache (runtime/moecache.c) with %d slots, all 256 tokens" % cap, n,
+                                                warm=MOE_WARM)
                 r["cpu_baseline"] = res
         except Exception as e:  # the baseline is reported, never required
             log("cpu baseline for %s failed: %s" % (w[:20], e))
