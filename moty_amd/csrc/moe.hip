@@ -755,27 +755,29 @@ __device__ __forceinline__ int4 d1_ldnt16(const int8_t* p) {
 // Router logits of one token (nn/matmul.c:15-27 -> hw/hw_avx512.h:231-243):
 // a half-wave per expert, lane c carrying FMA chain c (elements c, c+32, ...,
 // s0 for c < 16, s1 for c >= 16), then s0 + s1 and the _mm512_reduce_add_ps
-// tree; plus the logit bias.  One wave per workgroup, so the E/2 waves
-// spread over as many CUs; x and the wave's two router rows are staged in
-// LDS by 16-byte loads (a quarter of the load instructions of 4-byte loads
-// per chain element: decode MoE 21.4 -> 21.2 us at the C4 shape) and lane c
-// reads its chain's elements back.  NPL >= D/32.
-template <int NPL>
-__global__ __launch_bounds__(MOTY_WAVE) void k_router_t1v(const float* __restrict__ x, const float* __restrict__ Wr,
+// tree; plus the logit bias.  A workgroup per two experts (E/2 of them,
+// spread over as many CUs): its NWV waves stage x and the two router rows
+// in LDS by 16-byte loads (a quarter of the load instructions of 4-byte
+// loads per chain element: decode MoE 21.4 -> 21.2 us at the C4 shape; 8
+// waves sharing them instead of one: 21.4 -> 20.6 us), then the first wave
+// runs the chains, lane c reading its chain's elements back.  NPL >= D/32.
+template <int NPL, int NWV>
+__global__ __launch_bounds__(NWV * MOTY_WAVE) void k_router_t1v(const float* __restrict__ x, const float* __restrict__ Wr,
                                                           const float* __restrict__ bias, int D, int E,
                                                           float* __restrict__ logits) {
   __shared__ __align__(16) float xs[32 * NPL];
   __shared__ __align__(16) float ws[2][32 * NPL];
-  const int lane = threadIdx.x, c = lane & 31, hf = lane >> 5;
+  const int lane = threadIdx.x % MOTY_WAVE, c = lane & 31, hf = lane >> 5;
   const int e = blockIdx.x * 2 + hf;
   const int e0 = blockIdx.x * 2 < E ? blockIdx.x * 2 : E - 1, e1 = e0 + 1 < E ? e0 + 1 : E - 1;
-  for (int i = lane * 4; i < D; i += MOTY_WAVE * 4) {
+  for (int i = threadIdx.x * 4; i < D; i += NWV * MOTY_WAVE * 4) {
     *(float4*)(xs + i) = *(const float4*)(x + i);
     *(float4*)(ws[0] + i) = *(const float4*)(Wr + (int64_t)e0 * D + i);
     *(float4*)(ws[1] + i) = *(const float4*)(Wr + (int64_t)e1 * D + i);
   }
   const float bv = bias ? bias[hf ? e1 : e0] : 0.f;
   __syncthreads();
+  if (threadIdx.x >= MOTY_WAVE) return;  // the other waves only helped load
   const float* wr = ws[hf];
   float acc = 0.f;
 #pragma unroll
@@ -1158,7 +1160,7 @@ static int launch_moe_d1(const MoeArgs& a, void* scratch, hipStream_t st) {
   const int D = a.D, I = a.I, K = a.K, E = a.E;
 #define RT(N)                                                                                                \
   case N:                                                                                                    \
-    hipLaunchKernelGGL((k_router_t1v<N>), dim3((E + 1) / 2), dim3(MOTY_WAVE), 0, st, a.x, a.Wr, a.bias, D, E,    \
+    hipLaunchKernelGGL((k_router_t1v<N, 8>), dim3((E + 1) / 2), dim3(8 * MOTY_WAVE), 0, st, a.x, a.Wr, a.bias, D, E,    \
                        m.logits);                                                                            \
     break;
   switch ((D / 32 + 15) / 16 * 16) {
