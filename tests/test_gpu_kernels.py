@@ -116,6 +116,22 @@ def test_quantize_rows(ops, O, I, bits):
     assert same_bits(to_np(q), q2) and same_bits(to_np(s), s2)
 
 
+def test_weight_packers_unaligned(ops):
+    # weights that are only 4-byte aligned take the element-wise kernels: same bits
+    O, I = 6, 256
+    say("packers unaligned")
+    w = randn(O + 5 * I, (O, I), 0.02)
+    buf = torch.zeros(O * I + 1, dtype=torch.float32, device="cuda")
+    wv = buf[1:].view(O, I)
+    wv.copy_(to_dev(w))
+    q, s = ops.quantize_rows(wv)
+    q2, s2 = o_quantize_rows(w)
+    assert same_bits(to_np(q), q2) and same_bits(to_np(s), s2)
+    q4, s4 = ops.pack_int4_grouped(wv, 32)
+    q42, s42 = o_pack_int4_grouped(w, 32)
+    assert same_bits(to_np(q4), q42) and same_bits(to_np(s4), s42)
+
+
 # gs = 32 with I % 32 == 0: one workgroup per 256 consecutive groups staged
 # through LDS (full and ragged last workgroup); other shapes: one thread per group
 @pytest.mark.parametrize("O,I,gs", [(64, 4096, 32), (5, 31, 16), (8, 100, 32), (300, 1024, 32), (3, 96, 32),
